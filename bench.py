@@ -1,0 +1,233 @@
+"""Benchmark of the iPC training step on one MI355X.
+
+Workload (the headline metric's configuration): the paper efficiency profile
+at depth 6, dims (10, 64 x 6, 784), batch 128, tanh, alpha=1e-4, gamma=0.5,
+fp32 master states/weights with fp16 GEMM operands and fp32 accumulation,
+T=4 steps captured in one hipGraph.  A "step" is one iPC step (prediction
+errors, inference updates, weight updates) over the batch; ``value`` is
+batch * steps / elapsed with inputs resident in HBM.
+
+The same run also reports
+* each phase kernel's average duration (HIP events around a graph of
+  back-to-back launches of that kernel on its stream) and the roofline of the
+  dominant one;
+* the wide MFMA-bound configuration (1000, 4096 x 4, 4096), batch 1024, bf16
+  operands: ms/step and achieved TFLOP/s against the bf16 dense MFMA peak;
+* the CPU baseline: the oracle's fp32 step on this host's cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-wide] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "iPC train samples/sec (L=6,h=64,B=128); fused-GEMM TFLOP/s vs MFMA peak"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0  # dense, no sparsity
+FP16_PEAK_TFLOPS = 2500.0
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def phase_bytes_flops(dims, B, s=4):
+    """Algorithmic HBM bytes and GEMM flops of each phase launch (P, I, W)."""
+    L = len(dims) - 1
+    pb = sum(s * (dims[l] * dims[l + 1] + dims[l + 1] * B + 2 * dims[l] * B) for l in range(L))
+    ib = sum(s * (dims[l - 1] * dims[l] + dims[l - 1] * B + 3 * dims[l] * B) for l in range(1, L))
+    wb = sum(s * (2 * dims[l] * dims[l + 1] + dims[l] * B + dims[l + 1] * B) for l in range(L))
+    S = sum(dims[l] * dims[l + 1] for l in range(L))
+    S_I = S - dims[L - 1] * dims[L]
+    return {"pred": (pb, 2 * B * S), "infer": (ib, 2 * B * S_I), "weight": (wb, 2 * B * S)}
+
+
+def make_model(dims, B, act, dtype, seed, input_dist="uniform"):
+    import torch
+
+    from lich_amd.trainer import HipIPC, IPCConfig, init_weights_cpu
+
+    w0 = init_weights_cpu(dims, seed=seed, init="xavier_uniform")
+    g = torch.Generator().manual_seed(seed + 7919)
+    x_in = torch.rand((dims[-1], B), generator=g) if input_dist == "uniform" else torch.randn((dims[-1], B), generator=g)
+    labels = torch.randint(0, dims[0], (B,), generator=g)
+    y = torch.nn.functional.one_hot(labels, dims[0]).float().T.contiguous()
+    dev = torch.device("cuda", 0)
+    model = HipIPC(IPCConfig(dims=tuple(dims), activation=act, dtype=dtype, alpha=1e-4, gamma=0.5),
+                   device=dev, weights=w0)
+    return model, x_in.to(dev), y.to(dev)
+
+
+def time_phases(model, reps=50, replays=5):
+    """Average duration of one launch of each phase kernel, from HIP events
+    recorded on the stream the kernels run on, around graph replays of `reps`
+    back-to-back launches."""
+    import torch
+
+    from lich_amd import _native as nat
+
+    out = {}
+    for phase, name in ((0, "pred"), (1, "infer"), (2, "weight")):
+        graph = torch.cuda.CUDAGraph()
+        nat.check(nat.lib().ipc_plan_phase(model._plan, phase, 2, nat.current_stream_handle()))  # warm
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph):
+            nat.check(nat.lib().ipc_plan_phase(model._plan, phase, reps, nat.current_stream_handle()))
+        graph.replay()
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(replays):
+            graph.replay()
+        end.record(stream)
+        end.synchronize()
+        out[name] = start.elapsed_time(end) * 1e3 / (reps * replays)  # microseconds per launch
+        del graph
+    return out
+
+
+def run_steady(model, x, y, T, warmup_steps, steps):
+    import torch
+
+    assert model.prepare_steady_state(x, y, steps=T, use_graph=True)
+    for _ in range(max(1, warmup_steps // T)):
+        model._steady_state_runner.replay()
+    torch.cuda.synchronize()
+    replays = steps // T
+    t0 = time.perf_counter()
+    for _ in range(replays):
+        model._steady_state_runner.replay()
+    torch.cuda.synchronize()
+    return time.perf_counter() - t0, replays * T
+
+
+def cpu_baseline(dims, B, act, threads, warmup=20, steps=200, repeats=5):
+    """The oracle's fp32 step (reference.py:42-59 semantics) on the host cores."""
+    import torch
+
+    from oracle import ipc_oracle as O
+
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        w = O.init_weights(dims, seed=0, init="xavier_uniform")
+        x_in, _l, y = O.make_batch(dims, B, seed=0)
+        x = O.forward_init(x_in, y, w, act)
+        with torch.no_grad():
+            for _ in range(warmup):
+                x, w, _e, _m = O.ipc_step(x, w, act=act, alpha=1e-4, gamma=0.5)
+            per_step = []
+            for _ in range(repeats):
+                t0 = time.perf_counter()
+                for _ in range(steps):
+                    x, w, _e, _m = O.ipc_step(x, w, act=act, alpha=1e-4, gamma=0.5)
+                per_step.append((time.perf_counter() - t0) / steps)
+    finally:
+        torch.set_num_threads(prev)
+    med = statistics.median(per_step)
+    return B / med, med
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20000)
+    ap.add_argument("--warmup", type=int, default=400)
+    ap.add_argument("--no-wide", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(this build has no multi-GPU path)", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from lich_amd import _native as nat
+
+    T = 4
+    dims = (10,) + (64,) * 6 + (784,)
+    B = 128
+    steps = max(T, (args.steps // T) * T)
+    warmup = max(T, args.warmup)
+    log(f"device {torch.cuda.get_device_name(0)} arch {nat.device_arch(0)}")
+
+    model, x, y = make_model(dims, B, "tanh", torch.float16, seed=0)
+    elapsed, done = run_steady(model, x, y, T, warmup, steps)
+    ms_per_step = elapsed * 1e3 / done
+    value = B * done / elapsed
+    log(f"headline: {ms_per_step * 1e3:.2f} us/step, {value:,.0f} samples/s, {model.launches_per_step()} launches/step")
+
+    # per-phase kernel durations on a fresh model (the timing loops disturb state)
+    pmodel, px, py = make_model(dims, B, "tanh", torch.float16, seed=1)
+    pmodel.initialize_batch(px, py)
+    phase_us = time_phases(pmodel)
+    bf = phase_bytes_flops(dims, B)
+    dom = max(phase_us, key=phase_us.get)
+    dom_bytes, dom_flops = bf[dom]
+    achieved = dom_bytes / (phase_us[dom] * 1e-6) / 1e9
+    phases = {k: {"us": round(v, 3), "GB/s": round(bf[k][0] / (v * 1e-6) / 1e9, 2),
+                  "TFLOP/s": round(bf[k][1] / (v * 1e-6) / 1e12, 4)} for k, v in phase_us.items()}
+    log(f"phases: {phases}")
+    roofline = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None, "kernel": f"{dom} phase",
+                "algorithmic_bytes_per_launch": dom_bytes, "avg_launch_us": round(phase_us[dom], 3)}
+    del pmodel
+
+    wide = None
+    if not args.no_wide:
+        wdims = (1000,) + (4096,) * 4 + (4096,)
+        WB = 1024
+        wmodel, wx, wy = make_model(wdims, WB, "tanh", torch.bfloat16, seed=0, input_dist="normal")
+        w_elapsed, w_done = run_steady(wmodel, wx, wy, T, 2 * T, 5 * T)
+        w_ms = w_elapsed * 1e3 / w_done
+        flops_step = sum(v[1] for v in phase_bytes_flops(wdims, WB).values())
+        tflops = flops_step / (w_ms * 1e-3) / 1e12
+        wphase = time_phases(wmodel, reps=5, replays=3)
+        wbf = phase_bytes_flops(wdims, WB)
+        wide = {"workload": "wide iPC MLP dims (1000,4096x4,4096), B=1024, tanh, bf16 operands, fp32 master, T=4",
+                "ms_per_step": round(w_ms, 4), "samples_per_s": round(WB / (w_ms * 1e-3), 1),
+                "gflop_per_step": round(flops_step / 1e9, 3), "tflops": round(tflops, 2),
+                "frac_of_bf16_peak": round(tflops / BF16_PEAK_TFLOPS, 4),
+                "phases": {k: {"us": round(v, 2), "TFLOP/s": round(wbf[k][1] / (v * 1e-6) / 1e12, 2)}
+                           for k, v in wphase.items()}}
+        log(f"wide: {wide}")
+        del wmodel
+
+    cpu = None
+    if not args.no_cpu:
+        threads = torch.get_num_threads()
+        cpu_val, cpu_step = cpu_baseline(dims, B, "tanh", threads)
+        cpu1_val, _ = cpu_baseline(dims, B, "tanh", 1, warmup=10, steps=100, repeats=3)
+        cpu = {"value": round(cpu_val, 1), "unit": "samples/s", "cores": threads, "kind": "port",
+               "sample": f"oracle fp32 step, same dims/B/tanh, 20 warm-up + 5x200 timed steps, median "
+                         f"({cpu_step * 1e3:.3f} ms/step); 1 thread: {cpu1_val:.1f} samples/s",
+               "gpu_over_cpu": round(value / cpu_val, 2)}
+        log(f"cpu: {cpu}")
+
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "samples/s", "n_gpus": 1, "steps": done,
+        "warmup": warmup, "ms_per_step": round(ms_per_step, 6), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f16", "data": "synthetic (seeded U[0,1] inputs, uniform labels, Xavier W)",
+        "config": {"workload": "paper profile depth 6: dims (10,64x6,784), B=128, tanh, alpha=1e-4, gamma=0.5, "
+                               "T=4 steps per hipGraph replay, fp32 master x/eps/W, fp16 operands, fp32 accumulate",
+                   "global_batch": B, "seq_len": None, "parallelism": "single GPU",
+                   "launches_per_step": model.launches_per_step(), "phases": phases},
+        "roofline": roofline, "cpu_baseline": cpu, "wide": wide,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

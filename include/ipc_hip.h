@@ -1,0 +1,184 @@
+/*
+ * ipc_hip.h - C ABI of the MI355X (gfx950) iPC training-step library.
+ *
+ * The library replaces the reference's TileLang kernel builders
+ * (src/ipc_tilelang/tilelang_kernels.py, src/ipc_tilelang/layer_batching.py,
+ * src/ipc_tilelang/weight_update_specialization.py) and the per-layer launch
+ * loop of TileLangIPC.step_initialized (src/ipc_tilelang/trainer.py:601-679).
+ *
+ * Conventions (reference README.md:41-50, reference.py:35-59):
+ *   x[0] = fixed one-hot target, x[L] = fixed input, W[l] is [d_l, d_{l+1}]
+ *   and maps f(x[l+1]) -> x[l]; every tensor is contiguous, row-major and
+ *   feature-major ([features, batch]).  Grouped ("batched", grid.z) calls take
+ *   contiguous [groups, rows, cols] tensors.
+ *
+ * Ownership: the caller owns every buffer.  Kernels mutate their outputs in
+ * place, allocate nothing and never synchronise the stream.  Every call is
+ * enqueued on the hipStream_t passed as `stream` (NULL = the null stream), so
+ * calls can be captured into a hipGraph.
+ *
+ * Errors: every entry point returns IPC_OK (0) or a negative IPC_ERR_* code
+ * and never throws; ipc_last_error() returns the calling thread's message.
+ * Argument validation happens on the host before any HIP call.
+ */
+#ifndef IPC_HIP_H
+#define IPC_HIP_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define IPC_ABI_VERSION 1
+
+/* status codes */
+#define IPC_OK 0
+#define IPC_ERR_NULL (-1)     /* a required pointer is NULL                  */
+#define IPC_ERR_SHAPE (-2)    /* a dimension is < 1 or too large              */
+#define IPC_ERR_DTYPE (-3)    /* unknown dtype or unsupported combination     */
+#define IPC_ERR_ACT (-4)      /* unknown activation                           */
+#define IPC_ERR_ALIGN (-5)    /* pointer not aligned to its element size      */
+#define IPC_ERR_DEVICE (-6)   /* no device, or the device is not gfx950       */
+#define IPC_ERR_LAUNCH (-7)   /* the HIP launch failed                        */
+#define IPC_ERR_CONFIG (-8)   /* unknown tile config or plan option           */
+#define IPC_ERR_STATE (-9)    /* plan used before its buffers were bound      */
+
+/* element types (storage and GEMM operand) */
+#define IPC_DT_F32 0
+#define IPC_DT_F16 1
+#define IPC_DT_BF16 2
+
+/* activations: activations.py:9-29 and tilelang_kernels.py:61-96;
+ * IPC_ACT_IDENTITY is the linear case of weight_update_specialization.py:96-102 */
+#define IPC_ACT_IDENTITY 0
+#define IPC_ACT_RELU 1
+#define IPC_ACT_TANH 2
+#define IPC_ACT_SIGMOID 3
+#define IPC_ACT_SILU 4
+#define IPC_ACT_GELU 5
+
+/* tile configurations of the MFMA GEMM family; IPC_TILE_AUTO picks by shape */
+#define IPC_TILE_AUTO (-1)
+#define IPC_TILE_32x32 0
+#define IPC_TILE_64x64 1
+#define IPC_TILE_128x128 2
+#define IPC_TILE_COUNT 3
+
+/* weight-update backends of a plan */
+#define IPC_WMODE_GEMM 0
+#define IPC_WMODE_OUTER 1
+#define IPC_WMODE_AUTO 2
+
+/* Library version of this header's ABI. */
+int ipc_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* ipc_last_error(void);
+
+/* Writes the gcnArchName of `device` into buf (NUL-terminated) and returns
+ * IPC_OK if it is a gfx950 part, IPC_ERR_DEVICE otherwise.  Replaces the
+ * SM86 gate of trainer.py:58-63. */
+int ipc_device_check(int device, char* buf, int buflen);
+
+/*
+ * Prediction + error, E[g] = X_lower[g] - W[g] @ f(X_upper[g]).
+ * Replaces build_prediction_error(M,K,B,act,dtype,cfg)(X_upper,W,X_lower,E)
+ * (tilelang_kernels.py:114-177) and, for groups > 1,
+ * build_prediction_error_batched (layer_batching.py:89-150).
+ * X_upper [G,K,B], W [G,M,K], X_lower/E [G,M,B].  f is applied in the operand
+ * loader; out-of-range tail elements are zero after f.  With 16-bit storage
+ * the subtraction is rounded like tilelang_kernels.py:173.
+ * storage: element type of all four tensors; operand: type the GEMM operands
+ * are rounded to (must equal storage when storage is 16-bit); accumulation is
+ * always fp32.
+ */
+int ipc_pred_err(const void* x_upper, const void* w, const void* x_lower, void* e,
+                 int M, int K, int B, int groups,
+                 int storage, int operand, int act, int tile, void* stream);
+
+/*
+ * Forward prediction OUT[g] = W[g] @ f(X_upper[g]).  Used for the hidden-state
+ * forward initialisation (trainer.py:512-515) and predict() (trainer.py:828-833).
+ */
+int ipc_forward(const void* x_upper, const void* w, void* out,
+                int M, int K, int B, int groups,
+                int storage, int operand, int act, int tile, void* stream);
+
+/*
+ * Inference update X[g] += gamma * (-E[g] + f'(X[g]) * W_lower[g]^T @ E_lower[g]),
+ * optionally writing A_out[g] = f(X_new).  Replaces
+ * build_inference_update(M,K,B,act,dtype,cfg,gamma,save)(X,E,W_lower,E_lower[,A_out])
+ * (tilelang_kernels.py:180-265) and build_inference_update_batched
+ * (layer_batching.py:153-248).  X/E/A_out [G,M,B], W_lower [G,K,M] read
+ * transposed without a global transpose, E_lower [G,K,B].  a_out may be NULL.
+ */
+int ipc_infer_update(void* x, const void* e, const void* w_lower, const void* e_lower, void* a_out,
+                     int M, int K, int B, int groups, float gamma,
+                     int storage, int operand, int act, int tile, void* stream);
+
+/*
+ * Weight update W[g] += alpha * E[g] @ A[g]^T with A = f(X_upper) when
+ * recompute != 0, else A = the saved activation passed as x_upper.  Replaces
+ * build_weight_update(M,K,B,act,dtype,cfg,alpha,recompute)(W,E,X_upper_or_A)
+ * (tilelang_kernels.py:268-349) and build_weight_update_batched
+ * (layer_batching.py:251-346).  W [G,M,K], E [G,M,B], X_upper/A [G,K,B].
+ * The epilogue is W = cast(float(W) + alpha*acc) (tilelang_kernels.py:319-320).
+ */
+int ipc_weight_update(void* w, const void* e, const void* x_upper, int M, int K, int B, int groups,
+                      float alpha, int recompute, int storage, int operand, int act, int tile,
+                      void* stream);
+
+/*
+ * Rank-B outer-product weight update for small batches (B <= 32):
+ * W[g] += alpha * sum_b E[g][:,b] f(X_upper[g][:,b])^T, accumulated in fp32.
+ * Replaces SmallBWeightUpdater (weight_update_specialization.py:63-128) with
+ * the +alpha sign of the GEMM path and of reference.py:57 (the reference's
+ * -alpha there is a sign error) and with every activation, not only relu.
+ */
+int ipc_weight_update_outer(void* w, const void* e, const void* x_upper, int M, int K, int B, int groups,
+                            float alpha, int recompute, int storage, int act, void* stream);
+
+/*
+ * Whole-step plan: one call enqueues a complete iPC step (all prediction
+ * errors, then the inference updates l = 1..L-1, then all weight updates),
+ * replacing the Python launch loop of TileLangIPC.step_initialized
+ * (trainer.py:601-679) and, when captured, IPCGraphRunner (cuda_graph.py:6-36).
+ * dims has L+1 entries (dims[0] = classes, dims[L] = input features).
+ */
+typedef struct ipc_plan ipc_plan;
+
+int ipc_plan_create(ipc_plan** out, int L, const int* dims, int B,
+                    int storage, int operand, int act, float alpha, float gamma,
+                    int recompute, int weight_mode);
+
+/* Binds the caller's buffers: x and e hold L+1 pointers ([d_l, B] each; e[L]
+ * is unused and may be NULL), w holds L pointers ([d_l, d_{l+1}]), a holds
+ * L+1 pointers for save-activation mode (recompute == 0) or is NULL. */
+int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w, void* const* a);
+
+/* Enqueues `steps` iPC steps on `stream`. */
+int ipc_plan_step(ipc_plan* plan, int steps, void* stream);
+
+/* Enqueues the forward initialisation of the bound states: a[L] = f(x[L]) in
+ * save mode, hidden x[l] = W[l] f(x[l+1]) for l = L-1..1 (trainer.py:509-515).
+ * x[0] and x[L] are left to the caller. */
+int ipc_plan_forward_init(ipc_plan* plan, void* stream);
+
+/* Enqueues only one phase of the step `reps` times (0 = prediction+error,
+ * 1 = inference update, 2 = weight update), so that each phase's kernel can
+ * be timed on its own.  Mirrors the per-kernel timing of the reference's
+ * harnesses (scripts/autotune.py:200-215). */
+#define IPC_PHASE_PRED 0
+#define IPC_PHASE_INFER 1
+#define IPC_PHASE_WEIGHT 2
+int ipc_plan_phase(ipc_plan* plan, int phase, int reps, void* stream);
+
+/* Kernel launches one ipc_plan_step(steps=1) enqueues. */
+int ipc_plan_launch_count(const ipc_plan* plan);
+
+void ipc_plan_destroy(ipc_plan* plan);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* IPC_HIP_H */

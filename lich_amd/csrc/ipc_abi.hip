@@ -1,0 +1,437 @@
+// ipc_abi.hip - the extern "C" boundary of libipc_hip.so (declared in include/ipc_hip.h).
+//
+// Every entry point validates its arguments on the host before any HIP call
+// (so the error paths are testable without a GPU), converts them to
+// GemmProblem / OuterProblem records and enqueues on the caller's stream.
+// No entry point allocates device memory or synchronises.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../include/ipc_hip.h"
+#include "ipc_launch.h"
+
+using namespace ipc;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int ok() { return IPC_OK; }
+
+const long long kMaxElems = (1LL << 31) - 1;  // per-matrix element count (32-bit tile indices)
+
+int elem_size(int dt) { return dt == IPC_DT_F32 ? 4 : 2; }
+
+int check_dtypes(int storage, int operand) {
+  if (storage < IPC_DT_F32 || storage > IPC_DT_BF16)
+    return fail(IPC_ERR_DTYPE, "unknown storage dtype %d", storage);
+  if (operand < IPC_DT_F32 || operand > IPC_DT_BF16)
+    return fail(IPC_ERR_DTYPE, "unknown operand dtype %d", operand);
+  if (storage != IPC_DT_F32 && operand != storage)
+    return fail(IPC_ERR_DTYPE, "16-bit storage (%d) requires operand dtype == storage (got %d)",
+                storage, operand);
+  return ok();
+}
+
+int check_act(int act) {
+  if (act < IPC_ACT_IDENTITY || act > IPC_ACT_GELU)
+    return fail(IPC_ERR_ACT, "unknown activation %d", act);
+  return ok();
+}
+
+int check_dims(int M, int K, int B, int groups) {
+  if (M < 1 || K < 1 || B < 1 || groups < 1)
+    return fail(IPC_ERR_SHAPE, "dimensions must be >= 1 (M=%d K=%d B=%d groups=%d)", M, K, B, groups);
+  if ((long long)M * K > kMaxElems || (long long)M * B > kMaxElems || (long long)K * B > kMaxElems)
+    return fail(IPC_ERR_SHAPE, "matrix too large (M=%d K=%d B=%d)", M, K, B);
+  return ok();
+}
+
+int check_ptr(const void* p, const char* name, int esize) {
+  if (!p) return fail(IPC_ERR_NULL, "%s is NULL", name);
+  if (reinterpret_cast<uintptr_t>(p) % esize)
+    return fail(IPC_ERR_ALIGN, "%s is not aligned to its %d-byte element", name, esize);
+  return ok();
+}
+
+int check_tile(int tile) {
+  if (tile < IPC_TILE_AUTO || tile >= IPC_TILE_COUNT)
+    return fail(IPC_ERR_CONFIG, "unknown tile config %d", tile);
+  return ok();
+}
+
+#define TRY(x)                  \
+  do {                          \
+    const int _rc = (x);        \
+    if (_rc != IPC_OK) return _rc; \
+  } while (0)
+
+// 4-element vector loads need the contiguous length and the base aligned to 4 elements.
+int vec_ok(const void* p, long long contiguous, int esize) {
+  return (contiguous % 4 == 0) && (reinterpret_cast<uintptr_t>(p) % (4 * esize) == 0);
+}
+
+// Auto tile: the largest tile that still yields at least ~2 workgroups per CU
+// (256 CUs), falling back to smaller tiles for the latency-bound shapes.
+int pick_tile(long long M, long long N, long long groups) {
+  const long long t128 = ((M + 127) / 128) * ((N + 127) / 128) * groups;
+  const long long t64 = ((M + 63) / 64) * ((N + 63) / 64) * groups;
+  if (t128 >= 512) return IPC_TILE_128x128;
+  if (t64 >= 256) return IPC_TILE_64x64;
+  if (M >= 64 && N >= 64 && t64 >= 64) return IPC_TILE_64x64;
+  return IPC_TILE_32x32;
+}
+
+int launch_rc(hipError_t err, const char* what) {
+  if (err != hipSuccess) return fail(IPC_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(err));
+  return ok();
+}
+
+GemmProblem make_pf(int kind, const void* xu, const void* w, const void* xl, void* out, int M, int K,
+                    int B, int groups, int act, int esize) {
+  GemmProblem p{};
+  p.kind = kind;
+  p.M = M; p.N = B; p.K = K; p.groups = groups;
+  p.a = w; p.lda = K; p.a_gs = (long long)M * K;
+  p.b = xu; p.ldb = B; p.b_gs = (long long)K * B;
+  p.out = out; p.ldo = B; p.o_gs = (long long)M * B;
+  p.aux = xl; p.ldx = B; p.x_gs = (long long)M * B;
+  p.out2 = nullptr;
+  p.act_b = act; p.act_epi = act;
+  p.vec_a = vec_ok(w, K, esize);
+  p.vec_b = vec_ok(xu, B, esize);
+  return p;
+}
+
+GemmProblem make_inf(void* x, const void* e, const void* wl, const void* el, void* aout, int M, int K,
+                     int B, int groups, float gamma, int act, int esize) {
+  GemmProblem p{};
+  p.kind = KIND_INFER;
+  p.M = M; p.N = B; p.K = K; p.groups = groups;
+  p.a = wl; p.lda = M; p.a_gs = (long long)K * M;
+  p.b = el; p.ldb = B; p.b_gs = (long long)K * B;
+  p.out = x; p.ldo = B; p.o_gs = (long long)M * B;
+  p.aux = e; p.ldx = B; p.x_gs = (long long)M * B;
+  p.out2 = aout; p.ld2 = B; p.o2_gs = (long long)M * B;
+  p.scal = gamma;
+  p.act_b = IPC_ACT_IDENTITY; p.act_epi = act;
+  p.vec_a = vec_ok(wl, M, esize);
+  p.vec_b = vec_ok(el, B, esize);
+  return p;
+}
+
+GemmProblem make_wgt(void* w, const void* e, const void* xu, int M, int K, int B, int groups,
+                     float alpha, int recompute, int act, int esize) {
+  GemmProblem p{};
+  p.kind = KIND_WEIGHT;
+  p.M = M; p.N = K; p.K = B; p.groups = groups;
+  p.a = e; p.lda = B; p.a_gs = (long long)M * B;
+  p.b = xu; p.ldb = B; p.b_gs = (long long)K * B;
+  p.out = w; p.ldo = K; p.o_gs = (long long)M * K;
+  p.aux = nullptr;
+  p.out2 = nullptr;
+  p.scal = alpha;
+  p.act_b = recompute ? act : IPC_ACT_IDENTITY; p.act_epi = act;
+  p.vec_a = vec_ok(e, B, esize);
+  p.vec_b = vec_ok(xu, B, esize);
+  return p;
+}
+
+OuterProblem make_outer(void* w, const void* e, const void* xu, int M, int K, int B, int groups,
+                        float alpha, int recompute, int act) {
+  OuterProblem p{};
+  p.M = M; p.K = K; p.B = B; p.groups = groups;
+  p.w = w; p.w_gs = (long long)M * K;
+  p.e = e; p.e_gs = (long long)M * B;
+  p.x = xu; p.x_gs = (long long)K * B;
+  p.alpha = alpha;
+  p.act = recompute ? act : IPC_ACT_IDENTITY;
+  return p;
+}
+
+constexpr int kOuterMaxB = 32;
+
+}  // namespace
+
+// =========================================================================== C ABI
+extern "C" {
+
+int ipc_abi_version(void) { return IPC_ABI_VERSION; }
+
+const char* ipc_last_error(void) { return g_last_error.c_str(); }
+
+int ipc_device_check(int device, char* buf, int buflen) {
+  hipDeviceProp_t prop;
+  const hipError_t err = hipGetDeviceProperties(&prop, device);
+  if (err != hipSuccess) return fail(IPC_ERR_DEVICE, "no HIP device %d: %s", device, hipGetErrorString(err));
+  if (buf && buflen > 0) {
+    std::strncpy(buf, prop.gcnArchName, (size_t)buflen - 1);
+    buf[buflen - 1] = '\0';
+  }
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(IPC_ERR_DEVICE, "device %d is %s; this library is built for gfx950 (MI355X) only",
+                device, prop.gcnArchName);
+  return ok();
+}
+
+int ipc_pred_err(const void* x_upper, const void* w, const void* x_lower, void* e, int M, int K, int B,
+                 int groups, int storage, int operand, int act, int tile, void* stream) {
+  TRY(check_dtypes(storage, operand));
+  TRY(check_act(act));
+  TRY(check_dims(M, K, B, groups));
+  TRY(check_tile(tile));
+  const int es = elem_size(storage);
+  TRY(check_ptr(x_upper, "x_upper", es));
+  TRY(check_ptr(w, "w", es));
+  TRY(check_ptr(x_lower, "x_lower", es));
+  TRY(check_ptr(e, "e", es));
+  GemmProblem p = make_pf(KIND_PRED, x_upper, w, x_lower, e, M, K, B, groups, act, es);
+  if (tile == IPC_TILE_AUTO) tile = pick_tile(M, B, groups);
+  return launch_rc(launch_gemm(&p, 1, storage, operand, tile, (hipStream_t)stream), "ipc_pred_err");
+}
+
+int ipc_forward(const void* x_upper, const void* w, void* out, int M, int K, int B, int groups, int storage,
+                int operand, int act, int tile, void* stream) {
+  TRY(check_dtypes(storage, operand));
+  TRY(check_act(act));
+  TRY(check_dims(M, K, B, groups));
+  TRY(check_tile(tile));
+  const int es = elem_size(storage);
+  TRY(check_ptr(x_upper, "x_upper", es));
+  TRY(check_ptr(w, "w", es));
+  TRY(check_ptr(out, "out", es));
+  GemmProblem p = make_pf(KIND_FWD, x_upper, w, nullptr, out, M, K, B, groups, act, es);
+  if (tile == IPC_TILE_AUTO) tile = pick_tile(M, B, groups);
+  return launch_rc(launch_gemm(&p, 1, storage, operand, tile, (hipStream_t)stream), "ipc_forward");
+}
+
+int ipc_infer_update(void* x, const void* e, const void* w_lower, const void* e_lower, void* a_out, int M,
+                     int K, int B, int groups, float gamma, int storage, int operand, int act, int tile,
+                     void* stream) {
+  TRY(check_dtypes(storage, operand));
+  TRY(check_act(act));
+  TRY(check_dims(M, K, B, groups));
+  TRY(check_tile(tile));
+  const int es = elem_size(storage);
+  TRY(check_ptr(x, "x", es));
+  TRY(check_ptr(e, "e", es));
+  TRY(check_ptr(w_lower, "w_lower", es));
+  TRY(check_ptr(e_lower, "e_lower", es));
+  if (a_out) TRY(check_ptr(a_out, "a_out", es));
+  GemmProblem p = make_inf(x, e, w_lower, e_lower, a_out, M, K, B, groups, gamma, act, es);
+  if (tile == IPC_TILE_AUTO) tile = pick_tile(M, B, groups);
+  return launch_rc(launch_gemm(&p, 1, storage, operand, tile, (hipStream_t)stream), "ipc_infer_update");
+}
+
+int ipc_weight_update(void* w, const void* e, const void* x_upper, int M, int K, int B, int groups,
+                      float alpha, int recompute, int storage, int operand, int act, int tile, void* stream) {
+  TRY(check_dtypes(storage, operand));
+  TRY(check_act(act));
+  TRY(check_dims(M, K, B, groups));
+  TRY(check_tile(tile));
+  const int es = elem_size(storage);
+  TRY(check_ptr(w, "w", es));
+  TRY(check_ptr(e, "e", es));
+  TRY(check_ptr(x_upper, "x_upper", es));
+  GemmProblem p = make_wgt(w, e, x_upper, M, K, B, groups, alpha, recompute, act, es);
+  if (tile == IPC_TILE_AUTO) tile = pick_tile(M, K, groups);
+  return launch_rc(launch_gemm(&p, 1, storage, operand, tile, (hipStream_t)stream), "ipc_weight_update");
+}
+
+int ipc_weight_update_outer(void* w, const void* e, const void* x_upper, int M, int K, int B, int groups,
+                            float alpha, int recompute, int storage, int act, void* stream) {
+  TRY(check_dtypes(storage, storage));
+  TRY(check_act(act));
+  TRY(check_dims(M, K, B, groups));
+  if (B > kOuterMaxB) return fail(IPC_ERR_SHAPE, "outer-product update supports B <= %d (got %d)", kOuterMaxB, B);
+  const int es = elem_size(storage);
+  TRY(check_ptr(w, "w", es));
+  TRY(check_ptr(e, "e", es));
+  TRY(check_ptr(x_upper, "x_upper", es));
+  OuterProblem p = make_outer(w, e, x_upper, M, K, B, groups, alpha, recompute, act);
+  return launch_rc(launch_outer(p, storage, (hipStream_t)stream), "ipc_weight_update_outer");
+}
+
+}  // extern "C"
+
+// =========================================================================== plan
+struct ipc_plan {
+  int L = 0, B = 0, storage = 0, operand = 0, act = 0, recompute = 1, wmode = 0;
+  float alpha = 0.f, gamma = 0.f;
+  std::vector<int> dims;
+  bool bound = false;
+  // prepared launches of one step
+  std::vector<GemmProblem> pred, infer, weight;
+  std::vector<OuterProblem> outer;
+  int tile_pred = 0, tile_infer = 0, tile_weight = 0;
+  // forward initialisation launches (l = L-1 .. 1, sequential)
+  std::vector<GemmProblem> fwd;
+  const void* act_src = nullptr;  // x[L]
+  void* act_dst = nullptr;        // a[L] in save mode
+  int launches = 0;
+};
+
+extern "C" {
+
+int ipc_plan_create(ipc_plan** out, int L, const int* dims, int B, int storage, int operand, int act,
+                    float alpha, float gamma, int recompute, int weight_mode) {
+  if (!out) return fail(IPC_ERR_NULL, "out is NULL");
+  *out = nullptr;
+  if (!dims) return fail(IPC_ERR_NULL, "dims is NULL");
+  if (L < 1 || L > 4096) return fail(IPC_ERR_SHAPE, "L must be in [1, 4096] (got %d)", L);
+  TRY(check_dtypes(storage, operand));
+  TRY(check_act(act));
+  if (weight_mode < IPC_WMODE_GEMM || weight_mode > IPC_WMODE_AUTO)
+    return fail(IPC_ERR_CONFIG, "unknown weight mode %d", weight_mode);
+  for (int l = 0; l < L; ++l) TRY(check_dims(dims[l], dims[l + 1], B, 1));
+  if (weight_mode == IPC_WMODE_OUTER && B > kOuterMaxB)
+    return fail(IPC_ERR_SHAPE, "outer weight mode supports B <= %d (got %d)", kOuterMaxB, B);
+  ipc_plan* p = new (std::nothrow) ipc_plan();
+  if (!p) return fail(IPC_ERR_CONFIG, "out of host memory");
+  p->L = L; p->B = B; p->storage = storage; p->operand = operand; p->act = act;
+  p->alpha = alpha; p->gamma = gamma; p->recompute = recompute ? 1 : 0;
+  p->wmode = weight_mode;
+  p->dims.assign(dims, dims + L + 1);
+  *out = p;
+  return ok();
+}
+
+int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w, void* const* a) {
+  if (!plan) return fail(IPC_ERR_NULL, "plan is NULL");
+  if (!x || !e || !w) return fail(IPC_ERR_NULL, "x, e and w pointer arrays are required");
+  if (!plan->recompute && !a) return fail(IPC_ERR_NULL, "save-activation plan needs the a[] array");
+  const int L = plan->L, B = plan->B, es = elem_size(plan->storage);
+  char name[32];
+  for (int l = 0; l <= L; ++l) {
+    snprintf(name, sizeof(name), "x[%d]", l);
+    TRY(check_ptr(x[l], name, es));
+    if (l < L) {
+      snprintf(name, sizeof(name), "e[%d]", l);
+      TRY(check_ptr(e[l], name, es));
+      snprintf(name, sizeof(name), "w[%d]", l);
+      TRY(check_ptr(w[l], name, es));
+    }
+    if (!plan->recompute && l >= 1) {
+      snprintf(name, sizeof(name), "a[%d]", l);
+      TRY(check_ptr(a[l], name, es));
+    }
+  }
+  const std::vector<int>& d = plan->dims;
+  plan->pred.clear(); plan->infer.clear(); plan->weight.clear(); plan->outer.clear(); plan->fwd.clear();
+  // Prediction always applies f to x[l+1] in its loader (trainer.py:617-618);
+  // only the weight update consumes the saved activation.
+  for (int l = 0; l < L; ++l)
+    plan->pred.push_back(make_pf(KIND_PRED, x[l + 1], w[l], x[l], e[l], d[l], d[l + 1], B, 1, plan->act, es));
+  for (int l = 1; l < L; ++l) {
+    plan->infer.push_back(make_inf(x[l], e[l], w[l - 1], e[l - 1], plan->recompute ? nullptr : a[l], d[l],
+                                   d[l - 1], B, 1, plan->gamma, plan->act, es));
+  }
+  for (int l = 0; l < L; ++l) {
+    const bool use_outer = plan->wmode == IPC_WMODE_OUTER || (plan->wmode == IPC_WMODE_AUTO && B <= 16);
+    const void* src = plan->recompute ? x[l + 1] : a[l + 1];
+    if (use_outer)
+      plan->outer.push_back(make_outer(w[l], e[l], src, d[l], d[l + 1], B, 1, plan->alpha, plan->recompute, plan->act));
+    else
+      plan->weight.push_back(make_wgt(w[l], e[l], src, d[l], d[l + 1], B, 1, plan->alpha, plan->recompute, plan->act, es));
+  }
+  plan->act_src = x[L];
+  plan->act_dst = plan->recompute ? nullptr : a[L];
+  for (int l = L - 1; l >= 1; --l)
+    plan->fwd.push_back(make_pf(KIND_FWD, x[l + 1], w[l], nullptr, x[l], d[l], d[l + 1], B, 1, plan->act, es));
+  // One tile configuration per phase, chosen from the phase's total work.
+  long long rows_p = 0, rows_i = 0, rows_w = 0, cols_w = 0;
+  for (auto& q : plan->pred) rows_p += q.M;
+  for (auto& q : plan->infer) rows_i += q.M;
+  for (auto& q : plan->weight) { rows_w += q.M; cols_w = std::max(cols_w, (long long)q.N); }
+  plan->tile_pred = pick_tile(rows_p, B, 1);
+  plan->tile_infer = rows_i ? pick_tile(rows_i, B, 1) : 0;
+  plan->tile_weight = rows_w ? pick_tile(rows_w, cols_w, 1) : 0;
+  plan->launches = 1 + (plan->infer.empty() ? 0 : 1) + (plan->weight.empty() ? 0 : 1) + (int)plan->outer.size();
+  plan->bound = true;
+  return ok();
+}
+
+}  // extern "C"
+
+namespace {
+
+int run_phase(ipc_plan* plan, int phase, hipStream_t s) {
+  switch (phase) {
+    case IPC_PHASE_PRED:
+      return launch_rc(launch_gemm(plan->pred.data(), (int)plan->pred.size(), plan->storage, plan->operand,
+                                   plan->tile_pred, s), "plan prediction phase");
+    case IPC_PHASE_INFER:
+      if (plan->infer.empty()) return ok();
+      return launch_rc(launch_gemm(plan->infer.data(), (int)plan->infer.size(), plan->storage, plan->operand,
+                                   plan->tile_infer, s), "plan inference phase");
+    default:
+      if (!plan->weight.empty())
+        TRY(launch_rc(launch_gemm(plan->weight.data(), (int)plan->weight.size(), plan->storage, plan->operand,
+                                  plan->tile_weight, s), "plan weight phase"));
+      for (auto& q : plan->outer) TRY(launch_rc(launch_outer(q, plan->storage, s), "plan outer weight update"));
+      return ok();
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int ipc_plan_step(ipc_plan* plan, int steps, void* stream) {
+  if (!plan) return fail(IPC_ERR_NULL, "plan is NULL");
+  if (!plan->bound) return fail(IPC_ERR_STATE, "plan has no bound buffers");
+  if (steps < 0) return fail(IPC_ERR_SHAPE, "steps must be >= 0");
+  hipStream_t s = (hipStream_t)stream;
+  for (int t = 0; t < steps; ++t)
+    for (int phase = IPC_PHASE_PRED; phase <= IPC_PHASE_WEIGHT; ++phase) TRY(run_phase(plan, phase, s));
+  return ok();
+}
+
+int ipc_plan_phase(ipc_plan* plan, int phase, int reps, void* stream) {
+  if (!plan) return fail(IPC_ERR_NULL, "plan is NULL");
+  if (!plan->bound) return fail(IPC_ERR_STATE, "plan has no bound buffers");
+  if (phase < IPC_PHASE_PRED || phase > IPC_PHASE_WEIGHT) return fail(IPC_ERR_CONFIG, "unknown phase %d", phase);
+  if (reps < 0) return fail(IPC_ERR_SHAPE, "reps must be >= 0");
+  for (int r = 0; r < reps; ++r) TRY(run_phase(plan, phase, (hipStream_t)stream));
+  return ok();
+}
+
+int ipc_plan_forward_init(ipc_plan* plan, void* stream) {
+  if (!plan) return fail(IPC_ERR_NULL, "plan is NULL");
+  if (!plan->bound) return fail(IPC_ERR_STATE, "plan has no bound buffers");
+  hipStream_t s = (hipStream_t)stream;
+  if (plan->act_dst) {
+    const long long n = (long long)plan->dims[plan->L] * plan->B;
+    TRY(launch_rc(launch_act(plan->act_src, plan->act_dst, n, plan->act, plan->storage, s), "plan a[L] = f(x[L])"));
+  }
+  for (auto& q : plan->fwd) {
+    const int tile = pick_tile(q.M, q.N, 1);
+    TRY(launch_rc(launch_gemm(&q, 1, plan->storage, plan->operand, tile, s), "plan forward init"));
+  }
+  return ok();
+}
+
+int ipc_plan_launch_count(const ipc_plan* plan) { return plan ? plan->launches : 0; }
+
+void ipc_plan_destroy(ipc_plan* plan) { delete plan; }
+
+}  // extern "C"

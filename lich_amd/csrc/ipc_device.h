@@ -1,0 +1,122 @@
+// ipc_device.h - device helpers shared by the iPC kernels (gfx950 only).
+//
+// Element types, conversions, the fused activations of
+// src/ipc_tilelang/tilelang_kernels.py:61-96 (activations.py:9-29) evaluated
+// in fp32, and thin wrappers over the CDNA4 MFMA builtins.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ipc {
+
+typedef _Float16 f16;
+typedef __bf16 bf16;
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+enum { ACT_IDENTITY = 0, ACT_RELU = 1, ACT_TANH = 2, ACT_SIGMOID = 3, ACT_SILU = 4, ACT_GELU = 5 };
+
+// ---------------------------------------------------------------- conversions
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(f16 v) { return (float)v; }
+__device__ __forceinline__ float to_f32(bf16 v) { return (float)v; }
+
+template <typename T> __device__ __forceinline__ T cvt(float v);
+template <> __device__ __forceinline__ float cvt<float>(float v) { return v; }
+template <> __device__ __forceinline__ f16 cvt<f16>(float v) { return (f16)v; }
+template <> __device__ __forceinline__ bf16 cvt<bf16>(float v) { return (bf16)v; }
+
+// Loads 4 consecutive elements (aligned to 4 elements) and widens them to fp32.
+__device__ __forceinline__ void load4(const float* p, float o[4]) {
+  const float4 v = *reinterpret_cast<const float4*>(p);
+  o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+}
+__device__ __forceinline__ float h2f(uint32_t bits16, f16*) {
+  return (float)__builtin_bit_cast(f16, (uint16_t)bits16);
+}
+__device__ __forceinline__ float h2f(uint32_t bits16, bf16*) {
+  return __builtin_bit_cast(float, bits16 << 16);
+}
+template <typename T>
+__device__ __forceinline__ void load4_16(const T* p, float o[4]) {
+  const uint2 v = *reinterpret_cast<const uint2*>(p);
+  o[0] = h2f(v.x & 0xffffu, (T*)nullptr);
+  o[1] = h2f(v.x >> 16, (T*)nullptr);
+  o[2] = h2f(v.y & 0xffffu, (T*)nullptr);
+  o[3] = h2f(v.y >> 16, (T*)nullptr);
+}
+__device__ __forceinline__ void load4(const f16* p, float o[4]) { load4_16(p, o); }
+__device__ __forceinline__ void load4(const bf16* p, float o[4]) { load4_16(p, o); }
+
+// ---------------------------------------------------------------- activations
+// fp32 evaluation as in tilelang_kernels.py:61-96.  tanh/exp are the HIP
+// device library's tanhf/expf.
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+__device__ __forceinline__ float act_f(int act, float x) {
+  switch (act) {
+    case ACT_RELU: return x > 0.0f ? x : 0.0f;
+    case ACT_TANH: return tanhf(x);
+    case ACT_SIGMOID: return sigmoidf_(x);
+    case ACT_SILU: return x * sigmoidf_(x);
+    case ACT_GELU: {
+      const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+      return 0.5f * x * (1.0f + tanhf(u));
+    }
+    default: return x;
+  }
+}
+
+__device__ __forceinline__ float act_df(int act, float x) {
+  switch (act) {
+    case ACT_RELU: return x > 0.0f ? 1.0f : 0.0f;
+    case ACT_TANH: { const float y = tanhf(x); return 1.0f - y * y; }
+    case ACT_SIGMOID: { const float y = sigmoidf_(x); return y * (1.0f - y); }
+    case ACT_SILU: { const float s = sigmoidf_(x); return s * (1.0f + x * (1.0f - s)); }
+    case ACT_GELU: {
+      const float c = 0.044715f, k = 0.7978845608028654f;
+      const float u = k * (x + c * x * x * x);
+      const float t = tanhf(u);
+      const float du = k * (1.0f + 3.0f * c * x * x);
+      return 0.5f * (1.0f + t) + 0.5f * x * (1.0f - t * t) * du;
+    }
+    default: return 1.0f;
+  }
+}
+
+// ---------------------------------------------------------------- MFMA
+// 32x32 output block per wave.  Operand lane layout (both operands): lane l
+// supplies row/column (l % 32) and the k-slice (l / 32) of the instruction's
+// K; the fp32 result element j of lane l is C[8*(j/4) + 4*(l/32) + j%4][l%32].
+template <typename OT> struct Mfma32;
+
+template <> struct Mfma32<float> {
+  static constexpr int KI = 2;    // k per instruction
+  static constexpr int KPL = 1;   // k values per lane
+  typedef float operand;
+  __device__ __forceinline__ static f32x16 run(float a, float b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct Mfma32<f16> {
+  static constexpr int KI = 16;
+  static constexpr int KPL = 8;
+  typedef f16x8 operand;
+  __device__ __forceinline__ static f32x16 run(f16x8 a, f16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct Mfma32<bf16> {
+  static constexpr int KI = 16;
+  static constexpr int KPL = 8;
+  typedef bf16x8 operand;
+  __device__ __forceinline__ static f32x16 run(bf16x8 a, bf16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+}  // namespace ipc

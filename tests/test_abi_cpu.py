@@ -1,0 +1,213 @@
+"""CPU tests of the C ABI and the host-side logic (no GPU, no compute calls).
+
+Every call made here fails host-side validation before any HIP call, which
+is exactly what is being tested.
+"""
+import ctypes
+import json
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from lich_amd import _native as nat
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "ipc_hip.h"
+
+
+def _declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^(?:int|void|const char\*)\s+(ipc_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(nat.LIB_PATH))
+    names = _declared_functions()
+    assert len(names) >= 14
+    for name in names:
+        assert hasattr(lib, name), name
+
+
+def test_abi_version_matches_header():
+    m = re.search(r"#define IPC_ABI_VERSION (\d+)", HEADER.read_text())
+    assert nat.lib().ipc_abi_version() == int(m.group(1))
+
+
+def test_header_constants_match_python():
+    text = HEADER.read_text()
+    consts = dict(re.findall(r"#define (IPC_\w+) \(?(-?\d+)\)?", text))
+    assert int(consts["IPC_DT_F32"]) == nat.DT_F32 and int(consts["IPC_DT_BF16"]) == nat.DT_BF16
+    assert int(consts["IPC_ACT_TANH"]) == nat.ACT_CODES["tanh"]
+    assert int(consts["IPC_ACT_GELU"]) == nat.ACT_CODES["gelu"]
+    assert int(consts["IPC_ERR_STATE"]) == nat.ERR_STATE
+    assert int(consts["IPC_TILE_COUNT"]) == nat.TILE_COUNT
+
+
+L = None
+
+
+def _lib():
+    return nat.lib()
+
+
+P = 4096  # a fake, aligned, non-null address; never dereferenced (validation fails first)
+
+
+@pytest.mark.parametrize("args,code,needle", [
+    ((None, P, P, P, 64, 64, 128, 1, 0, 0, 2, -1, None), nat.ERR_NULL, "x_upper"),
+    ((P, P, P, P, 0, 64, 128, 1, 0, 0, 2, -1, None), nat.ERR_SHAPE, "dimensions"),
+    ((P, P, P, P, 64, 64, 128, 0, 0, 0, 2, -1, None), nat.ERR_SHAPE, "groups"),
+    ((P, P, P, P, 64, 64, 128, 1, 7, 0, 2, -1, None), nat.ERR_DTYPE, "storage"),
+    ((P, P, P, P, 64, 64, 128, 1, 1, 2, 2, -1, None), nat.ERR_DTYPE, "16-bit"),
+    ((P, P, P, P, 64, 64, 128, 1, 0, 0, 9, -1, None), nat.ERR_ACT, "activation"),
+    ((P, P, P, P, 64, 64, 128, 1, 0, 0, 2, 7, None), nat.ERR_CONFIG, "tile"),
+    ((P + 2, P, P, P, 64, 64, 128, 1, 0, 0, 2, -1, None), nat.ERR_ALIGN, "aligned"),
+    ((P, P, P, P, 1 << 20, 1 << 20, 128, 1, 0, 0, 2, -1, None), nat.ERR_SHAPE, "too large"),
+])
+def test_pred_err_validation(args, code, needle):
+    assert _lib().ipc_pred_err(*args) == code
+    assert needle in nat.last_error()
+
+
+def test_other_entry_points_validate():
+    lib = _lib()
+    assert lib.ipc_forward(P, P, None, 10, 64, 128, 1, 0, 0, 1, -1, None) == nat.ERR_NULL
+    assert lib.ipc_infer_update(P, P, P, None, None, 64, 10, 128, 1, 0.5, 0, 0, 2, -1, None) == nat.ERR_NULL
+    assert lib.ipc_infer_update(P, P, P, P, P + 1, 64, 10, 128, 1, 0.5, 0, 0, 2, -1, None) == nat.ERR_ALIGN
+    assert lib.ipc_weight_update(P, P, P, 64, 64, -1, 1, 1e-4, 1, 0, 0, 2, -1, None) == nat.ERR_SHAPE
+    assert lib.ipc_weight_update_outer(P, P, P, 64, 64, 33, 1, 1e-4, 1, 0, 2, None) == nat.ERR_SHAPE
+    assert "B <= 32" in nat.last_error()
+    assert lib.ipc_weight_update_outer(P, P, P, 64, 64, 8, 1, 1e-4, 1, 0, 11, None) == nat.ERR_ACT
+
+
+def test_plan_validation():
+    lib = _lib()
+    h = ctypes.c_void_p()
+    dims = (ctypes.c_int * 4)(10, 64, 64, 784)
+    assert lib.ipc_plan_create(None, 3, dims, 128, 0, 0, 2, 1e-4, 0.5, 1, 0) == nat.ERR_NULL
+    assert lib.ipc_plan_create(ctypes.byref(h), 3, None, 128, 0, 0, 2, 1e-4, 0.5, 1, 0) == nat.ERR_NULL
+    assert lib.ipc_plan_create(ctypes.byref(h), 0, dims, 128, 0, 0, 2, 1e-4, 0.5, 1, 0) == nat.ERR_SHAPE
+    assert lib.ipc_plan_create(ctypes.byref(h), 3, dims, 128, 0, 0, 2, 1e-4, 0.5, 1, 5) == nat.ERR_CONFIG
+    assert lib.ipc_plan_create(ctypes.byref(h), 3, dims, 64, 0, 0, 2, 1e-4, 0.5, 1, 1) == nat.ERR_SHAPE
+    bad = (ctypes.c_int * 4)(10, 0, 64, 784)
+    assert lib.ipc_plan_create(ctypes.byref(h), 3, bad, 128, 0, 0, 2, 1e-4, 0.5, 1, 0) == nat.ERR_SHAPE
+    assert lib.ipc_plan_create(ctypes.byref(h), 3, dims, 128, 0, 0, 2, 1e-4, 0.5, 1, 0) == nat.IPC_OK
+    try:
+        # stepping an unbound plan is a state error, not a crash
+        assert lib.ipc_plan_step(h, 1, None) == nat.ERR_STATE
+        assert lib.ipc_plan_forward_init(h, None) == nat.ERR_STATE
+        assert lib.ipc_plan_launch_count(h) == 0
+        arr = (ctypes.c_void_p * 4)(P, P, P, P)
+        assert lib.ipc_plan_bind(h, None, arr, arr, None) == nat.ERR_NULL
+        arr_bad = (ctypes.c_void_p * 4)(P, None, P, P)
+        assert lib.ipc_plan_bind(h, arr_bad, arr, arr, None) == nat.ERR_NULL
+        assert "x[1]" in nat.last_error()
+        # binding fake (never dereferenced) addresses succeeds and prepares 3 launches/step
+        assert lib.ipc_plan_bind(h, arr, arr, arr, None) == nat.IPC_OK
+        assert lib.ipc_plan_launch_count(h) == 3
+    finally:
+        lib.ipc_plan_destroy(h)
+    assert lib.ipc_plan_step(None, 1, None) == nat.ERR_NULL
+    lib.ipc_plan_destroy(None)  # no-op
+
+
+def test_check_maps_codes_to_exceptions():
+    _lib().ipc_pred_err(None, P, P, P, 64, 64, 128, 1, 0, 0, 2, -1, None)
+    with pytest.raises(ValueError, match="x_upper is NULL"):
+        nat.check(nat.ERR_NULL)
+    with pytest.raises(nat.IPCNativeError):
+        nat.check(nat.ERR_LAUNCH)
+    nat.check(nat.IPC_OK)
+
+
+def test_device_check_refuses_without_gpu():
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    with pytest.raises(nat.IPCNativeError):
+        nat.device_arch(0)
+
+
+def test_kernel_config_tile_mapping():
+    from lich_amd.kernels import KernelConfig
+    assert KernelConfig().tile_id() == -1
+    assert KernelConfig(64, 128, 16, 128, 2, True, 8, False).tile_id() == 1  # reference scripts' config
+    assert KernelConfig(128, 128).tile_id() == 2
+    assert KernelConfig(32, 32).tile_id() == 0
+    assert KernelConfig(tile=0).tile_id() == 0
+    with pytest.raises(ValueError):
+        KernelConfig(tile=9).tile_id()
+
+
+def test_builders_validate_arguments_on_host():
+    from lich_amd.kernels import build_prediction_error, build_weight_update_outer
+    with pytest.raises(ValueError):
+        build_prediction_error(64, 64, 128, "softplus", "float32")
+    with pytest.raises(ValueError):
+        build_prediction_error(64, 64, 128, "tanh", "float16", operand_dtype="bfloat16")
+    with pytest.raises(ValueError):
+        build_prediction_error(0, 64, 128, "tanh", "float32")
+    with pytest.raises(ValueError):
+        build_weight_update_outer(64, 64, 64, "tanh", "float32")
+    k = build_prediction_error(64, 64, 128, "tanh", "float32")
+    with pytest.raises(ValueError, match="device tensor"):
+        k(torch.zeros(64, 128), torch.zeros(64, 64), torch.zeros(64, 128), torch.zeros(64, 128))
+
+
+def test_find_internal_square_groups_matches_reference_semantics():
+    from lich_amd.layer_batching import LayerBatchGroup, find_internal_square_groups as f
+    d6 = (10,) + (64,) * 6 + (784,)
+    assert f(d6, max_group_count=2) == (LayerBatchGroup(1, 2, 64), LayerBatchGroup(4, 5, 64))
+    assert f(d6, max_group_count=5) == (LayerBatchGroup(1, 5, 64),)
+    assert f((10,) + (64,) * 4 + (784,), max_group_count=3) == (LayerBatchGroup(1, 3, 64),)
+    assert f((10, 64, 784), max_group_count=2) == ()
+    assert f(d6, max_group_count=1) == ()
+    g = LayerBatchGroup(1, 3, 64)
+    assert g.count == 3 and g.state_count == 4 and g.state_indices == (1, 2, 3, 4)
+
+
+def test_batched_builders_require_square_groups():
+    from lich_amd.layer_batching import build_prediction_error_batched
+    with pytest.raises(ValueError):
+        build_prediction_error_batched(64, 64, 128, 1, "tanh", "float32")
+    with pytest.raises(ValueError):
+        build_prediction_error_batched(64, 32, 128, 2, "tanh", "float32")
+
+
+def test_small_b_policy_reader(tmp_path):
+    from lich_amd.weight_update_specialization import SmallBWeightPolicy
+    p = tmp_path / "policy.json"
+    p.write_text(json.dumps({"entries": [
+        {"M": 64, "K": 784, "B": 4, "activation": "relu", "dtype": "float16", "backend": "outer"},
+        {"M": 64, "K": 64, "B": 4, "backend": "bogus"},
+        {"K": 1},
+    ]}))
+    pol = SmallBWeightPolicy(p)
+    assert pol.backend(M=64, K=784, B=4, activation="relu", dtype=torch.float16) == "outer"
+    assert pol.backend(M=64, K=64, B=4, activation="relu", dtype=torch.float16) == "gemm"
+
+
+def test_product_init_matches_oracle_init():
+    from lich_amd.trainer import init_weights_cpu
+    from oracle.ipc_oracle import init_weights
+    dims = (10, 64, 64, 784)
+    for init in ("kaiming_a_sqrt5", "xavier_uniform"):
+        for a, b in zip(init_weights_cpu(dims, seed=5, init=init), init_weights(dims, seed=5, init=init)):
+            assert torch.equal(a, b)
+
+
+def test_prepare_batch_layout():
+    from lich_amd.trainer import prepare_batch
+    imgs = torch.rand(5, 1, 28, 28)
+    labels = torch.tensor([3, 1, 4, 1, 5])
+    x, y = prepare_batch(imgs, labels, device="cpu", dtype=torch.float32, num_classes=10)
+    assert x.shape == (784, 5) and y.shape == (10, 5)
+    assert torch.equal(x[:, 2], imgs[2].flatten())
+    assert y[:, 0].argmax() == 3 and float(y.sum()) == 5
+
+
+def test_trainer_refuses_cpu_device():
+    from lich_amd.trainer import HipIPC, IPCConfig
+    with pytest.raises(ValueError):
+        HipIPC(IPCConfig(dims=(10, 64, 784)), device="cpu")

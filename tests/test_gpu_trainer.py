@@ -1,0 +1,209 @@
+"""Whole-step GPU parity: the trainer against the fp32 oracle on identical seeded inputs.
+
+Bars (relative errors normalised globally over layers, as the weight deltas
+of the top layers are exactly zero after T steps from the forward init):
+* fp32 mode: states and weight deltas <= 1e-5;
+* 16-bit operand mode after T steps: states <= 2e-2, weight deltas <= 5e-3.
+Exact properties: graph replay == direct launches (bitwise), save-activation
+== recompute (bitwise), and the forward-init wavefront (eps[l] == 0 for
+l > t, dW[l] == 0 for l >= T) holds exactly on the GPU too.
+"""
+import pytest
+import torch
+
+from lich_amd.trainer import HipIPC, IPCConfig
+from oracle import ipc_oracle as O
+from tests.helpers import DEV, report
+
+pytestmark = pytest.mark.gpu
+
+
+def _setup(dims, B, *, seed=0, init="xavier_uniform", input_dist="uniform"):
+    w0 = O.init_weights(dims, seed=seed, init=init)
+    x_in, labels, y = O.make_batch(dims, B, seed=seed, input_dist=input_dist)
+    return w0, x_in, y
+
+
+def _oracle_run(w0, x_in, y, act, T):
+    x = O.forward_init(x_in, y, w0, act)
+    x_t, w_t, e_t = O.run_steps(x, w0, T, act=act, alpha=1e-4, gamma=0.5)
+    return x, x_t, w_t, e_t
+
+
+def _gpu_run(dims, w0, x_in, y, act, T, dtype, **cfg):
+    model = HipIPC(IPCConfig(dims=dims, activation=act, dtype=dtype, **cfg), device=DEV, weights=w0)
+    model.initialize_batch(x_in.to(DEV), y.to(DEV))
+    x_init = [t.clone() for t in model.x]
+    for _ in range(T):
+        model.step_initialized()
+    torch.cuda.synchronize()
+    return model, x_init
+
+
+def _errors(model, w0, x_t, w_t):
+    L = len(w0)
+    hid = range(1, L)
+    s_err = O.global_rel_err([model.x[l] for l in hid], [x_t[l] for l in hid])
+    dw_gpu = [model.w[l].double().cpu() - w0[l].double() for l in range(L)]
+    dw_ref = [w_t[l].double() - w0[l].double() for l in range(L)]
+    return s_err, O.global_rel_err(dw_gpu, dw_ref)
+
+
+def test_c1_cpu_plumbing_config_fp32():
+    """dims (10,64,64,64,784), B=128, tanh, T=4, fp32."""
+    dims, B, T = (10, 64, 64, 64, 784), 128, 4
+    report("c1", dims=dims, B=B, T=T)
+    w0, x_in, y = _setup(dims, B)
+    x0, x_t, w_t, e_t = _oracle_run(w0, x_in, y, "tanh", T)
+    model, x_init = _gpu_run(dims, w0, x_in, y, "tanh", T, torch.float32)
+    assert O.global_rel_err(x_init[1:-1], x0[1:-1]) <= 1e-5
+    s_err, dw_err = _errors(model, w0, x_t, w_t)
+    print(f"c1 fp32: state_err={s_err:.3e} dW_err={dw_err:.3e}")
+    assert s_err <= 1e-5 and dw_err <= 1e-5
+    assert O.global_rel_err(model.e[:-1], e_t) <= 1e-5
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+@pytest.mark.parametrize("act", ["tanh", "relu"])
+@pytest.mark.parametrize("depth", [3, 4, 6])
+def test_c2_paper_profile_fp16_operands(depth, act, seed):
+    """(10, 64^d, 784), B=128, T=4, fp32 master / fp16 operands."""
+    dims, B, T = (10,) + (64,) * depth + (784,), 128, 4
+    report("c2", depth=depth, act=act, seed=seed)
+    w0, x_in, y = _setup(dims, B, seed=seed)
+    _x0, x_t, w_t, _e = _oracle_run(w0, x_in, y, act, T)
+    model, _ = _gpu_run(dims, w0, x_in, y, act, T, torch.float16)
+    s_err, dw_err = _errors(model, w0, x_t, w_t)
+    print(f"c2 d={depth} {act} seed={seed}: state_err={s_err:.3e} dW_err={dw_err:.3e}")
+    assert s_err <= 2e-2 and dw_err <= 5e-3
+
+
+@pytest.mark.parametrize("depth", [3, 6])
+def test_c2_bf16_operands(depth):
+    dims, B, T = (10,) + (64,) * depth + (784,), 128, 4
+    report("c2-bf16", depth=depth)
+    w0, x_in, y = _setup(dims, B, seed=3)
+    _x0, x_t, w_t, _e = _oracle_run(w0, x_in, y, "tanh", T)
+    model, _ = _gpu_run(dims, w0, x_in, y, "tanh", T, torch.bfloat16)
+    s_err, dw_err = _errors(model, w0, x_t, w_t)
+    print(f"c2 bf16 d={depth}: state_err={s_err:.3e} dW_err={dw_err:.3e}")
+    assert s_err <= 2e-2 and dw_err <= 5e-3
+
+
+@pytest.mark.parametrize("mode", ["outer", "gemm"])
+@pytest.mark.parametrize("B", [1, 4, 8])
+def test_c3_small_batch_fp32(B, mode):
+    """(10, 64^4, 784), B in {1,4,8}, fp32, T=8; rank-B outer-product weight update."""
+    dims, T = (10,) + (64,) * 4 + (784,), 8
+    report("c3", B=B, mode=mode)
+    w0, x_in, y = _setup(dims, B, seed=B)
+    _x0, x_t, w_t, _e = _oracle_run(w0, x_in, y, "tanh", T)
+    model, _ = _gpu_run(dims, w0, x_in, y, "tanh", T, torch.float32, weight_update_mode=mode)
+    s_err, dw_err = _errors(model, w0, x_t, w_t)
+    print(f"c3 B={B} {mode}: state_err={s_err:.3e} dW_err={dw_err:.3e}")
+    assert s_err <= 1e-5 and dw_err <= 1e-5
+
+
+def test_c4_wide_bf16_operands():
+    """(1000, 4096^4, 4096), B=1024, inputs N(0,1), tanh, bf16 operands, T=4, recompute."""
+    dims, B, T = (1000,) + (4096,) * 4 + (4096,), 1024, 4
+    report("c4", dims=dims, B=B)
+    w0, x_in, y = _setup(dims, B, seed=0, input_dist="normal")
+    _x0, x_t, w_t, _e = _oracle_run(w0, x_in, y, "tanh", T)
+    model, _ = _gpu_run(dims, w0, x_in, y, "tanh", T, torch.bfloat16)
+    s_err, dw_err = _errors(model, w0, x_t, w_t)
+    print(f"c4 bf16: state_err={s_err:.3e} dW_err={dw_err:.3e}")
+    assert s_err <= 2e-2 and dw_err <= 5e-3
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_forward_init_wavefront_is_exact_on_gpu(dtype):
+    dims, B, T = (10,) + (64,) * 6 + (784,), 128, 4
+    w0, x_in, y = _setup(dims, B, seed=7)
+    model = HipIPC(IPCConfig(dims=dims, activation="tanh", dtype=dtype), device=DEV, weights=w0)
+    model.initialize_batch(x_in.to(DEV), y.to(DEV))
+    x0 = [t.clone() for t in model.x]
+    for t in range(T):
+        model.step_initialized()
+        torch.cuda.synchronize()
+        for l in range(t + 1, model.L):
+            assert torch.count_nonzero(model.e[l]) == 0, (t, l)
+        for l in range(t + 2, model.L):
+            assert torch.equal(model.x[l], x0[l]), (t, l)
+    for l in range(model.L):
+        nz = torch.count_nonzero(model.w[l].cpu() - w0[l])
+        assert (nz == 0) if l >= T else (nz > 0), l
+
+
+def test_graph_replay_equals_direct_bitwise():
+    dims, B, T = (10,) + (64,) * 6 + (784,), 128, 4
+    w0, x_in, y = _setup(dims, B, seed=11)
+    direct = HipIPC(IPCConfig(dims=dims, activation="tanh", dtype=torch.float16), device=DEV, weights=w0)
+    direct.initialize_batch(x_in.to(DEV), y.to(DEV))
+    for _ in range(3 * T):
+        direct.step_initialized()
+    graph = HipIPC(IPCConfig(dims=dims, activation="tanh", dtype=torch.float16), device=DEV, weights=w0)
+    assert graph.prepare_steady_state(x_in.to(DEV), y.to(DEV), steps=T, use_graph=True)
+    for r in range(3):
+        graph.run_prepared_steady_state(steps=T, repeats=1, use_graph=True)
+        torch.cuda.synchronize()
+    for a, b in zip(direct.w + direct.x + direct.e[:-1], graph.w + graph.x + graph.e[:-1]):
+        assert torch.equal(a, b)
+
+
+def test_run_steps_equals_step_loop():
+    dims, B = (10, 64, 64, 784), 128
+    w0, x_in, y = _setup(dims, B, seed=12)
+    m1 = HipIPC(IPCConfig(dims=dims, activation="relu", dtype=torch.float16), device=DEV, weights=w0)
+    m2 = HipIPC(IPCConfig(dims=dims, activation="relu", dtype=torch.float16), device=DEV, weights=w0)
+    for m in (m1, m2):
+        m.initialize_batch(x_in.to(DEV), y.to(DEV))
+    for _ in range(5):
+        m1.step_initialized()
+    m2.run_steps(5)
+    torch.cuda.synchronize()
+    for a, b in zip(m1.w + m1.x, m2.w + m2.x):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_save_activation_equals_recompute(dtype):
+    dims, B, T = (10, 64, 64, 64, 784), 128, 4
+    w0, x_in, y = _setup(dims, B, seed=13)
+    ms = []
+    for recompute in (True, False):
+        m = HipIPC(IPCConfig(dims=dims, activation="gelu", dtype=dtype, recompute_activation=recompute),
+                   device=DEV, weights=w0)
+        m.initialize_batch(x_in.to(DEV), y.to(DEV))
+        for _ in range(T):
+            m.step_initialized()
+        ms.append(m)
+    torch.cuda.synchronize()
+    for a, b in zip(ms[0].w + ms[0].x, ms[1].w + ms[1].x):
+        assert torch.equal(a, b)
+
+
+def test_predict_and_metrics():
+    dims, B = (10, 64, 64, 784), 32
+    w0, x_in, y = _setup(dims, B, seed=14)
+    m = HipIPC(IPCConfig(dims=dims, activation="tanh", dtype=torch.float32), device=DEV, weights=w0)
+    out = m.predict(x_in.to(DEV))
+    assert O.global_rel_err([out], [O.predict(w0, x_in, "tanh")]) <= 1e-5
+    met = m.step(x_in.to(DEV), y.to(DEV))
+    x = O.forward_init(x_in, y, w0, "tanh")
+    _, _, _, om = O.ipc_step(x, w0, act="tanh", alpha=1e-4, gamma=0.5)
+    assert abs(met["max_abs_error"] - om["max_abs_error"]) <= 1e-5 * max(1.0, om["max_abs_error"])
+
+
+def test_reinitialize_with_new_batch_size_rebuilds_buffers():
+    dims = (10, 64, 784)
+    w0 = O.init_weights(dims, seed=1)
+    m = HipIPC(IPCConfig(dims=dims, activation="tanh", dtype=torch.float32), device=DEV, weights=w0)
+    for B in (16, 8, 16):
+        x_in, _, y = O.make_batch(dims, B, seed=B)
+        m.initialize_batch(x_in.to(DEV), y.to(DEV))
+        m.step_initialized()
+        assert m.x[0].shape == (10, B)
+    torch.cuda.synchronize()
+    with pytest.raises(ValueError):
+        m.initialize_batch(torch.zeros(783, 4, device=DEV), torch.zeros(10, 4, device=DEV))

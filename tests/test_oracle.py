@@ -1,0 +1,208 @@
+"""Pins the CPU oracle (``oracle/ipc_oracle.py``) before anything is checked against it.
+
+Each check is chosen so that a plausible mistake fails it: independent
+float64 loops (``oracle/ipc_brute.py``) catch wrong indices, transposes and
+phase order; ``torch.autograd`` pins every activation derivative; closed forms
+and invariants pin special cases.  The reference ships no golden vectors for
+this path, so these checks are the anchor.
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import ipc_brute as brute
+from oracle import ipc_oracle as O
+
+ACTS = ["relu", "tanh", "sigmoid", "silu", "gelu", "identity"]
+
+
+def _tol(a, b):
+    return float((torch.as_tensor(a, dtype=torch.float64) - torch.as_tensor(b, dtype=torch.float64)).abs().max())
+
+
+def _to_list(t):
+    return t.double().tolist()
+
+
+@pytest.mark.parametrize("act", ACTS)
+def test_activation_values_match_math_module(act):
+    xs = torch.linspace(-4, 4, 101, dtype=torch.float64)
+    got = O.act_forward(act, xs)
+    ref = torch.tensor([brute.f(act, float(v)) for v in xs], dtype=torch.float64)
+    assert _tol(got, ref) < 1e-12
+
+
+@pytest.mark.parametrize("act", ACTS)
+def test_activation_derivative_matches_autograd(act):
+    xs = torch.linspace(-4, 4, 97, dtype=torch.float64)  # avoids exactly 0 for relu
+    xs = xs[xs != 0].clone().requires_grad_(True)
+    y = O.act_forward(act, xs).sum()
+    (g,) = torch.autograd.grad(y, xs)
+    assert _tol(O.act_derivative(act, xs.detach()), g) < 1e-12
+    ref = torch.tensor([brute.df(act, float(v)) for v in xs.detach()], dtype=torch.float64)
+    assert _tol(O.act_derivative(act, xs.detach()), ref) < 1e-12
+
+
+def test_relu_derivative_is_strict_at_zero():
+    # activations.py:17 and tilelang_kernels.py:79 use x > 0.
+    assert float(O.act_derivative("relu", torch.zeros(1))) == 0.0
+
+
+def test_gelu_is_the_tanh_approximation():
+    v = 1.3
+    k = math.sqrt(2 / math.pi)
+    expect = 0.5 * v * (1 + math.tanh(k * (v + 0.044715 * v ** 3)))
+    assert abs(float(O.act_forward("gelu", torch.tensor([v], dtype=torch.float64))) - expect) < 1e-15
+
+
+def test_one_hot_layout_is_classes_by_batch():
+    y = O.one_hot(torch.tensor([2, 0, 1]), 4)
+    assert y.shape == (4, 3)
+    assert y[:, 0].tolist() == [0, 0, 1, 0] and y[:, 1].tolist() == [1, 0, 0, 0]
+
+
+@pytest.mark.parametrize("init", ["kaiming_a_sqrt5", "xavier_uniform"])
+def test_init_bounds_and_layer_order(init):
+    dims = (10, 64, 64, 784)
+    ws = O.init_weights(dims, seed=3, init=init)
+    for w, (n_l, n_u) in zip(ws, zip(dims[:-1], dims[1:])):
+        assert w.shape == (n_l, n_u)
+        bound = 1 / math.sqrt(n_u) if init == "kaiming_a_sqrt5" else math.sqrt(6 / (n_l + n_u))
+        assert float(w.abs().max()) <= bound * (1 + 1e-6)
+        assert float(w.abs().max()) > 0.9 * bound  # uses the full range
+    # one generator consumed strictly in layer order: the first layer does not
+    # depend on later shapes, and the draw is reproducible from the seed.
+    ws2 = O.init_weights((10, 64, 32, 784), seed=3, init=init)
+    assert torch.equal(ws[0], ws2[0])
+    assert torch.equal(O.init_weights(dims, seed=3, init=init)[2], ws[2])
+    assert not torch.equal(O.init_weights(dims, seed=4, init=init)[0], ws[0])
+
+
+def _tiny(act, seed=0, dims=(3, 4, 5, 6), B=2):
+    torch.manual_seed(seed)
+    ws = [torch.randn(a, b, dtype=torch.float64) * 0.5 for a, b in zip(dims[:-1], dims[1:])]
+    xs = [torch.randn(d, B, dtype=torch.float64) for d in dims]
+    return xs, ws
+
+
+@pytest.mark.parametrize("act", ACTS)
+def test_step_matches_brute_force_loops(act):
+    xs, ws = _tiny(act, seed=11)
+    nx, nw, e, _ = O.ipc_step(xs, ws, act=act, alpha=0.05, gamma=0.3)
+    bx, bw, be = brute.step([_to_list(v) for v in xs], [_to_list(v) for v in ws], act, 0.05, 0.3)
+    for a, b in zip(e, be):
+        assert _tol(a, b) < 1e-12
+    for a, b in zip(nx, bx):
+        assert _tol(a, b) < 1e-12
+    for a, b in zip(nw, bw):
+        assert _tol(a, b) < 1e-12
+
+
+def test_several_steps_match_brute_force():
+    xs, ws = _tiny("tanh", seed=5, dims=(2, 3, 3, 4), B=3)
+    bx, bw = [_to_list(v) for v in xs], [_to_list(v) for v in ws]
+    for _ in range(3):
+        xs, ws, _e, _m = O.ipc_step(xs, ws, act="tanh", alpha=0.1, gamma=0.5)
+        bx, bw, _be = brute.step(bx, bw, "tanh", 0.1, 0.5)
+    assert max(_tol(a, b) for a, b in zip(xs, bx)) < 1e-12
+    assert max(_tol(a, b) for a, b in zip(ws, bw)) < 1e-12
+
+
+def test_endpoints_stay_fixed():
+    xs, ws = _tiny("tanh", seed=1)
+    nx, _, _, _ = O.ipc_step(xs, ws, act="tanh", alpha=0.1, gamma=0.5)
+    assert torch.equal(nx[0], xs[0]) and torch.equal(nx[-1], xs[-1])
+
+
+def test_weight_update_uses_post_update_state():
+    # reference.py:53-57: the weight update consumes the just-updated x[l+1].
+    xs, ws = _tiny("tanh", seed=2)
+    nx, nw, e, _ = O.ipc_step(xs, ws, act="tanh", alpha=0.1, gamma=0.5)
+    l = 1
+    post = ws[l] + 0.1 * e[l] @ torch.tanh(nx[l + 1]).T
+    pre = ws[l] + 0.1 * e[l] @ torch.tanh(xs[l + 1]).T
+    assert _tol(nw[l], post) < 1e-14
+    assert _tol(nw[l], pre) > 1e-6
+
+
+def test_special_cases():
+    xs, ws = _tiny("sigmoid", seed=3)
+    nx, nw, e, _ = O.ipc_step(xs, ws, act="sigmoid", alpha=0.0, gamma=0.0)
+    assert all(torch.equal(a, b) for a, b in zip(nx, xs))
+    assert all(torch.equal(a, b) for a, b in zip(nw, ws))
+    zeros = [torch.zeros_like(w) for w in ws]
+    e0 = O.prediction_errors(xs, zeros, "sigmoid")
+    assert all(torch.equal(a, b) for a, b in zip(e0, xs[:-1]))
+    # E_lower = 0 for every layer => x -= gamma * eps
+    x_new, _ = O.infer_update(xs[1], e0[1], ws[0], torch.zeros_like(xs[0]), "sigmoid", 0.25)
+    assert _tol(x_new, xs[1] - 0.25 * e0[1]) < 1e-15
+
+
+def test_weight_delta_is_linear_in_alpha():
+    xs, ws = _tiny("gelu", seed=4)
+    _, w1, _, _ = O.ipc_step(xs, ws, act="gelu", alpha=1e-3, gamma=0.5)
+    _, w2, _, _ = O.ipc_step(xs, ws, act="gelu", alpha=2e-3, gamma=0.5)
+    for a, b, w0 in zip(w1, w2, ws):
+        assert _tol(2 * (a - w0), b - w0) < 1e-15
+
+
+def test_rank_b_outer_equals_gemm_sum():
+    torch.manual_seed(0)
+    w = torch.randn(5, 7, dtype=torch.float64)
+    e = torch.randn(5, 3, dtype=torch.float64)
+    xu = torch.randn(7, 3, dtype=torch.float64)
+    outer = w.clone()
+    for b in range(3):
+        outer += 0.01 * torch.outer(e[:, b], torch.relu(xu[:, b]))
+    assert _tol(O.weight_update(w, e, xu, "relu", 0.01), outer) < 1e-14
+    assert _tol(O.weight_update(w, e, torch.relu(xu), "relu", 0.01, recompute=False), outer) < 1e-14
+
+
+@pytest.mark.parametrize("depth,T", [(3, 2), (4, 4), (6, 4)])
+def test_forward_init_wavefront_invariant(depth, T):
+    """From the forward init, after t steps eps[l] == 0 exactly for l > t and
+    x[l] is untouched for l > t; dW[l] == 0 exactly for l >= T."""
+    dims = (10,) + (16,) * depth + (40,)
+    ws = O.init_weights(dims, seed=1, init="xavier_uniform")
+    x_in, _, y = O.make_batch(dims, 8, seed=1)
+    x0 = O.forward_init(x_in, y, ws, "tanh")
+    x, w = x0, ws
+    for t in range(T):
+        e = O.prediction_errors(x, w, "tanh")
+        for l in range(t + 1, len(ws)):
+            assert torch.count_nonzero(e[l]) == 0
+        for l in range(t + 2, len(ws)):
+            assert torch.equal(x[l], x0[l])
+        x, w, _, _ = O.ipc_step(x, w, act="tanh", alpha=1e-4, gamma=0.5)
+    for l in range(len(ws)):
+        d = w[l] - ws[l]
+        if l >= T:
+            assert torch.count_nonzero(d) == 0
+        else:
+            assert torch.count_nonzero(d) > 0
+
+
+def test_forward_init_matches_predict_chain():
+    dims = (10, 16, 16, 40)
+    ws = O.init_weights(dims, seed=2)
+    x_in, _, y = O.make_batch(dims, 4, seed=2)
+    x = O.forward_init(x_in, y, ws, "relu")
+    assert torch.equal(x[0], y)
+    assert _tol(x[1], ws[1] @ torch.relu(ws[2] @ torch.relu(x_in))) < 1e-6
+    assert _tol(O.predict(ws, x_in, "relu"), ws[0] @ torch.relu(x[1])) < 1e-6
+
+
+def test_global_rel_err():
+    a = [torch.tensor([1.0, 2.0]), torch.tensor([0.0])]
+    b = [torch.tensor([1.0, 4.0]), torch.tensor([0.0])]
+    assert O.global_rel_err(a, b) == pytest.approx(0.5)
+    assert O.global_rel_err([torch.zeros(2)], [torch.zeros(2)]) == 0.0
+
+
+def test_flops_per_sample_matches_published_derivation():
+    # 784->64^d->10: 253,696 / 278,272 / 327,424 flop per sample for d=3/4/6.
+    assert O.flops_per_sample((10,) + (64,) * 3 + (784,)) == 253_696
+    assert O.flops_per_sample((10,) + (64,) * 4 + (784,)) == 278_272
+    assert O.flops_per_sample((10,) + (64,) * 6 + (784,)) == 327_424
+    assert O.flops_per_sample((1000,) + (4096,) * 4 + (4096,)) == 393_674_752
