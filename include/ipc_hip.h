@@ -89,11 +89,18 @@ int ipc_device_check(int device, char* buf, int buflen);
  * the subtraction is rounded like tilelang_kernels.py:173.
  * storage: element type of all four tensors; operand: type the GEMM operands
  * are rounded to (must equal storage when storage is 16-bit); accumulation is
- * always fp32.
+ * always fp32.  split (fp32 storage with 16-bit operands only, else 1):
+ * 1 = one MFMA per block; 2 = W carried as hi + lo 16-bit terms (2 MFMAs);
+ * 3 = W and f(X_upper) both split, hi*hi + lo*hi + hi*lo (3 MFMAs).  The
+ * prediction error is a cancelling difference, and the split keeps its error
+ * near fp32 level.
  */
+#define IPC_SPLIT_NONE 1
+#define IPC_SPLIT_W 2
+#define IPC_SPLIT_WX 3
 int ipc_pred_err(const void* x_upper, const void* w, const void* x_lower, void* e,
                  int M, int K, int B, int groups,
-                 int storage, int operand, int act, int tile, void* stream);
+                 int storage, int operand, int split, int act, int tile, void* stream);
 
 /*
  * Forward prediction OUT[g] = W[g] @ f(X_upper[g]).  Used for the hidden-state
@@ -101,7 +108,7 @@ int ipc_pred_err(const void* x_upper, const void* w, const void* x_lower, void* 
  */
 int ipc_forward(const void* x_upper, const void* w, void* out,
                 int M, int K, int B, int groups,
-                int storage, int operand, int act, int tile, void* stream);
+                int storage, int operand, int split, int act, int tile, void* stream);
 
 /*
  * Inference update X[g] += gamma * (-E[g] + f'(X[g]) * W_lower[g]^T @ E_lower[g]),
@@ -146,8 +153,9 @@ int ipc_weight_update_outer(void* w, const void* e, const void* x_upper, int M, 
  */
 typedef struct ipc_plan ipc_plan;
 
+/* split applies to the prediction phase and the forward initialisation. */
 int ipc_plan_create(ipc_plan** out, int L, const int* dims, int B,
-                    int storage, int operand, int act, float alpha, float gamma,
+                    int storage, int operand, int split, int act, float alpha, float gamma,
                     int recompute, int weight_mode);
 
 /* Binds the caller's buffers: x and e hold L+1 pointers ([d_l, B] each; e[L]

@@ -25,6 +25,7 @@ ACT_CODES = {"identity": 0, "linear": 0, "relu": 1, "tanh": 2, "sigmoid": 3, "si
 TILE_AUTO = -1
 TILE_COUNT = 3
 WMODE = {"gemm": 0, "outer": 1, "auto": 2}
+SPLIT_NONE, SPLIT_W, SPLIT_WX = 1, 2, 3
 
 _DTYPE_CODES = {torch.float32: DT_F32, torch.float16: DT_F16, torch.bfloat16: DT_BF16}
 
@@ -63,12 +64,12 @@ def _declare(lib):
         "ipc_abi_version": ([], i),
         "ipc_last_error": ([], c_char_p),
         "ipc_device_check": ([i, c_char_p, i], i),
-        "ipc_pred_err": ([vp, vp, vp, vp, i, i, i, i, i, i, i, i, vp], i),
-        "ipc_forward": ([vp, vp, vp, i, i, i, i, i, i, i, i, vp], i),
+        "ipc_pred_err": ([vp, vp, vp, vp, i, i, i, i, i, i, i, i, i, vp], i),
+        "ipc_forward": ([vp, vp, vp, i, i, i, i, i, i, i, i, i, vp], i),
         "ipc_infer_update": ([vp, vp, vp, vp, vp, i, i, i, i, f, i, i, i, i, vp], i),
         "ipc_weight_update": ([vp, vp, vp, i, i, i, i, f, i, i, i, i, i, vp], i),
         "ipc_weight_update_outer": ([vp, vp, vp, i, i, i, i, f, i, i, i, vp], i),
-        "ipc_plan_create": ([POINTER(vp), i, POINTER(c_int), i, i, i, i, f, f, i, i], i),
+        "ipc_plan_create": ([POINTER(vp), i, POINTER(c_int), i, i, i, i, i, f, f, i, i], i),
         "ipc_plan_bind": ([vp, POINTER(vp), POINTER(vp), POINTER(vp), POINTER(vp)], i),
         "ipc_plan_step": ([vp, i, vp], i),
         "ipc_plan_forward_init": ([vp, vp], i),

@@ -73,6 +73,16 @@ int check_ptr(const void* p, const char* name, int esize) {
   return ok();
 }
 
+int check_split(int split) {
+  if (split < IPC_SPLIT_NONE || split > IPC_SPLIT_WX) return fail(IPC_ERR_CONFIG, "unknown split %d", split);
+  return ok();
+}
+
+// Splitting only changes anything for fp32 data feeding 16-bit operands.
+int effective_split(int storage, int operand, int split) {
+  return (storage == IPC_DT_F32 && operand != IPC_DT_F32) ? split : IPC_SPLIT_NONE;
+}
+
 int check_tile(int tile) {
   if (tile < IPC_TILE_AUTO || tile >= IPC_TILE_COUNT)
     return fail(IPC_ERR_CONFIG, "unknown tile config %d", tile);
@@ -194,8 +204,9 @@ int ipc_device_check(int device, char* buf, int buflen) {
 }
 
 int ipc_pred_err(const void* x_upper, const void* w, const void* x_lower, void* e, int M, int K, int B,
-                 int groups, int storage, int operand, int act, int tile, void* stream) {
+                 int groups, int storage, int operand, int split, int act, int tile, void* stream) {
   TRY(check_dtypes(storage, operand));
+  TRY(check_split(split));
   TRY(check_act(act));
   TRY(check_dims(M, K, B, groups));
   TRY(check_tile(tile));
@@ -206,12 +217,14 @@ int ipc_pred_err(const void* x_upper, const void* w, const void* x_lower, void* 
   TRY(check_ptr(e, "e", es));
   GemmProblem p = make_pf(KIND_PRED, x_upper, w, x_lower, e, M, K, B, groups, act, es);
   if (tile == IPC_TILE_AUTO) tile = pick_tile(M, B, groups);
-  return launch_rc(launch_gemm(&p, 1, storage, operand, tile, (hipStream_t)stream), "ipc_pred_err");
+  return launch_rc(launch_gemm(&p, 1, storage, operand, effective_split(storage, operand, split), tile,
+                               (hipStream_t)stream), "ipc_pred_err");
 }
 
 int ipc_forward(const void* x_upper, const void* w, void* out, int M, int K, int B, int groups, int storage,
-                int operand, int act, int tile, void* stream) {
+                int operand, int split, int act, int tile, void* stream) {
   TRY(check_dtypes(storage, operand));
+  TRY(check_split(split));
   TRY(check_act(act));
   TRY(check_dims(M, K, B, groups));
   TRY(check_tile(tile));
@@ -221,7 +234,8 @@ int ipc_forward(const void* x_upper, const void* w, void* out, int M, int K, int
   TRY(check_ptr(out, "out", es));
   GemmProblem p = make_pf(KIND_FWD, x_upper, w, nullptr, out, M, K, B, groups, act, es);
   if (tile == IPC_TILE_AUTO) tile = pick_tile(M, B, groups);
-  return launch_rc(launch_gemm(&p, 1, storage, operand, tile, (hipStream_t)stream), "ipc_forward");
+  return launch_rc(launch_gemm(&p, 1, storage, operand, effective_split(storage, operand, split), tile,
+                               (hipStream_t)stream), "ipc_forward");
 }
 
 int ipc_infer_update(void* x, const void* e, const void* w_lower, const void* e_lower, void* a_out, int M,
@@ -239,7 +253,8 @@ int ipc_infer_update(void* x, const void* e, const void* w_lower, const void* e_
   if (a_out) TRY(check_ptr(a_out, "a_out", es));
   GemmProblem p = make_inf(x, e, w_lower, e_lower, a_out, M, K, B, groups, gamma, act, es);
   if (tile == IPC_TILE_AUTO) tile = pick_tile(M, B, groups);
-  return launch_rc(launch_gemm(&p, 1, storage, operand, tile, (hipStream_t)stream), "ipc_infer_update");
+  return launch_rc(launch_gemm(&p, 1, storage, operand, IPC_SPLIT_NONE, tile, (hipStream_t)stream),
+                   "ipc_infer_update");
 }
 
 int ipc_weight_update(void* w, const void* e, const void* x_upper, int M, int K, int B, int groups,
@@ -254,7 +269,8 @@ int ipc_weight_update(void* w, const void* e, const void* x_upper, int M, int K,
   TRY(check_ptr(x_upper, "x_upper", es));
   GemmProblem p = make_wgt(w, e, x_upper, M, K, B, groups, alpha, recompute, act, es);
   if (tile == IPC_TILE_AUTO) tile = pick_tile(M, K, groups);
-  return launch_rc(launch_gemm(&p, 1, storage, operand, tile, (hipStream_t)stream), "ipc_weight_update");
+  return launch_rc(launch_gemm(&p, 1, storage, operand, IPC_SPLIT_NONE, tile, (hipStream_t)stream),
+                   "ipc_weight_update");
 }
 
 int ipc_weight_update_outer(void* w, const void* e, const void* x_upper, int M, int K, int B, int groups,
@@ -275,7 +291,7 @@ int ipc_weight_update_outer(void* w, const void* e, const void* x_upper, int M, 
 
 // =========================================================================== plan
 struct ipc_plan {
-  int L = 0, B = 0, storage = 0, operand = 0, act = 0, recompute = 1, wmode = 0;
+  int L = 0, B = 0, storage = 0, operand = 0, split = 1, act = 0, recompute = 1, wmode = 0;
   float alpha = 0.f, gamma = 0.f;
   std::vector<int> dims;
   bool bound = false;
@@ -292,13 +308,14 @@ struct ipc_plan {
 
 extern "C" {
 
-int ipc_plan_create(ipc_plan** out, int L, const int* dims, int B, int storage, int operand, int act,
+int ipc_plan_create(ipc_plan** out, int L, const int* dims, int B, int storage, int operand, int split, int act,
                     float alpha, float gamma, int recompute, int weight_mode) {
   if (!out) return fail(IPC_ERR_NULL, "out is NULL");
   *out = nullptr;
   if (!dims) return fail(IPC_ERR_NULL, "dims is NULL");
   if (L < 1 || L > 4096) return fail(IPC_ERR_SHAPE, "L must be in [1, 4096] (got %d)", L);
   TRY(check_dtypes(storage, operand));
+  TRY(check_split(split));
   TRY(check_act(act));
   if (weight_mode < IPC_WMODE_GEMM || weight_mode > IPC_WMODE_AUTO)
     return fail(IPC_ERR_CONFIG, "unknown weight mode %d", weight_mode);
@@ -308,6 +325,7 @@ int ipc_plan_create(ipc_plan** out, int L, const int* dims, int B, int storage, 
   ipc_plan* p = new (std::nothrow) ipc_plan();
   if (!p) return fail(IPC_ERR_CONFIG, "out of host memory");
   p->L = L; p->B = B; p->storage = storage; p->operand = operand; p->act = act;
+  p->split = effective_split(storage, operand, split);
   p->alpha = alpha; p->gamma = gamma; p->recompute = recompute ? 1 : 0;
   p->wmode = weight_mode;
   p->dims.assign(dims, dims + L + 1);
@@ -378,15 +396,15 @@ int run_phase(ipc_plan* plan, int phase, hipStream_t s) {
   switch (phase) {
     case IPC_PHASE_PRED:
       return launch_rc(launch_gemm(plan->pred.data(), (int)plan->pred.size(), plan->storage, plan->operand,
-                                   plan->tile_pred, s), "plan prediction phase");
+                                   plan->split, plan->tile_pred, s), "plan prediction phase");
     case IPC_PHASE_INFER:
       if (plan->infer.empty()) return ok();
       return launch_rc(launch_gemm(plan->infer.data(), (int)plan->infer.size(), plan->storage, plan->operand,
-                                   plan->tile_infer, s), "plan inference phase");
+                                   IPC_SPLIT_NONE, plan->tile_infer, s), "plan inference phase");
     default:
       if (!plan->weight.empty())
         TRY(launch_rc(launch_gemm(plan->weight.data(), (int)plan->weight.size(), plan->storage, plan->operand,
-                                  plan->tile_weight, s), "plan weight phase"));
+                                  IPC_SPLIT_NONE, plan->tile_weight, s), "plan weight phase"));
       for (auto& q : plan->outer) TRY(launch_rc(launch_outer(q, plan->storage, s), "plan outer weight update"));
       return ok();
   }
@@ -425,7 +443,7 @@ int ipc_plan_forward_init(ipc_plan* plan, void* stream) {
   }
   for (auto& q : plan->fwd) {
     const int tile = pick_tile(q.M, q.N, 1);
-    TRY(launch_rc(launch_gemm(&q, 1, plan->storage, plan->operand, tile, s), "plan forward init"));
+    TRY(launch_rc(launch_gemm(&q, 1, plan->storage, plan->operand, plan->split, tile, s), "plan forward init"));
   }
   return ok();
 }

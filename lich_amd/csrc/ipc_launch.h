@@ -45,7 +45,9 @@ struct GemmBatch {
 
 // Launches `count` problems (split into several launches if count > MAX_BATCH);
 // `storage`/`operand` are DT_* codes, `tile` a tile id.
-hipError_t launch_gemm(const GemmProblem* probs, int count, int storage, int operand, int tile,
+// `split` (1, 2 or 3) selects the error-compensated 16-bit prediction
+// operands of the PF layout; other layouts ignore it.
+hipError_t launch_gemm(const GemmProblem* probs, int count, int storage, int operand, int split, int tile,
                        hipStream_t s);
 
 struct OuterProblem {

@@ -59,6 +59,8 @@ __global__ void __launch_bounds__(OUTER_TK) outer_kernel(const OuterProblem p) {
 #pragma unroll
     for (int r = 0; r < OUTER_RM; ++r) {
       if (r < mn) {
+        // W + (alpha * acc), each rounded, as the fp32 reference does.
+#pragma clang fp contract(off)
         const long long o = (long long)(m0 + r) * K + k;
         W[o] = cvt<ST>(to_f32(W[o]) + p.alpha * acc[r]);
       }

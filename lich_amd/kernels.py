@@ -88,7 +88,7 @@ class _Kernel:
     """Common state of a built kernel callable."""
 
     def __init__(self, kind: str, M: int, K: int, B: int, activation: str, dtype, cfg, operand_dtype,
-                 groups: int = 1):
+                 groups: int = 1, split: int = 1):
         self.kind = kind
         self.M, self.K, self.B = int(M), int(K), int(B)
         self.groups = int(groups)
@@ -103,6 +103,9 @@ class _Kernel:
             raise ValueError("16-bit storage requires operand_dtype == dtype")
         self.cfg = cfg if cfg is not None else KernelConfig()
         self.tile = self.cfg.tile_id()
+        if int(split) not in (1, 2, 3):
+            raise ValueError(f"split must be 1, 2 or 3 (got {split})")
+        self.split = int(split)
 
     def _shape(self, *dims):
         return (self.groups, *dims) if self.groups > 1 else tuple(dims)
@@ -119,7 +122,7 @@ class PredictionErrorKernel(_Kernel):
         _check(e, "E", self._shape(M, B), dt)
         nat.check(nat.lib().ipc_pred_err(
             x_upper.data_ptr(), w.data_ptr(), x_lower.data_ptr(), e.data_ptr(), M, K, B, self.groups,
-            self.storage, self.operand, self.act, self.tile, nat.current_stream_handle(e.device)))
+            self.storage, self.operand, self.split, self.act, self.tile, nat.current_stream_handle(e.device)))
 
 
 class ForwardKernel(_Kernel):
@@ -132,7 +135,7 @@ class ForwardKernel(_Kernel):
         _check(out, "OUT", self._shape(M, B), dt)
         nat.check(nat.lib().ipc_forward(
             x_upper.data_ptr(), w.data_ptr(), out.data_ptr(), M, K, B, self.groups,
-            self.storage, self.operand, self.act, self.tile, nat.current_stream_handle(out.device)))
+            self.storage, self.operand, self.split, self.act, self.tile, nat.current_stream_handle(out.device)))
 
 
 class InferenceUpdateKernel(_Kernel):
@@ -204,16 +207,19 @@ class OuterWeightUpdateKernel(_Kernel):
 
 @lru_cache(maxsize=256)
 def build_prediction_error(M: int, K: int, B: int, activation: str, dtype, cfg: KernelConfig | None = None,
-                           *, operand_dtype=None):
-    """``W[M,K] @ f(X_upper[K,B]) -> E[M,B]`` (reference ``tilelang_kernels.py:114-177``)."""
-    return PredictionErrorKernel("prediction", M, K, B, activation, dtype, cfg, operand_dtype)
+                           *, operand_dtype=None, split: int = 1):
+    """``W[M,K] @ f(X_upper[K,B]) -> E[M,B]`` (reference ``tilelang_kernels.py:114-177``).
+
+    ``split`` (fp32 storage with 16-bit operands): 1 = plain 16-bit operands,
+    2 = W as hi + lo 16-bit terms, 3 = W and f(X_upper) both split."""
+    return PredictionErrorKernel("prediction", M, K, B, activation, dtype, cfg, operand_dtype, split=split)
 
 
 @lru_cache(maxsize=256)
 def build_forward(M: int, K: int, B: int, activation: str, dtype, cfg: KernelConfig | None = None,
-                  *, operand_dtype=None):
+                  *, operand_dtype=None, split: int = 1):
     """``OUT = W f(X_upper)`` (forward initialisation ``trainer.py:512-515``)."""
-    return ForwardKernel("forward", M, K, B, activation, dtype, cfg, operand_dtype)
+    return ForwardKernel("forward", M, K, B, activation, dtype, cfg, operand_dtype, split=split)
 
 
 @lru_cache(maxsize=256)

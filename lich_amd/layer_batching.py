@@ -84,17 +84,18 @@ def _square(M: int, K: int, groups: int) -> None:
 
 @lru_cache(maxsize=128)
 def build_prediction_error_batched(M: int, K: int, B: int, groups: int, activation: str, dtype,
-                                   cfg: KernelConfig | None = None, *, operand_dtype=None):
+                                   cfg: KernelConfig | None = None, *, operand_dtype=None, split: int = 1):
     """``E[g] = X_lower[g] - W[g] f(X_upper[g])`` over ``[G, ...]`` tensors (reference ``:89-150``)."""
     _square(M, K, groups)
-    return PredictionErrorKernel("prediction", M, K, B, activation, dtype, cfg, operand_dtype, groups=groups)
+    return PredictionErrorKernel("prediction", M, K, B, activation, dtype, cfg, operand_dtype, groups=groups,
+                                 split=split)
 
 
 @lru_cache(maxsize=128)
 def build_forward_batched(M: int, K: int, B: int, groups: int, activation: str, dtype,
-                          cfg: KernelConfig | None = None, *, operand_dtype=None):
+                          cfg: KernelConfig | None = None, *, operand_dtype=None, split: int = 1):
     _square(M, K, groups)
-    return ForwardKernel("forward", M, K, B, activation, dtype, cfg, operand_dtype, groups=groups)
+    return ForwardKernel("forward", M, K, B, activation, dtype, cfg, operand_dtype, groups=groups, split=split)
 
 
 @lru_cache(maxsize=128)

@@ -60,6 +60,11 @@ class IPCConfig:
     # additions
     master_dtype: torch.dtype = torch.float32
     init: str = "kaiming_a_sqrt5"
+    # Prediction-phase operand split for 16-bit operands over fp32 master
+    # data: 1 plain, 2 = W as hi + lo terms, 3 = W and f(x) both split.  None
+    # picks 3 for narrow nets (every width <= 1024, latency-bound, the extra
+    # MFMAs are free) and 2 otherwise.
+    pred_split: int | None = None
 
 
 def init_weights_cpu(dims: Sequence[int], *, seed: int, init: str) -> list[torch.Tensor]:
@@ -116,6 +121,12 @@ class HipIPC:
         self._operand = nat.dtype_code(self.operand_dtype)
         if self._storage != nat.DT_F32 and self._operand != self._storage:
             raise ValueError("16-bit master_dtype requires dtype == master_dtype")
+        if cfg.pred_split is not None:
+            self.pred_split = int(cfg.pred_split)
+        elif self._storage == nat.DT_F32 and self._operand != nat.DT_F32:
+            self.pred_split = 3 if max(int(d) for d in cfg.dims) <= 1024 else 2
+        else:
+            self.pred_split = 1
         mode = str(cfg.weight_update_mode).lower()
         if mode not in nat.WMODE:
             raise ValueError(f"Unknown weight_update_mode {cfg.weight_update_mode!r}")
@@ -165,7 +176,7 @@ class HipIPC:
         dims = (ctypes.c_int * len(self.cfg.dims))(*[int(d) for d in self.cfg.dims])
         handle = ctypes.c_void_p()
         nat.check(nat.lib().ipc_plan_create(
-            ctypes.byref(handle), self.L, dims, int(B), self._storage, self._operand, self._act,
+            ctypes.byref(handle), self.L, dims, int(B), self._storage, self._operand, self.pred_split, self._act,
             float(self.cfg.alpha), float(self.cfg.gamma), int(self.recompute_activation), self._wmode))
         self._plan = handle
         a = None if self.a is None else _ptr_array(self.a)
@@ -325,7 +336,7 @@ class HipIPC:
             M, K = int(self.cfg.dims[l]), int(self.cfg.dims[l + 1])
             out = torch.empty((M, B), device=self.device, dtype=self.storage_dtype)
             build_forward(M, K, B, self.act_name, self.storage_dtype, None,
-                          operand_dtype=self.operand_dtype)(h, self.w[l], out)
+                          operand_dtype=self.operand_dtype, split=self.pred_split)(h, self.w[l], out)
             h = out
         return h
 

@@ -25,11 +25,43 @@ def _r(t: torch.Tensor, op: torch.dtype) -> torch.Tensor:
     return t.to(op).to(torch.float32)
 
 
-def step_operand16(x: Sequence[torch.Tensor], w: Sequence[torch.Tensor], *, act: str, alpha: float,
-                   gamma: float, op: torch.dtype):
-    """fp32 master x/eps/W; GEMM operands rounded to ``op``; fp32 accumulate."""
+def _split(t: torch.Tensor, op: torch.dtype):
+    hi = _r(t, op)
+    return hi, _r(t - hi, op)
+
+
+def pred_matmul(w: torch.Tensor, a: torch.Tensor, op: torch.dtype, split: int = 1) -> torch.Tensor:
+    """``w @ a`` with 16-bit operands: split 1 rounds both operands once;
+    split 2 carries ``w`` as hi + lo terms; split 3 carries both operands as
+    hi + lo and keeps hi*hi + lo*hi + hi*lo (the lo*lo term is dropped)."""
+    if split == 1:
+        return _r(w, op) @ _r(a, op)
+    wh, wl = _split(w, op)
+    if split == 2:
+        ah = _r(a, op)
+        return wh @ ah + wl @ ah
+    ah, al = _split(a, op)
+    return wh @ ah + wl @ ah + wh @ al
+
+
+def forward_init_operand16(x_input, y_target, w, *, act: str, op: torch.dtype, split: int = 1):
+    """Forward initialisation with the same prediction arithmetic as the step."""
     L = len(w)
-    e = [x[l] - _r(w[l], op) @ _r(act_forward(act, x[l + 1]), op) for l in range(L)]
+    x = [None] * (L + 1)
+    x[L] = x_input.clone()
+    for l in reversed(range(L)):
+        p = pred_matmul(w[l], act_forward(act, x[l + 1]), op, split)
+        x[l] = p if l > 0 else None
+    x[0] = y_target.clone()
+    return x
+
+
+def step_operand16(x: Sequence[torch.Tensor], w: Sequence[torch.Tensor], *, act: str, alpha: float,
+                   gamma: float, op: torch.dtype, split: int = 1):
+    """fp32 master x/eps/W; GEMM operands rounded to ``op`` (the prediction
+    optionally split, see ``pred_matmul``); fp32 accumulate."""
+    L = len(w)
+    e = [x[l] - pred_matmul(w[l], act_forward(act, x[l + 1]), op, split) for l in range(L)]
     new_x = [v.clone() for v in x]
     for l in range(1, L):
         sig = _r(w[l - 1], op).T @ _r(e[l - 1], op)

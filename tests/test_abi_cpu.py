@@ -56,15 +56,15 @@ P = 4096  # a fake, aligned, non-null address; never dereferenced (validation fa
 
 
 @pytest.mark.parametrize("args,code,needle", [
-    ((None, P, P, P, 64, 64, 128, 1, 0, 0, 2, -1, None), nat.ERR_NULL, "x_upper"),
-    ((P, P, P, P, 0, 64, 128, 1, 0, 0, 2, -1, None), nat.ERR_SHAPE, "dimensions"),
-    ((P, P, P, P, 64, 64, 128, 0, 0, 0, 2, -1, None), nat.ERR_SHAPE, "groups"),
-    ((P, P, P, P, 64, 64, 128, 1, 7, 0, 2, -1, None), nat.ERR_DTYPE, "storage"),
-    ((P, P, P, P, 64, 64, 128, 1, 1, 2, 2, -1, None), nat.ERR_DTYPE, "16-bit"),
-    ((P, P, P, P, 64, 64, 128, 1, 0, 0, 9, -1, None), nat.ERR_ACT, "activation"),
-    ((P, P, P, P, 64, 64, 128, 1, 0, 0, 2, 7, None), nat.ERR_CONFIG, "tile"),
-    ((P + 2, P, P, P, 64, 64, 128, 1, 0, 0, 2, -1, None), nat.ERR_ALIGN, "aligned"),
-    ((P, P, P, P, 1 << 20, 1 << 20, 128, 1, 0, 0, 2, -1, None), nat.ERR_SHAPE, "too large"),
+    ((None, P, P, P, 64, 64, 128, 1, 0, 0, 1, 2, -1, None), nat.ERR_NULL, "x_upper"),
+    ((P, P, P, P, 0, 64, 128, 1, 0, 0, 1, 2, -1, None), nat.ERR_SHAPE, "dimensions"),
+    ((P, P, P, P, 64, 64, 128, 0, 0, 0, 1, 2, -1, None), nat.ERR_SHAPE, "groups"),
+    ((P, P, P, P, 64, 64, 128, 1, 7, 0, 1, 2, -1, None), nat.ERR_DTYPE, "storage"),
+    ((P, P, P, P, 64, 64, 128, 1, 1, 2, 1, 2, -1, None), nat.ERR_DTYPE, "16-bit"),
+    ((P, P, P, P, 64, 64, 128, 1, 0, 0, 1, 9, -1, None), nat.ERR_ACT, "activation"),
+    ((P, P, P, P, 64, 64, 128, 1, 0, 0, 1, 2, 7, None), nat.ERR_CONFIG, "tile"),
+    ((P + 2, P, P, P, 64, 64, 128, 1, 0, 0, 1, 2, -1, None), nat.ERR_ALIGN, "aligned"),
+    ((P, P, P, P, 1 << 20, 1 << 20, 128, 1, 0, 0, 1, 2, -1, None), nat.ERR_SHAPE, "too large"),
 ])
 def test_pred_err_validation(args, code, needle):
     assert _lib().ipc_pred_err(*args) == code
@@ -73,7 +73,7 @@ def test_pred_err_validation(args, code, needle):
 
 def test_other_entry_points_validate():
     lib = _lib()
-    assert lib.ipc_forward(P, P, None, 10, 64, 128, 1, 0, 0, 1, -1, None) == nat.ERR_NULL
+    assert lib.ipc_forward(P, P, None, 10, 64, 128, 1, 0, 0, 1, 1, -1, None) == nat.ERR_NULL
     assert lib.ipc_infer_update(P, P, P, None, None, 64, 10, 128, 1, 0.5, 0, 0, 2, -1, None) == nat.ERR_NULL
     assert lib.ipc_infer_update(P, P, P, P, P + 1, 64, 10, 128, 1, 0.5, 0, 0, 2, -1, None) == nat.ERR_ALIGN
     assert lib.ipc_weight_update(P, P, P, 64, 64, -1, 1, 1e-4, 1, 0, 0, 2, -1, None) == nat.ERR_SHAPE
@@ -86,14 +86,14 @@ def test_plan_validation():
     lib = _lib()
     h = ctypes.c_void_p()
     dims = (ctypes.c_int * 4)(10, 64, 64, 784)
-    assert lib.ipc_plan_create(None, 3, dims, 128, 0, 0, 2, 1e-4, 0.5, 1, 0) == nat.ERR_NULL
-    assert lib.ipc_plan_create(ctypes.byref(h), 3, None, 128, 0, 0, 2, 1e-4, 0.5, 1, 0) == nat.ERR_NULL
-    assert lib.ipc_plan_create(ctypes.byref(h), 0, dims, 128, 0, 0, 2, 1e-4, 0.5, 1, 0) == nat.ERR_SHAPE
-    assert lib.ipc_plan_create(ctypes.byref(h), 3, dims, 128, 0, 0, 2, 1e-4, 0.5, 1, 5) == nat.ERR_CONFIG
-    assert lib.ipc_plan_create(ctypes.byref(h), 3, dims, 64, 0, 0, 2, 1e-4, 0.5, 1, 1) == nat.ERR_SHAPE
+    assert lib.ipc_plan_create(None, 3, dims, 128, 0, 0, 1, 2, 1e-4, 0.5, 1, 0) == nat.ERR_NULL
+    assert lib.ipc_plan_create(ctypes.byref(h), 3, None, 128, 0, 0, 1, 2, 1e-4, 0.5, 1, 0) == nat.ERR_NULL
+    assert lib.ipc_plan_create(ctypes.byref(h), 0, dims, 128, 0, 0, 1, 2, 1e-4, 0.5, 1, 0) == nat.ERR_SHAPE
+    assert lib.ipc_plan_create(ctypes.byref(h), 3, dims, 128, 0, 0, 1, 2, 1e-4, 0.5, 1, 5) == nat.ERR_CONFIG
+    assert lib.ipc_plan_create(ctypes.byref(h), 3, dims, 64, 0, 0, 1, 2, 1e-4, 0.5, 1, 1) == nat.ERR_SHAPE
     bad = (ctypes.c_int * 4)(10, 0, 64, 784)
-    assert lib.ipc_plan_create(ctypes.byref(h), 3, bad, 128, 0, 0, 2, 1e-4, 0.5, 1, 0) == nat.ERR_SHAPE
-    assert lib.ipc_plan_create(ctypes.byref(h), 3, dims, 128, 0, 0, 2, 1e-4, 0.5, 1, 0) == nat.IPC_OK
+    assert lib.ipc_plan_create(ctypes.byref(h), 3, bad, 128, 0, 0, 1, 2, 1e-4, 0.5, 1, 0) == nat.ERR_SHAPE
+    assert lib.ipc_plan_create(ctypes.byref(h), 3, dims, 128, 0, 0, 1, 2, 1e-4, 0.5, 1, 0) == nat.IPC_OK
     try:
         # stepping an unbound plan is a state error, not a crash
         assert lib.ipc_plan_step(h, 1, None) == nat.ERR_STATE
@@ -114,7 +114,7 @@ def test_plan_validation():
 
 
 def test_check_maps_codes_to_exceptions():
-    _lib().ipc_pred_err(None, P, P, P, 64, 64, 128, 1, 0, 0, 2, -1, None)
+    _lib().ipc_pred_err(None, P, P, P, 64, 64, 128, 1, 0, 0, 1, 2, -1, None)
     with pytest.raises(ValueError, match="x_upper is NULL"):
         nat.check(nat.ERR_NULL)
     with pytest.raises(nat.IPCNativeError):

@@ -52,6 +52,51 @@ def test_prediction_error(M, K, B, act, op):
         assert rel_err(e, ref) <= 2e-2
 
 
+def _split_model(w, a, op, split):
+    """float64 value of the split 16-bit product (same terms as the kernel)."""
+    def parts(t):
+        hi = t.to(op).double()
+        return hi, (t.double() - hi).to(op).double()
+    wh, wl = parts(w)
+    if split == 2:
+        return wh @ a.to(op).double() + wl @ a.to(op).double()
+    ah, al = parts(a)
+    return wh @ ah + wl @ ah + wh @ al
+
+
+@pytest.mark.parametrize("split", [2, 3])
+@pytest.mark.parametrize("op", ["f16", "bf16"])
+@pytest.mark.parametrize("act", ["tanh", "sigmoid", "relu"])
+@pytest.mark.parametrize("M,K,B", [(10, 64, 128), (64, 784, 128), (37, 53, 19), (200, 300, 256), (1000, 4096, 64)])
+def test_prediction_error_split_operands(M, K, B, act, op, split):
+    report("pred_err_split", M=M, K=K, B=B, act=act, op=op, split=split)
+    xu, w, xl = _pe_inputs(M, K, B, 77 + M + K)
+    e = torch.empty((M, B), device=DEV)
+    build_prediction_error(M, K, B, act, "float32", operand_dtype=OPS[op], split=split)(
+        to_dev(xu), to_dev(w), to_dev(xl), e)
+    out = torch.empty((M, B), device=DEV)
+    build_forward(M, K, B, act, "float32", operand_dtype=OPS[op], split=split)(to_dev(xu), to_dev(w), out)
+    torch.cuda.synchronize()
+    a = O.act_forward(act, xu)
+    prod = _split_model(w, a, OPS[op], split)
+    # split 3 carries f(X) as hi + lo, so a one-ulp difference between device
+    # and host tanh/exp cannot flip a 16-bit rounding; split 2 rounds f(X) once.
+    model_tol = 1e-4 if split == 3 else 1e-3
+    assert rel_err(e, xl.double() - prod) <= model_tol
+    assert rel_err(out, prod) <= model_tol
+    ref = O.pred_err(xu, w, xl, act)
+    # the split must be closer to fp32 than one rounding of each operand
+    bound = 2e-4 if split == 3 else 2e-2
+    assert rel_err(e, ref) <= bound
+    # forward and prediction share the product bit for bit (the wavefront
+    # invariant of the forward initialisation relies on it)
+    e2 = torch.empty((M, B), device=DEV)
+    build_prediction_error(M, K, B, act, "float32", operand_dtype=OPS[op], split=split)(
+        to_dev(xu), to_dev(w), out, e2)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(e2) == 0
+
+
 @pytest.mark.parametrize("op", ["f32", "bf16"])
 @pytest.mark.parametrize("act", ["tanh", "sigmoid"])
 @pytest.mark.parametrize("M,K,B", [(10, 64, 128), (64, 784, 128), (37, 53, 19)])

