@@ -76,7 +76,9 @@ def time_phases(model, reps=50, replays=5):
     from lich_amd import _native as nat
 
     out = {}
-    for phase, name in ((0, "pred"), (1, "infer"), (2, "weight")):
+    phases = ((0, "phaseA_pred+infer"), (2, "phaseB_weight")) if model.fused else \
+        ((0, "pred"), (1, "infer"), (2, "weight"))
+    for phase, name in phases:
         graph = torch.cuda.CUDAGraph()
         nat.check(nat.lib().ipc_plan_phase(model._plan, phase, 2, nat.current_stream_handle()))  # warm
         torch.cuda.synchronize()
@@ -97,6 +99,8 @@ def time_phases(model, reps=50, replays=5):
 
 
 def run_steady(model, x, y, T, warmup_steps, steps):
+    """Replays a hipGraph of T steps; returns (wall seconds, steps done, GPU
+    microseconds per replay from HIP events on the replay stream)."""
     import torch
 
     assert model.prepare_steady_state(x, y, steps=T, use_graph=True)
@@ -104,11 +108,16 @@ def run_steady(model, x, y, T, warmup_steps, steps):
         model._steady_state_runner.replay()
     torch.cuda.synchronize()
     replays = steps // T
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    start.record(stream)
     for _ in range(replays):
         model._steady_state_runner.replay()
+    end.record(stream)
     torch.cuda.synchronize()
-    return time.perf_counter() - t0, replays * T
+    wall = time.perf_counter() - t0
+    return wall, replays * T, start.elapsed_time(end) * 1e3 / replays
 
 
 def cpu_baseline(dims, B, act, threads, warmup=20, steps=200, repeats=5):
@@ -163,25 +172,37 @@ def main() -> int:
     log(f"device {torch.cuda.get_device_name(0)} arch {nat.device_arch(0)}")
 
     model, x, y = make_model(dims, B, "tanh", torch.float16, seed=0)
-    elapsed, done = run_steady(model, x, y, T, warmup, steps)
+    elapsed, done, replay_us = run_steady(model, x, y, T, warmup, steps)
     ms_per_step = elapsed * 1e3 / done
     value = B * done / elapsed
-    log(f"headline: {ms_per_step * 1e3:.2f} us/step, {value:,.0f} samples/s, {model.launches_per_step()} launches/step")
+    log(f"headline: {ms_per_step * 1e3:.2f} us/step, {value:,.0f} samples/s, fused={model.fused}, "
+        f"{model.launches_per_step()} launch(es) per step call, {replay_us:.2f} us per {T}-step replay")
 
+    bf = phase_bytes_flops(dims, B)
+    step_bytes = sum(v[0] for v in bf.values())
+    step_flops = sum(v[1] for v in bf.values())
     # per-phase kernel durations on a fresh model (the timing loops disturb state)
     pmodel, px, py = make_model(dims, B, "tanh", torch.float16, seed=1)
     pmodel.initialize_batch(px, py)
     phase_us = time_phases(pmodel)
-    bf = phase_bytes_flops(dims, B)
-    dom = max(phase_us, key=phase_us.get)
-    dom_bytes, dom_flops = bf[dom]
-    achieved = dom_bytes / (phase_us[dom] * 1e-6) / 1e9
-    phases = {k: {"us": round(v, 3), "GB/s": round(bf[k][0] / (v * 1e-6) / 1e9, 2),
-                  "TFLOP/s": round(bf[k][1] / (v * 1e-6) / 1e12, 4)} for k, v in phase_us.items()}
+    phases = {k: {"us": round(v, 3)} for k, v in phase_us.items()}
     log(f"phases: {phases}")
+    if model.fused:
+        # the dominant (only) kernel is the whole-step kernel: one launch per
+        # T-step replay, so its launch duration is the replay's GPU time
+        launch_us = replay_us
+        kernel = f"whole-step kernel, {T} steps per launch"
+        launch_bytes, launch_flops = T * step_bytes, T * step_flops
+    else:
+        dom = max(phase_us, key=phase_us.get)
+        launch_us = phase_us[dom]
+        kernel = f"{dom} phase"
+        launch_bytes, launch_flops = bf[dom]
+    achieved = launch_bytes / (launch_us * 1e-6) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None, "kernel": f"{dom} phase",
-                "algorithmic_bytes_per_launch": dom_bytes, "avg_launch_us": round(phase_us[dom], 3)}
+                "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None, "kernel": kernel,
+                "algorithmic_bytes_per_launch": launch_bytes, "avg_launch_us": round(launch_us, 3),
+                "achieved_tflops": round(launch_flops / (launch_us * 1e-6) / 1e12, 4)}
     del pmodel
 
     wide = None
@@ -189,7 +210,7 @@ def main() -> int:
         wdims = (1000,) + (4096,) * 4 + (4096,)
         WB = 1024
         wmodel, wx, wy = make_model(wdims, WB, "tanh", torch.bfloat16, seed=0, input_dist="normal")
-        w_elapsed, w_done = run_steady(wmodel, wx, wy, T, 2 * T, 5 * T)
+        w_elapsed, w_done, _w_replay_us = run_steady(wmodel, wx, wy, T, 2 * T, 5 * T)
         w_ms = w_elapsed * 1e3 / w_done
         flops_step = sum(v[1] for v in phase_bytes_flops(wdims, WB).values())
         tflops = flops_step / (w_ms * 1e-3) / 1e12
@@ -222,7 +243,7 @@ def main() -> int:
         "config": {"workload": "paper profile depth 6: dims (10,64x6,784), B=128, tanh, alpha=1e-4, gamma=0.5, "
                                "T=4 steps per hipGraph replay, fp32 master x/eps/W, fp16 operands, fp32 accumulate",
                    "global_batch": B, "seq_len": None, "parallelism": "single GPU",
-                   "launches_per_step": model.launches_per_step(), "phases": phases},
+                   "fused_whole_step_kernel": model.fused, "phases": phases},
         "roofline": roofline, "cpu_baseline": cpu, "wide": wide,
     }
     print(json.dumps(line), flush=True)

@@ -153,15 +153,33 @@ int ipc_weight_update_outer(void* w, const void* e, const void* x_upper, int M, 
  */
 typedef struct ipc_plan ipc_plan;
 
-/* split applies to the prediction phase and the forward initialisation. */
+/* split applies to the prediction phase and the forward initialisation.
+ * fused: IPC_FUSED_AUTO picks the whole-step kernel when the net is narrow
+ * (fp32 storage, every output width d_0..d_{L-1} <= 128, L <= 16);
+ * IPC_FUSED_OFF always uses one multi-layer launch per phase; IPC_FUSED_ON
+ * requires the whole-step kernel (IPC_ERR_CONFIG if the net is not narrow). */
+#define IPC_FUSED_AUTO (-1)
+#define IPC_FUSED_OFF 0
+#define IPC_FUSED_ON 1
 int ipc_plan_create(ipc_plan** out, int L, const int* dims, int B,
                     int storage, int operand, int split, int act, float alpha, float gamma,
-                    int recompute, int weight_mode);
+                    int recompute, int weight_mode, int fused);
+
+/* 1 if the plan runs the whole-step kernel, 0 otherwise. */
+int ipc_plan_fused(const ipc_plan* plan);
+
+/* Bytes of zero-initialised device workspace ipc_plan_bind needs (0 when not
+ * fused).  The whole-step kernel keeps its grid-barrier counters there and
+ * leaves them zero after every launch; word 2 becomes non-zero if a barrier
+ * wait ever ran past its spin limit. */
+int ipc_plan_workspace_bytes(const ipc_plan* plan);
 
 /* Binds the caller's buffers: x and e hold L+1 pointers ([d_l, B] each; e[L]
  * is unused and may be NULL), w holds L pointers ([d_l, d_{l+1}]), a holds
- * L+1 pointers for save-activation mode (recompute == 0) or is NULL. */
-int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w, void* const* a);
+ * L+1 pointers for save-activation mode (recompute == 0) or is NULL;
+ * workspace as above (may be NULL when ipc_plan_workspace_bytes is 0). */
+int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w, void* const* a,
+                  void* workspace);
 
 /* Enqueues `steps` iPC steps on `stream`. */
 int ipc_plan_step(ipc_plan* plan, int steps, void* stream);
@@ -174,7 +192,8 @@ int ipc_plan_forward_init(ipc_plan* plan, void* stream);
 /* Enqueues only one phase of the step `reps` times (0 = prediction+error,
  * 1 = inference update, 2 = weight update), so that each phase's kernel can
  * be timed on its own.  Mirrors the per-kernel timing of the reference's
- * harnesses (scripts/autotune.py:200-215). */
+ * harnesses (scripts/autotune.py:200-215).  A fused plan runs prediction and
+ * inference in one phase: phase 0 launches both and phase 1 launches nothing. */
 #define IPC_PHASE_PRED 0
 #define IPC_PHASE_INFER 1
 #define IPC_PHASE_WEIGHT 2

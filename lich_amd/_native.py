@@ -26,6 +26,7 @@ TILE_AUTO = -1
 TILE_COUNT = 3
 WMODE = {"gemm": 0, "outer": 1, "auto": 2}
 SPLIT_NONE, SPLIT_W, SPLIT_WX = 1, 2, 3
+FUSED = {"auto": -1, "off": 0, "on": 1}
 
 _DTYPE_CODES = {torch.float32: DT_F32, torch.float16: DT_F16, torch.bfloat16: DT_BF16}
 
@@ -69,8 +70,10 @@ def _declare(lib):
         "ipc_infer_update": ([vp, vp, vp, vp, vp, i, i, i, i, f, i, i, i, i, vp], i),
         "ipc_weight_update": ([vp, vp, vp, i, i, i, i, f, i, i, i, i, i, vp], i),
         "ipc_weight_update_outer": ([vp, vp, vp, i, i, i, i, f, i, i, i, vp], i),
-        "ipc_plan_create": ([POINTER(vp), i, POINTER(c_int), i, i, i, i, i, f, f, i, i], i),
-        "ipc_plan_bind": ([vp, POINTER(vp), POINTER(vp), POINTER(vp), POINTER(vp)], i),
+        "ipc_plan_create": ([POINTER(vp), i, POINTER(c_int), i, i, i, i, i, f, f, i, i, i], i),
+        "ipc_plan_fused": ([vp], i),
+        "ipc_plan_workspace_bytes": ([vp], i),
+        "ipc_plan_bind": ([vp, POINTER(vp), POINTER(vp), POINTER(vp), POINTER(vp), vp], i),
         "ipc_plan_step": ([vp, i, vp], i),
         "ipc_plan_forward_init": ([vp, vp], i),
         "ipc_plan_phase": ([vp, i, i, vp], i),

@@ -17,6 +17,7 @@
 
 #include "../../include/ipc_hip.h"
 #include "ipc_launch.h"
+#include "ipc_narrow.h"
 
 using namespace ipc;
 
@@ -304,12 +305,40 @@ struct ipc_plan {
   const void* act_src = nullptr;  // x[L]
   void* act_dst = nullptr;        // a[L] in save mode
   int launches = 0;
+  // whole-step kernel for narrow nets
+  bool narrow = false;
+  NarrowArgs nargs{};
 };
+
+namespace {
+
+constexpr int kNarrowWorkspaceBytes = 64;
+constexpr int kNarrowSpinLimit = 1 << 22;
+
+bool narrow_eligible(int L, const int* dims, int storage, int operand, int split) {
+  if (storage != IPC_DT_F32 || L > NARROW_MAX_L) return false;
+  for (int l = 0; l < L; ++l)
+    if (dims[l] > NARROW_MAX_WIDTH) return false;
+  // one column block's states, errors and staged activations must fit in LDS
+  return narrow_lds_bytes(dims, L, operand, split) <= NARROW_LDS_LIMIT - 1024;
+}
+
+int launch_narrow_mode(ipc_plan* plan, int mode, int steps, hipStream_t s) {
+  NarrowArgs a = plan->nargs;
+  a.mode = mode;
+  a.steps = steps;
+  if (mode == NMODE_PHASE_A || mode == NMODE_FORWARD) a.nblocks = (plan->B + NARROW_NC - 1) / NARROW_NC;
+  if (mode == NMODE_PHASE_B) a.nblocks = a.wtile_start[plan->L];
+  if (a.nblocks > 256) a.nblocks = 256;
+  return launch_rc(launch_narrow(a, plan->operand, plan->split, s), "whole-step kernel");
+}
+
+}  // namespace
 
 extern "C" {
 
 int ipc_plan_create(ipc_plan** out, int L, const int* dims, int B, int storage, int operand, int split, int act,
-                    float alpha, float gamma, int recompute, int weight_mode) {
+                    float alpha, float gamma, int recompute, int weight_mode, int fused) {
   if (!out) return fail(IPC_ERR_NULL, "out is NULL");
   *out = nullptr;
   if (!dims) return fail(IPC_ERR_NULL, "dims is NULL");
@@ -322,6 +351,12 @@ int ipc_plan_create(ipc_plan** out, int L, const int* dims, int B, int storage, 
   for (int l = 0; l < L; ++l) TRY(check_dims(dims[l], dims[l + 1], B, 1));
   if (weight_mode == IPC_WMODE_OUTER && B > kOuterMaxB)
     return fail(IPC_ERR_SHAPE, "outer weight mode supports B <= %d (got %d)", kOuterMaxB, B);
+  if (fused < IPC_FUSED_AUTO || fused > IPC_FUSED_ON) return fail(IPC_ERR_CONFIG, "unknown fused option %d", fused);
+  const bool eligible = narrow_eligible(L, dims, storage, operand, effective_split(storage, operand, split));
+  if (fused == IPC_FUSED_ON && !eligible)
+    return fail(IPC_ERR_CONFIG,
+                "the whole-step kernel needs fp32 storage, L <= %d, widths d_0..d_{L-1} <= %d and a column "
+                "block that fits in LDS", NARROW_MAX_L, NARROW_MAX_WIDTH);
   ipc_plan* p = new (std::nothrow) ipc_plan();
   if (!p) return fail(IPC_ERR_CONFIG, "out of host memory");
   p->L = L; p->B = B; p->storage = storage; p->operand = operand; p->act = act;
@@ -329,12 +364,19 @@ int ipc_plan_create(ipc_plan** out, int L, const int* dims, int B, int storage, 
   p->alpha = alpha; p->gamma = gamma; p->recompute = recompute ? 1 : 0;
   p->wmode = weight_mode;
   p->dims.assign(dims, dims + L + 1);
+  p->narrow = eligible && fused != IPC_FUSED_OFF;
   *out = p;
   return ok();
 }
 
-int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w, void* const* a) {
+int ipc_plan_fused(const ipc_plan* plan) { return plan && plan->narrow ? 1 : 0; }
+
+int ipc_plan_workspace_bytes(const ipc_plan* plan) { return plan && plan->narrow ? kNarrowWorkspaceBytes : 0; }
+
+int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w, void* const* a,
+                  void* workspace) {
   if (!plan) return fail(IPC_ERR_NULL, "plan is NULL");
+  if (plan->narrow) TRY(check_ptr(workspace, "workspace", 4));
   if (!x || !e || !w) return fail(IPC_ERR_NULL, "x, e and w pointer arrays are required");
   if (!plan->recompute && !a) return fail(IPC_ERR_NULL, "save-activation plan needs the a[] array");
   const int L = plan->L, B = plan->B, es = elem_size(plan->storage);
@@ -384,6 +426,44 @@ int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w
   plan->tile_infer = rows_i ? pick_tile(rows_i, B, 1) : 0;
   plan->tile_weight = rows_w ? pick_tile(rows_w, cols_w, 1) : 0;
   plan->launches = 1 + (plan->infer.empty() ? 0 : 1) + (plan->weight.empty() ? 0 : 1) + (int)plan->outer.size();
+  if (plan->narrow) {
+    NarrowArgs& na = plan->nargs;
+    na = NarrowArgs{};
+    na.L = L; na.B = B; na.act = plan->act;
+    na.alpha = plan->alpha; na.gamma = plan->gamma;
+    na.spin_limit = kNarrowSpinLimit;
+    na.outer = (B <= NARROW_OUTER_MAX_B) &&
+               (plan->wmode == IPC_WMODE_OUTER || (plan->wmode == IPC_WMODE_AUTO && B <= 16));
+    int tiles = 0;
+    for (int l = 0; l <= L; ++l) {
+      na.dims[l] = d[l];
+      na.x[l] = static_cast<float*>(x[l]);
+      na.e[l] = l < L ? static_cast<float*>(e[l]) : nullptr;
+      na.a[l] = (!plan->recompute && l >= 1) ? static_cast<float*>(a[l]) : nullptr;
+      if (l < L) na.w[l] = static_cast<float*>(w[l]);
+      na.wtile_start[l] = tiles;
+      if (l < L) tiles += narrow_tiles(&d[l], 1);
+    }
+    // prediction/inference units (layer, 16-row tile), the longest contraction first
+    std::vector<std::pair<int, int>> units;
+    for (int l = 0; l < L; ++l)
+      for (int rt = 0; rt * 16 < d[l]; ++rt) units.push_back({l, rt});
+    std::stable_sort(units.begin(), units.end(),
+                     [&](const std::pair<int, int>& u, const std::pair<int, int>& v) {
+                       return d[u.first + 1] > d[v.first + 1];
+                     });
+    na.n_units = (int)units.size();
+    for (int i = 0; i < na.n_units; ++i) {
+      na.unit_l[i] = (unsigned char)units[i].first;
+      na.unit_rt[i] = (unsigned char)units[i].second;
+    }
+    na.lds_bytes = narrow_lds_bytes(d.data(), L, plan->operand, plan->split);
+    const int ncb = (B + NARROW_NC - 1) / NARROW_NC;
+    na.nblocks = std::min(256, std::max(ncb, tiles));
+    na.bar = static_cast<unsigned*>(workspace);
+    TRY(launch_rc(narrow_prepare(plan->operand, plan->split, na.lds_bytes), "whole-step kernel LDS limit"));
+    plan->launches = 1;
+  }
   plan->bound = true;
   return ok();
 }
@@ -419,6 +499,7 @@ int ipc_plan_step(ipc_plan* plan, int steps, void* stream) {
   if (!plan->bound) return fail(IPC_ERR_STATE, "plan has no bound buffers");
   if (steps < 0) return fail(IPC_ERR_SHAPE, "steps must be >= 0");
   hipStream_t s = (hipStream_t)stream;
+  if (plan->narrow) return steps > 0 ? launch_narrow_mode(plan, NMODE_STEPS, steps, s) : ok();
   for (int t = 0; t < steps; ++t)
     for (int phase = IPC_PHASE_PRED; phase <= IPC_PHASE_WEIGHT; ++phase) TRY(run_phase(plan, phase, s));
   return ok();
@@ -429,6 +510,12 @@ int ipc_plan_phase(ipc_plan* plan, int phase, int reps, void* stream) {
   if (!plan->bound) return fail(IPC_ERR_STATE, "plan has no bound buffers");
   if (phase < IPC_PHASE_PRED || phase > IPC_PHASE_WEIGHT) return fail(IPC_ERR_CONFIG, "unknown phase %d", phase);
   if (reps < 0) return fail(IPC_ERR_SHAPE, "reps must be >= 0");
+  if (plan->narrow) {
+    if (phase == IPC_PHASE_INFER) return ok();
+    const int mode = phase == IPC_PHASE_PRED ? NMODE_PHASE_A : NMODE_PHASE_B;
+    for (int r = 0; r < reps; ++r) TRY(launch_narrow_mode(plan, mode, 1, (hipStream_t)stream));
+    return ok();
+  }
   for (int r = 0; r < reps; ++r) TRY(run_phase(plan, phase, (hipStream_t)stream));
   return ok();
 }
@@ -437,6 +524,7 @@ int ipc_plan_forward_init(ipc_plan* plan, void* stream) {
   if (!plan) return fail(IPC_ERR_NULL, "plan is NULL");
   if (!plan->bound) return fail(IPC_ERR_STATE, "plan has no bound buffers");
   hipStream_t s = (hipStream_t)stream;
+  if (plan->narrow) return launch_narrow_mode(plan, NMODE_FORWARD, 1, s);
   if (plan->act_dst) {
     const long long n = (long long)plan->dims[plan->L] * plan->B;
     TRY(launch_rc(launch_act(plan->act_src, plan->act_dst, n, plan->act, plan->storage, s), "plan a[L] = f(x[L])"));

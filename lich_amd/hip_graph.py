@@ -2,9 +2,8 @@
 
 Mirrors ``IPCGraphRunner`` (``src/ipc_tilelang/cuda_graph.py:6-36``).  On
 ROCm ``torch.cuda.CUDAGraph`` records a hipGraph: the plan's launches read
-torch's current stream at call time, so ``steps`` calls of
-``step_initialized`` land on the capture stream and replay as one graph
-launch.  Buffer addresses stay fixed because the model reuses its buffers for
+torch's current stream at call time, so the ``steps`` steps land on the
+capture stream and replay as one graph launch.  Buffer addresses stay fixed because the model reuses its buffers for
 every batch of the same shape.
 """
 from __future__ import annotations
@@ -27,8 +26,9 @@ class IPCGraphRunner:
         torch.cuda.synchronize()
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
-            for _ in range(self.steps):
-                self.model.step_initialized(collect_metrics=False)
+            # the same `steps` steps as a loop of step_initialized calls, enqueued
+            # by one library call (the whole-step kernel runs them in one launch)
+            self.model.run_steps(self.steps)
         torch.cuda.synchronize()
         self._captured = True
 

@@ -65,6 +65,8 @@ class IPCConfig:
     # picks 3 for narrow nets (every width <= 1024, latency-bound, the extra
     # MFMAs are free) and 2 otherwise.
     pred_split: int | None = None
+    # Whole-step kernel for narrow nets: "auto" (when eligible), "on", "off".
+    fused: str = "auto"
 
 
 def init_weights_cpu(dims: Sequence[int], *, seed: int, init: str) -> list[torch.Tensor]:
@@ -131,6 +133,10 @@ class HipIPC:
         if mode not in nat.WMODE:
             raise ValueError(f"Unknown weight_update_mode {cfg.weight_update_mode!r}")
         self._wmode = nat.WMODE[mode]
+        if str(cfg.fused).lower() not in nat.FUSED:
+            raise ValueError(f"Unknown fused option {cfg.fused!r}")
+        self._fused = nat.FUSED[str(cfg.fused).lower()]
+        self._workspace: torch.Tensor | None = None
         if weights is None:
             weights = init_weights_cpu(cfg.dims, seed=seed, init=cfg.init)
         if len(weights) != len(cfg.dims) - 1:
@@ -177,10 +183,15 @@ class HipIPC:
         handle = ctypes.c_void_p()
         nat.check(nat.lib().ipc_plan_create(
             ctypes.byref(handle), self.L, dims, int(B), self._storage, self._operand, self.pred_split, self._act,
-            float(self.cfg.alpha), float(self.cfg.gamma), int(self.recompute_activation), self._wmode))
+            float(self.cfg.alpha), float(self.cfg.gamma), int(self.recompute_activation), self._wmode,
+            self._fused))
         self._plan = handle
+        nbytes = int(nat.lib().ipc_plan_workspace_bytes(handle))
+        self._workspace = (torch.zeros(((nbytes + 3) // 4,), dtype=torch.int32, device=self.device)
+                           if nbytes else None)
         a = None if self.a is None else _ptr_array(self.a)
-        nat.check(nat.lib().ipc_plan_bind(handle, _ptr_array(self.x), _ptr_array(self.e), _ptr_array(self.w), a))
+        ws = None if self._workspace is None else self._workspace.data_ptr()
+        nat.check(nat.lib().ipc_plan_bind(handle, _ptr_array(self.x), _ptr_array(self.e), _ptr_array(self.w), a, ws))
         self._plan_key = (int(B), tuple(t.data_ptr() for t in self.w))
 
     def runtime_plan_ready(self) -> bool:
@@ -188,6 +199,18 @@ class HipIPC:
 
     def launches_per_step(self) -> int:
         return int(nat.lib().ipc_plan_launch_count(self._plan)) if self._plan is not None else 0
+
+    @property
+    def fused(self) -> bool:
+        """True when the step runs as the whole-step kernel."""
+        return self._plan is not None and bool(nat.lib().ipc_plan_fused(self._plan))
+
+    def barrier_timeouts(self) -> int:
+        """Non-zero if a grid-barrier wait of the whole-step kernel ever hit its
+        spin limit (synchronises the device)."""
+        if self._workspace is None:
+            return 0
+        return int(self._workspace[2].item())
 
     # ------------------------------------------------------------------ batch
     def initialize_batch(self, x_input: torch.Tensor, y_target: torch.Tensor) -> None:

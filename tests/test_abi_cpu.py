@@ -86,29 +86,53 @@ def test_plan_validation():
     lib = _lib()
     h = ctypes.c_void_p()
     dims = (ctypes.c_int * 4)(10, 64, 64, 784)
-    assert lib.ipc_plan_create(None, 3, dims, 128, 0, 0, 1, 2, 1e-4, 0.5, 1, 0) == nat.ERR_NULL
-    assert lib.ipc_plan_create(ctypes.byref(h), 3, None, 128, 0, 0, 1, 2, 1e-4, 0.5, 1, 0) == nat.ERR_NULL
-    assert lib.ipc_plan_create(ctypes.byref(h), 0, dims, 128, 0, 0, 1, 2, 1e-4, 0.5, 1, 0) == nat.ERR_SHAPE
-    assert lib.ipc_plan_create(ctypes.byref(h), 3, dims, 128, 0, 0, 1, 2, 1e-4, 0.5, 1, 5) == nat.ERR_CONFIG
-    assert lib.ipc_plan_create(ctypes.byref(h), 3, dims, 64, 0, 0, 1, 2, 1e-4, 0.5, 1, 1) == nat.ERR_SHAPE
+    assert lib.ipc_plan_create(None, 3, dims, 128, 0, 0, 1, 2, 1e-4, 0.5, 1, 0, -1) == nat.ERR_NULL
+    assert lib.ipc_plan_create(ctypes.byref(h), 3, None, 128, 0, 0, 1, 2, 1e-4, 0.5, 1, 0, -1) == nat.ERR_NULL
+    assert lib.ipc_plan_create(ctypes.byref(h), 0, dims, 128, 0, 0, 1, 2, 1e-4, 0.5, 1, 0, -1) == nat.ERR_SHAPE
+    assert lib.ipc_plan_create(ctypes.byref(h), 3, dims, 128, 0, 0, 1, 2, 1e-4, 0.5, 1, 5, -1) == nat.ERR_CONFIG
+    assert lib.ipc_plan_create(ctypes.byref(h), 3, dims, 64, 0, 0, 1, 2, 1e-4, 0.5, 1, 1, -1) == nat.ERR_SHAPE
     bad = (ctypes.c_int * 4)(10, 0, 64, 784)
-    assert lib.ipc_plan_create(ctypes.byref(h), 3, bad, 128, 0, 0, 1, 2, 1e-4, 0.5, 1, 0) == nat.ERR_SHAPE
-    assert lib.ipc_plan_create(ctypes.byref(h), 3, dims, 128, 0, 0, 1, 2, 1e-4, 0.5, 1, 0) == nat.IPC_OK
+    assert lib.ipc_plan_create(ctypes.byref(h), 3, bad, 128, 0, 0, 1, 2, 1e-4, 0.5, 1, 0, -1) == nat.ERR_SHAPE
+    assert lib.ipc_plan_create(ctypes.byref(h), 3, dims, 128, 0, 0, 1, 2, 1e-4, 0.5, 1, 0, -1) == nat.IPC_OK
     try:
         # stepping an unbound plan is a state error, not a crash
         assert lib.ipc_plan_step(h, 1, None) == nat.ERR_STATE
         assert lib.ipc_plan_forward_init(h, None) == nat.ERR_STATE
         assert lib.ipc_plan_launch_count(h) == 0
         arr = (ctypes.c_void_p * 4)(P, P, P, P)
-        assert lib.ipc_plan_bind(h, None, arr, arr, None) == nat.ERR_NULL
+        assert lib.ipc_plan_bind(h, None, arr, arr, None, P) == nat.ERR_NULL
         arr_bad = (ctypes.c_void_p * 4)(P, None, P, P)
-        assert lib.ipc_plan_bind(h, arr_bad, arr, arr, None) == nat.ERR_NULL
+        assert lib.ipc_plan_bind(h, arr_bad, arr, arr, None, P) == nat.ERR_NULL
         assert "x[1]" in nat.last_error()
-        # binding fake (never dereferenced) addresses succeeds and prepares 3 launches/step
-        assert lib.ipc_plan_bind(h, arr, arr, arr, None) == nat.IPC_OK
+        # a narrow fp32 net runs the whole-step kernel, which needs a workspace
+        assert lib.ipc_plan_fused(h) == 1 and lib.ipc_plan_workspace_bytes(h) > 0
+        assert lib.ipc_plan_bind(h, arr, arr, arr, None, None) == nat.ERR_NULL
+        assert "workspace" in nat.last_error()
+        # binding validates every pointer first; a fused plan then raises the
+        # kernel's dynamic-LDS limit, the one HIP call of bind (fails without a GPU)
+        rc = lib.ipc_plan_bind(h, arr, arr, arr, None, P)
+        assert rc == (nat.IPC_OK if torch.cuda.is_available() else nat.ERR_LAUNCH)
+        if rc == nat.IPC_OK:
+            assert lib.ipc_plan_launch_count(h) == 1
+    finally:
+        lib.ipc_plan_destroy(h)
+    # fused off: one multi-layer launch per phase, no workspace
+    assert lib.ipc_plan_create(ctypes.byref(h), 3, dims, 128, 0, 0, 1, 2, 1e-4, 0.5, 1, 0, 0) == nat.IPC_OK
+    try:
+        assert lib.ipc_plan_fused(h) == 0 and lib.ipc_plan_workspace_bytes(h) == 0
+        arr = (ctypes.c_void_p * 4)(P, P, P, P)
+        assert lib.ipc_plan_bind(h, arr, arr, arr, None, None) == nat.IPC_OK
         assert lib.ipc_plan_launch_count(h) == 3
     finally:
         lib.ipc_plan_destroy(h)
+    # forcing the whole-step kernel on a wide net is a configuration error
+    wide = (ctypes.c_int * 3)(1000, 4096, 4096)
+    assert lib.ipc_plan_create(ctypes.byref(h), 2, wide, 1024, 0, 2, 2, 2, 1e-4, 0.5, 1, 0, 1) == nat.ERR_CONFIG
+    assert lib.ipc_plan_create(ctypes.byref(h), 2, wide, 1024, 0, 2, 2, 2, 1e-4, 0.5, 1, 0, -1) == nat.IPC_OK
+    assert lib.ipc_plan_fused(h) == 0
+    lib.ipc_plan_destroy(h)
+    # 16-bit storage never takes the whole-step kernel
+    assert lib.ipc_plan_create(ctypes.byref(h), 3, dims, 128, 1, 1, 1, 2, 1e-4, 0.5, 1, 0, 1) == nat.ERR_CONFIG
     assert lib.ipc_plan_step(None, 1, None) == nat.ERR_NULL
     lib.ipc_plan_destroy(None)  # no-op
 

@@ -50,13 +50,15 @@ def _errors(model, w0, x_t, w_t):
     return s_err, O.global_rel_err(dw_gpu, dw_ref)
 
 
-def test_c1_cpu_plumbing_config_fp32():
+@pytest.mark.parametrize("fused", ["on", "off"])
+def test_c1_cpu_plumbing_config_fp32(fused):
     """dims (10,64,64,64,784), B=128, tanh, T=4, fp32."""
     dims, B, T = (10, 64, 64, 64, 784), 128, 4
-    report("c1", dims=dims, B=B, T=T)
+    report("c1", dims=dims, B=B, T=T, fused=fused)
     w0, x_in, y = _setup(dims, B)
     x0, x_t, w_t, e_t = _oracle_run(w0, x_in, y, "tanh", T)
-    model, x_init = _gpu_run(dims, w0, x_in, y, "tanh", T, torch.float32)
+    model, x_init = _gpu_run(dims, w0, x_in, y, "tanh", T, torch.float32, fused=fused)
+    assert model.fused == (fused == "on")
     assert O.global_rel_err(x_init[1:-1], x0[1:-1]) <= 1e-5
     s_err, dw_err = _errors(model, w0, x_t, w_t)
     print(f"c1 fp32: state_err={s_err:.3e} dW_err={dw_err:.3e}")
@@ -124,9 +126,10 @@ def test_c2_relu_fp16_operands(depth, seed):
     assert dw_err <= 5e-3 and frac <= 0.01
 
 
+@pytest.mark.parametrize("fused", ["auto", "off"])
 @pytest.mark.parametrize("mode", ["outer", "gemm"])
 @pytest.mark.parametrize("B", [1, 4, 8])
-def test_c3_small_batch_fp32(B, mode):
+def test_c3_small_batch_fp32(B, mode, fused):
     """(10, 64^4, 784), B in {1,4,8}, fp32, T=8; rank-B outer-product weight update.
 
     States and weights meet 1e-5 against the fp32 oracle.  The weight *delta*
@@ -139,7 +142,7 @@ def test_c3_small_batch_fp32(B, mode):
     report("c3", B=B, mode=mode)
     w0, x_in, y = _setup(dims, B, seed=B)
     _x0, x_t, w_t, _e = _oracle_run(w0, x_in, y, "tanh", T)
-    model, _ = _gpu_run(dims, w0, x_in, y, "tanh", T, torch.float32, weight_update_mode=mode)
+    model, _ = _gpu_run(dims, w0, x_in, y, "tanh", T, torch.float32, weight_update_mode=mode, fused=fused)
     s_err, dw_err = _errors(model, w0, x_t, w_t)
     w_err = O.global_rel_err(model.w, w_t)
     # float64 truth
@@ -259,3 +262,41 @@ def test_reinitialize_with_new_batch_size_rebuilds_buffers():
     torch.cuda.synchronize()
     with pytest.raises(ValueError):
         m.initialize_batch(torch.zeros(783, 4, device=DEV), torch.zeros(10, 4, device=DEV))
+
+
+@pytest.mark.parametrize("B", [128, 40, 4])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_fused_multi_step_launch_equals_phase_launches(dtype, B):
+    """T steps inside one launch (grid barriers between the phases) give the
+    same bits as launching phase A and phase B separately, step by step: the
+    barrier orders every write of one phase before every read of the next."""
+    from lich_amd import _native as nat
+    dims, T = (10,) + (64,) * 6 + (784,), 6
+    report("fused-barrier", dtype=dtype, B=B)
+    w0, x_in, y = _setup(dims, B, seed=21)
+    models = []
+    for _ in range(2):
+        m = HipIPC(IPCConfig(dims=dims, activation="tanh", dtype=dtype, fused="on"), device=DEV, weights=w0)
+        m.initialize_batch(x_in.to(DEV), y.to(DEV))
+        models.append(m)
+    models[0].run_steps(T)
+    stream = nat.current_stream_handle(DEV)
+    for _ in range(T):
+        nat.check(nat.lib().ipc_plan_phase(models[1]._plan, 0, 1, stream))
+        nat.check(nat.lib().ipc_plan_phase(models[1]._plan, 2, 1, stream))
+    torch.cuda.synchronize()
+    assert models[0].barrier_timeouts() == 0
+    for a, b in zip(models[0].w + models[0].x + models[0].e[:-1], models[1].w + models[1].x + models[1].e[:-1]):
+        assert torch.equal(a, b)
+
+
+def test_fused_and_unfused_paths_agree():
+    dims, B, T = (10,) + (64,) * 4 + (784,), 96, 4
+    w0, x_in, y = _setup(dims, B, seed=22)
+    res = []
+    for fused in ("on", "off"):
+        m, _ = _gpu_run(dims, w0, x_in, y, "sigmoid", T, torch.float32, fused=fused)
+        res.append(m)
+    assert O.global_rel_err(res[0].x[1:-1], res[1].x[1:-1]) <= 1e-5
+    assert O.global_rel_err([w.cpu() - w00 for w, w00 in zip(res[0].w, w0)],
+                            [w.cpu() - w00 for w, w00 in zip(res[1].w, w0)]) <= 1e-4
