@@ -155,7 +155,8 @@ typedef struct ipc_plan ipc_plan;
 
 /* split applies to the prediction phase and the forward initialisation.
  * fused: IPC_FUSED_AUTO picks the whole-step kernel when the net is narrow
- * (fp32 storage, every output width d_0..d_{L-1} <= 128, L <= 16);
+ * (fp32 storage, every output width d_0..d_{L-1} <= 128, L <= 16, split 1 or 3,
+ * one column block's buffers fit in LDS);
  * IPC_FUSED_OFF always uses one multi-layer launch per phase; IPC_FUSED_ON
  * requires the whole-step kernel (IPC_ERR_CONFIG if the net is not narrow). */
 #define IPC_FUSED_AUTO (-1)
@@ -169,9 +170,10 @@ int ipc_plan_create(ipc_plan** out, int L, const int* dims, int B,
 int ipc_plan_fused(const ipc_plan* plan);
 
 /* Bytes of zero-initialised device workspace ipc_plan_bind needs (0 when not
- * fused).  The whole-step kernel keeps its grid-barrier counters there and
- * leaves them zero after every launch; word 2 becomes non-zero if a barrier
- * wait ever ran past its spin limit. */
+ * fused).  The whole-step kernel keeps its grid-barrier counters in the first
+ * 256 bytes and leaves them zero after every launch (word 2 becomes non-zero
+ * if a barrier wait ever ran past its spin limit); in recompute mode the rest
+ * holds the f(x[l]) values phase A evaluates for the weight update. */
 int ipc_plan_workspace_bytes(const ipc_plan* plan);
 
 /* Binds the caller's buffers: x and e hold L+1 pointers ([d_l, B] each; e[L]

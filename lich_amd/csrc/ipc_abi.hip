@@ -312,11 +312,11 @@ struct ipc_plan {
 
 namespace {
 
-constexpr int kNarrowWorkspaceBytes = 64;
 constexpr int kNarrowSpinLimit = 1 << 22;
 
 bool narrow_eligible(int L, const int* dims, int storage, int operand, int split) {
   if (storage != IPC_DT_F32 || L > NARROW_MAX_L) return false;
+  if (split == IPC_SPLIT_W) return false;  // the whole-step kernel carries split 1 or 3
   for (int l = 0; l < L; ++l)
     if (dims[l] > NARROW_MAX_WIDTH) return false;
   // one column block's states, errors and staged activations must fit in LDS
@@ -371,7 +371,11 @@ int ipc_plan_create(ipc_plan** out, int L, const int* dims, int B, int storage, 
 
 int ipc_plan_fused(const ipc_plan* plan) { return plan && plan->narrow ? 1 : 0; }
 
-int ipc_plan_workspace_bytes(const ipc_plan* plan) { return plan && plan->narrow ? kNarrowWorkspaceBytes : 0; }
+int ipc_plan_workspace_bytes(const ipc_plan* plan) {
+  if (!plan || !plan->narrow) return 0;
+  const long long b = narrow_workspace_bytes(plan->dims.data(), plan->L, plan->B, plan->recompute != 0);
+  return b > (1LL << 30) ? -1 : (int)b;
+}
 
 int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w, void* const* a,
                   void* workspace) {
@@ -440,6 +444,7 @@ int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w
       na.x[l] = static_cast<float*>(x[l]);
       na.e[l] = l < L ? static_cast<float*>(e[l]) : nullptr;
       na.a[l] = (!plan->recompute && l >= 1) ? static_cast<float*>(a[l]) : nullptr;
+      na.fx[l] = na.a[l];
       if (l < L) na.w[l] = static_cast<float*>(w[l]);
       na.wtile_start[l] = tiles;
       if (l < L) tiles += narrow_tiles(&d[l], 1);
@@ -461,7 +466,15 @@ int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w
     const int ncb = (B + NARROW_NC - 1) / NARROW_NC;
     na.nblocks = std::min(256, std::max(ncb, tiles));
     na.bar = static_cast<unsigned*>(workspace);
-    TRY(launch_rc(narrow_prepare(plan->operand, plan->split, na.lds_bytes), "whole-step kernel LDS limit"));
+    if (plan->recompute) {
+      // pre-evaluated f(x[l]) buffers follow the barrier counters in the workspace
+      char* ws = static_cast<char*>(workspace) + 256;
+      for (int l = 1; l <= L; ++l) {
+        na.fx[l] = reinterpret_cast<float*>(ws);
+        ws += ((long long)d[l] * B * 4 + 255) / 256 * 256;
+      }
+    }
+    TRY(launch_rc(narrow_prepare(plan->operand, plan->split, plan->act, na.lds_bytes), "whole-step kernel LDS limit"));
     plan->launches = 1;
   }
   plan->bound = true;

@@ -88,6 +88,35 @@ __device__ __forceinline__ float act_df(int act, float x) {
   }
 }
 
+// Compile-time forms of the same activations, for kernels instantiated per
+// activation (no switch in their inner loops).
+template <int ACT> __device__ __forceinline__ float act_t(float x) {
+  if (ACT == ACT_RELU) return x > 0.0f ? x : 0.0f;
+  if (ACT == ACT_TANH) return tanhf(x);
+  if (ACT == ACT_SIGMOID) return sigmoidf_(x);
+  if (ACT == ACT_SILU) return x * sigmoidf_(x);
+  if (ACT == ACT_GELU) {
+    const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+    return 0.5f * x * (1.0f + tanhf(u));
+  }
+  return x;
+}
+
+template <int ACT> __device__ __forceinline__ float dact_t(float x) {
+  if (ACT == ACT_RELU) return x > 0.0f ? 1.0f : 0.0f;
+  if (ACT == ACT_TANH) { const float y = tanhf(x); return 1.0f - y * y; }
+  if (ACT == ACT_SIGMOID) { const float y = sigmoidf_(x); return y * (1.0f - y); }
+  if (ACT == ACT_SILU) { const float s = sigmoidf_(x); return s * (1.0f + x * (1.0f - s)); }
+  if (ACT == ACT_GELU) {
+    const float c = 0.044715f, k = 0.7978845608028654f;
+    const float u = k * (x + c * x * x * x);
+    const float t = tanhf(u);
+    const float du = k * (1.0f + 3.0f * c * x * x);
+    return 0.5f * (1.0f + t) + 0.5f * x * (1.0f - t * t) * du;
+  }
+  return 1.0f;
+}
+
 // ---------------------------------------------------------------- MFMA
 // 32x32 output block per wave.  Operand lane layout (both operands): lane l
 // supplies row/column (l % 32) and the k-slice (l / 32) of the instruction's

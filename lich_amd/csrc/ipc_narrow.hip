@@ -8,18 +8,22 @@
 // round trips as the math allows:
 //
 //   phase A (column-parallel, one workgroup per 16 batch columns):
-//     1. stage, in one round trip, every layer's x[l] (fp32) and f(x[l])
-//        (operand type, [column][k]) for the block's columns into LDS;
+//     1. stage every layer's x[l] (fp32) and f(x[l]) (operand type,
+//        [column][k]) for the block's columns into LDS;
 //     2. every prediction unit (layer, 16-row tile) at once - they are
-//        mutually independent - eps = x[l] - W[l] f(x[l+1]), W rows streaming
-//        from L2 straight into MFMA 16x16 operand registers;
+//        mutually independent - eps = x[l] - W[l] f(x[l+1]); W rows are
+//        prefetched a chunk of k-steps at a time straight into MFMA 16x16
+//        operand registers;
 //     3. every inference unit at once, x[l] += gamma(-eps[l] + f'(x[l]) W[l-1]^T eps[l-1]),
-//        W[l-1] read transposed from global memory, eps[l-1] from LDS.
+//        W[l-1] read transposed from global memory, eps[l-1] from LDS; the
+//        epilogue also writes f(x_new) for phase B and refreshes the LDS copies.
 //     No column block depends on another, so phase A has no inter-workgroup
-//     synchronisation.
+//     synchronisation.  In a multi-step launch every workgroup owns one column
+//     block for all steps and its LDS copies stay resident: only W is re-read.
 //   phase B (weight update): 64x64 tiles of every W[l] are spread over the
 //     workgroups, W[l] += alpha eps[l] f(x_new[l+1])^T contracting over the
-//     batch with MFMA, or, for B <= 16, as a rank-B outer product on the VALU.
+//     batch with MFMA (f(x_new) comes pre-evaluated from phase A), or, for
+//     B <= 16, as a rank-B outer product on the VALU.
 //
 // The phases are separated by a grid barrier (a monotonically increasing
 // arrival counter in a caller-provided workspace, every wait bounded by a spin
@@ -29,8 +33,10 @@
 // with the same prediction units as phase A, so the hidden prediction errors
 // are exactly 0 after it, as in trainer.py:512-515.
 //
-// Global loads in the inner loops are branch-free (clamped address, masked
-// value) so the compiler can issue several of them before the first wait.
+// Inner loops issue their global loads first (branch-free: clamped address,
+// masked value) and compute afterwards, so each chunk of loads costs one
+// memory latency instead of one per k-step.  The activation is a template
+// parameter, so no switch sits in any inner loop.
 #include "ipc_device.h"
 #include "ipc_launch.h"
 #include "ipc_narrow.h"
@@ -42,7 +48,8 @@ namespace {
 constexpr int NT = 512;  // threads per workgroup (8 waves)
 constexpr int NW = NT / 64;
 constexpr int NC = NARROW_NC;
-constexpr int WT = 64;  // weight-update tile edge
+constexpr int WT = 64;   // weight-update tile edge
+constexpr int SCH = 8;   // staging: elements per thread per load batch
 
 // acc(16x16) += A(16 x KS) B(KS x 16).  Lane (r = lane % 16, g = lane / 16)
 // supplies a[q] = A[r][k0 + g*KL + q] and b[q] = B[k0 + g*KL + q][r], q < KL.
@@ -79,12 +86,12 @@ template <> struct Mma16<bf16> {
 __device__ __forceinline__ int round_up(int v, int m) { return (v + m - 1) / m * m; }
 
 // KL consecutive values row[k .. k+KL), zero outside [0, K) or when !ok.
-// Every lane loads from an in-bounds address (row[0] when masked), so the
-// loads carry no branches.  `vec` (K % KL == 0 and a 16-byte aligned matrix)
-// selects 16-byte loads; then a KL-run is either wholly in or wholly out.
-template <int KL>
-__device__ __forceinline__ void load_run(const float* row, int k, int K, bool ok, bool vec, float* o) {
-  if (vec) {
+// Every lane loads from an in-bounds address (row[0] when masked): no branch.
+// VEC (K % KL == 0, 16-byte aligned matrix): 16-byte loads; a run is then
+// wholly in or wholly out of range.
+template <int KL, bool VEC>
+__device__ __forceinline__ void load_run(const float* row, int k, int K, bool ok, float* o) {
+  if (VEC) {
     const bool in = ok && k < K;
     const float4* src = reinterpret_cast<const float4*>(row + (in ? k : 0));
 #pragma unroll
@@ -139,11 +146,12 @@ __device__ void barrier_exit(unsigned* bar, int nblocks) {
   }
 }
 
-template <typename OT, int SPLIT>
+template <typename OT, int SPLIT, int ACT>
 struct Narrow {
   using MM = Mma16<OT>;
   static constexpr int KS = MM::KS, KL = MM::KL, PAD = MM::PAD;
   static constexpr bool SA = SPLIT >= 2, SB = SPLIT >= 3;
+  static constexpr int NPF = 64 / KL;  // k-steps per prefetched chunk (64 floats per lane)
 
   const NarrowArgs& p;
   const NarrowLds& lay;
@@ -163,27 +171,72 @@ struct Narrow {
   __device__ __forceinline__ OT* fs_lo(int l) { return fs_hi(l) + NC * ldk(p.dims[l]); }
   __device__ __forceinline__ OT* es(int l) { return reinterpret_cast<OT*>(lds + lay.es_base) + lay.es_off[l]; }
 
-  // f(x[l][:, c0:c0+ncols]) -> fs block of layer l as [n][k], zero for k >= d_l or n >= ncols;
-  // with keep_raw the raw values also go to xr (layer l < L).
-  __device__ __forceinline__ void stage_layer(int l, int c0, int ncols, bool keep_raw, bool want_f) {
-    const int d = p.dims[l], ld = ldk(d), B = p.B, act = p.act;
+  // Stages layer l of column block [c0, c0+ncols): raw x into xr (keep_raw),
+  // f(x) into the fs block ([n][k], zero for k >= d_l or n >= ncols) and, with
+  // fx_out, f(x) into the global pre-activation buffer.  Loads are issued SCH
+  // at a time before any of them is used.
+  __device__ __forceinline__ void stage_layer(int l, int c0, int ncols, bool keep_raw, bool want_f, float* fx_out) {
+    const int d = p.dims[l], ld = ldk(d), B = p.B;
     const float* X = p.x[l];
-    OT* fh = want_f ? fs_hi(l) : nullptr;
-    OT* fl = (want_f && SB) ? fs_lo(l) : nullptr;
-    float* raw = keep_raw ? xr(l) : nullptr;
     const int rows = want_f ? ld : d;
-    for (int i = tid; i < rows * NC; i += NT) {
-      const int k = i / NC, n = i - k * NC;
-      const bool in = k < d && n < ncols;
-      const float v = in ? X[(long long)k * B + c0 + n] : 0.0f;
-      if (raw && k < d) raw[k * NC + n] = v;
-      if (want_f) {
-        const float fv = in ? act_f(act, v) : 0.0f;
-        const OT hi = cvt<OT>(fv);
-        fh[n * ld + k] = hi;
-        if (SB) fl[n * ld + k] = cvt<OT>(fv - to_f32(hi));
+    const int total = rows * NC;
+    for (int base = tid; base < total; base += NT * SCH) {
+      float v[SCH];
+#pragma unroll
+      for (int i = 0; i < SCH; ++i) {
+        const int idx = base + i * NT;
+        const int k = idx / NC, n = idx - k * NC;
+        const bool in = idx < total && k < d && n < ncols;
+        const float t = X[in ? (long long)k * B + c0 + n : 0];
+        v[i] = in ? t : 0.0f;
+      }
+#pragma unroll
+      for (int i = 0; i < SCH; ++i) {
+        const int idx = base + i * NT;
+        if (idx < total) {
+          const int k = idx / NC, n = idx - k * NC;
+          const bool in = k < d && n < ncols;
+          if (keep_raw && k < d) xr(l)[k * NC + n] = v[i];
+          if (want_f) {
+            const float fv = in ? act_t<ACT>(v[i]) : 0.0f;
+            const OT hi = cvt<OT>(fv);
+            fs_hi(l)[n * ld + k] = hi;
+            if (SB) fs_lo(l)[n * ld + k] = cvt<OT>(fv - to_f32(hi));
+            if (fx_out && in) fx_out[(long long)k * B + c0 + n] = fv;
+          }
+        }
       }
     }
+  }
+
+  template <bool VEC, int CH>
+  __device__ __forceinline__ f32x4 pred_loop(const float* wrow, bool rok, int K, const OT* fh, const OT* fl,
+                                             int nsteps) {
+    f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s0 = 0; s0 < nsteps; s0 += CH) {
+      float av[CH][KL];
+#pragma unroll
+      for (int i = 0; i < CH; ++i)
+        load_run<KL, VEC>(wrow, (s0 + i) * KS + lg * KL, K, rok && (s0 + i) < nsteps, av[i]);
+#pragma unroll
+      for (int i = 0; i < CH; ++i) {
+        if (s0 + i < nsteps) {
+          const int kk = (s0 + i) * KS;
+          OT ah[KL], al[KL], bh[KL], bl[KL];
+#pragma unroll
+          for (int q = 0; q < KL; ++q) {
+            ah[q] = cvt<OT>(av[i][q]);
+            if (SA) al[q] = cvt<OT>(av[i][q] - to_f32(ah[q]));
+            bh[q] = fh[kk + q];
+            if (SB) bl[q] = fl[kk + q];
+          }
+          c = MM::run(ah, bh, c);
+          if (SA) c = MM::run(al, bh, c);
+          if (SB) c = MM::run(ah, bl, c);
+        }
+      }
+    }
+    return c;
   }
 
   // One prediction unit: acc = W[l][rt*16 .. +16][:] f(x[l+1])[:, cols] from the staged fs block.
@@ -196,57 +249,52 @@ struct Narrow {
     const bool vec = (K % KL == 0) && ((reinterpret_cast<uintptr_t>(W) & 15) == 0);
     const OT* fh = fs_hi(l + 1) + lr * ld + lg * KL;
     const OT* fl = SB ? fs_lo(l + 1) + lr * ld + lg * KL : nullptr;
-    const int kpad = round_up(K, KS);
-    f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 4
-    for (int kk = 0; kk < kpad; kk += KS) {
-      float av[KL];
-      load_run<KL>(wrow, kk + lg * KL, K, rok, vec, av);
-      OT ah[KL], al[KL], bh[KL], bl[KL];
-#pragma unroll
-      for (int q = 0; q < KL; ++q) {
-        ah[q] = cvt<OT>(av[q]);
-        if (SA) al[q] = cvt<OT>(av[q] - to_f32(ah[q]));
-        bh[q] = fh[kk + q];
-        if (SB) bl[q] = fl[kk + q];
-      }
-      c = MM::run(ah, bh, c);
-      if (SA) c = MM::run(al, bh, c);
-      if (SB) c = MM::run(ah, bl, c);
-    }
-    return c;
+    const int nsteps = round_up(K, KS) / KS;
+    // one loop body per load type keeps the kernel's code small
+    if (vec) return pred_loop<true, NPF>(wrow, rok, K, fh, fl, nsteps);
+    return pred_loop<false, 4>(wrow, rok, K, fh, fl, nsteps);
   }
 
-  // One inference unit: acc = W[l-1]^T[rt*16 .. +16][:] eps[l-1][:, cols].
+  // One inference unit: acc = W[l-1]^T[rt*16 .. +16][:] eps[l-1][:, cols]
+  // (contraction d_{l-1} <= 128: every load of the unit is issued first).
   __device__ __forceinline__ f32x4 infer_unit(int l, int rt) {
+    constexpr int MAXS = NARROW_MAX_WIDTH / KS;
     const int M = p.dims[l], Kp = p.dims[l - 1], ld = ldk(Kp);
     const float* Wl = p.w[l - 1];  // [Kp][M]
     const int m = rt * 16 + lr;
     const bool mok = m < M;
     const OT* eb = es(l - 1) + lr * ld + lg * KL;
-    const int kpad = round_up(Kp, KS);
-    f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 2
-    for (int kk = 0; kk < kpad; kk += KS) {
-      OT ah[KL], bh[KL];
+    const int nsteps = round_up(Kp, KS) / KS;
+    float av[MAXS][KL];
+#pragma unroll
+    for (int i = 0; i < MAXS; ++i)
 #pragma unroll
       for (int q = 0; q < KL; ++q) {
-        const int k = kk + lg * KL + q;
-        const bool in = mok && k < Kp;
+        const int k = i * KS + lg * KL + q;
+        const bool in = mok && k < Kp && i < nsteps;
         const float v = Wl[in ? (long long)k * M + m : 0];
-        ah[q] = cvt<OT>(in ? v : 0.0f);
-        bh[q] = eb[kk + q];
+        av[i][q] = in ? v : 0.0f;
       }
-      c = MM::run(ah, bh, c);
+    f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < MAXS; ++i) {
+      if (i < nsteps) {
+        OT ah[KL], bh[KL];
+#pragma unroll
+        for (int q = 0; q < KL; ++q) {
+          ah[q] = cvt<OT>(av[i][q]);
+          bh[q] = eb[i * KS + q];
+        }
+        c = MM::run(ah, bh, c);
+      }
     }
     return c;
   }
 
-  // Phase A for column block cb.
-  __device__ __forceinline__ void phase_a(int cb) {
+  // Stages column block cb: every layer's x (raw) and f(x), zeroed eps blocks,
+  // and f(x[L]) of the block's columns into the pre-activation buffer.
+  __device__ __forceinline__ void stage_all(int cb) {
     const int B = p.B, L = p.L, c0 = cb * NC, ncols = min(NC, B - c0);
-    const float gamma = p.gamma;
-    const int act = p.act;
     __syncthreads();  // LDS of the previous column block / phase is free
     // eps blocks are the zero-padded B operands of the inference units
     for (int l = 0; l + 1 < L; ++l) {
@@ -254,7 +302,16 @@ struct Narrow {
       const int n_el = NC * ldk(p.dims[l]);
       for (int i = tid; i < n_el; i += NT) e_l[i] = cvt<OT>(0.0f);
     }
-    for (int l = 0; l <= L; ++l) stage_layer(l, c0, ncols, l < L, l >= 1);
+    for (int l = 0; l <= L; ++l) stage_layer(l, c0, ncols, l < L, l >= 1, l == L ? p.fx[L] : nullptr);
+  }
+
+  // Phase A for column block cb.  With `resident` the block's LDS already
+  // holds this column block's x, f(x) and eps padding from the previous step
+  // (the inference epilogue keeps them current), so nothing is restaged.
+  __device__ __forceinline__ void phase_a(int cb, bool resident) {
+    const int B = p.B, L = p.L, c0 = cb * NC, ncols = min(NC, B - c0);
+    const float gamma = p.gamma;
+    if (!resident) stage_all(cb);
     __syncthreads();
     // ---- every prediction unit: eps = x[l] - W[l] f(x[l+1])
     for (int u = wave; u < p.n_units; u += NW) {
@@ -280,6 +337,7 @@ struct Narrow {
       if (l == 0) continue;
       const int M = p.dims[l];
       const f32x4 c = infer_unit(l, rt);
+      float* fxl = p.fx[l];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int row = rt * 16 + lg * 4 + j;
@@ -287,9 +345,18 @@ struct Narrow {
 #pragma clang fp contract(off)
           const long long o = (long long)row * B + c0 + lr;
           const float x = xr(l)[row * NC + lr];
-          const float xn = x + gamma * (-ef(l)[row * NC + lr] + act_df(act, x) * c[j]);
+          const float xn = x + gamma * (-ef(l)[row * NC + lr] + dact_t<ACT>(x) * c[j]);
           p.x[l][o] = xn;
-          if (p.a[l]) p.a[l][o] = act_f(act, xn);
+          const float fxn = act_t<ACT>(xn);
+          fxl[o] = fxn;
+          if (resident) {
+            // keep the block's staged copies current for the next step
+            xr(l)[row * NC + lr] = xn;
+            const int ld = ldk(M);
+            const OT hi = cvt<OT>(fxn);
+            fs_hi(l)[lr * ld + row] = hi;
+            if (SB) fs_lo(l)[lr * ld + row] = cvt<OT>(fxn - to_f32(hi));
+          }
         }
       }
     }
@@ -300,7 +367,7 @@ struct Narrow {
     const int B = p.B, L = p.L, c0 = cb * NC, ncols = min(NC, B - c0);
     for (int l = L - 1; l >= 1; --l) {
       __syncthreads();
-      stage_layer(l + 1, c0, ncols, false, true);
+      stage_layer(l + 1, c0, ncols, false, true, nullptr);
       __syncthreads();
       const int M = p.dims[l];
       for (int rt = wave; rt * 16 < M; rt += NW) {
@@ -311,18 +378,17 @@ struct Narrow {
           if (row < M && lr < ncols) p.x[l][(long long)row * B + c0 + lr] = c[j];
         }
       }
-      __threadfence_block();
     }
     if (p.a[L]) {
-      const int act = p.act;
       for (int i = tid; i < p.dims[L] * NC; i += NT) {
         const int k = i / NC, n = i - k * NC;
-        if (n < ncols) p.a[L][(long long)k * B + c0 + n] = act_f(act, p.x[L][(long long)k * B + c0 + n]);
+        if (n < ncols) p.a[L][(long long)k * B + c0 + n] = act_t<ACT>(p.x[L][(long long)k * B + c0 + n]);
       }
     }
   }
 
-  // Phase B for weight tile `tile`: W[l] tile += alpha eps[l] f(x_new[l+1])^T.
+  // Phase B for weight tile `tile`: W[l] tile += alpha eps[l] f(x_new[l+1])^T,
+  // f(x_new[l+1]) read pre-evaluated from fx[l+1].
   __device__ __forceinline__ void phase_b(int tile) {
     int l = 0;
     while (l + 1 < p.L && tile >= p.wtile_start[l + 1]) ++l;
@@ -331,20 +397,18 @@ struct Narrow {
     const int local = tile - p.wtile_start[l];
     const int m0 = (local / tn) * WT, n0 = (local % tn) * WT;
     const float* E = p.e[l];
-    const bool saved = p.a[l + 1] != nullptr;
-    const float* X = saved ? p.a[l + 1] : p.x[l + 1];
-    const int act = saved ? (int)ACT_IDENTITY : p.act;
+    const float* X = p.fx[l + 1];
     float* W = p.w[l];
     const float alpha = p.alpha;
     if (p.outer) {
       // rank-B outer product on the VALU (B <= NC)
-      float* so_e = reinterpret_cast<float*>(lds);
+      float* so_e = reinterpret_cast<float*>(lds + lay.outer_base);
       float* so_x = so_e + WT * (NC + 1);
       __syncthreads();
       for (int i = tid; i < WT * B; i += NT) {
         const int r = i / B, b = i - r * B;
         so_e[r * (NC + 1) + b] = (m0 + r < M) ? E[(long long)(m0 + r) * B + b] : 0.0f;
-        so_x[r * (NC + 1) + b] = (n0 + r < N) ? act_f(act, X[(long long)(n0 + r) * B + b]) : 0.0f;
+        so_x[r * (NC + 1) + b] = (n0 + r < N) ? X[(long long)(n0 + r) * B + b] : 0.0f;
       }
       __syncthreads();
       for (int i = tid; i < WT * WT; i += NT) {
@@ -392,26 +456,40 @@ struct Narrow {
     f32x4 acc[2];
 #pragma unroll
     for (int s = 0; s < 2; ++s) acc[s] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    const int bpad = round_up(B, KS);
-#pragma unroll 4
-    for (int b0 = 0; b0 < bpad; b0 += KS) {
-      float av[KL];
-      load_run<KL>(erow, b0 + lg * KL, B, mok, vec, av);
-      float xv[2][KL];
+    constexpr int BCH = 16 / KL;  // k-steps per load batch (16 floats per operand row)
+    const int nsteps = round_up(B, KS) / KS;
+    for (int s0 = 0; s0 < nsteps; s0 += BCH) {
+      float av[BCH][KL], xv[2][BCH][KL];
+      if (vec) {
 #pragma unroll
-      for (int s = 0; s < 2; ++s) load_run<KL>(xrow[s], b0 + lg * KL, B, nok[s], vec, xv[s]);
-      OT ah[KL];
-#pragma unroll
-      for (int q = 0; q < KL; ++q) ah[q] = cvt<OT>(av[q]);
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        OT bh[KL];
-#pragma unroll
-        for (int q = 0; q < KL; ++q) {
-          const bool in = nok[s] && (b0 + lg * KL + q < B);
-          bh[q] = cvt<OT>(in ? act_f(act, xv[s][q]) : 0.0f);
+        for (int i = 0; i < BCH; ++i) {
+          const int b = (s0 + i) * KS + lg * KL;
+          load_run<KL, true>(erow, b, B, mok, av[i]);
+          load_run<KL, true>(xrow[0], b, B, nok[0], xv[0][i]);
+          load_run<KL, true>(xrow[1], b, B, nok[1], xv[1][i]);
         }
-        acc[s] = MM::run(ah, bh, acc[s]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < BCH; ++i) {
+          const int b = (s0 + i) * KS + lg * KL;
+          load_run<KL, false>(erow, b, B, mok, av[i]);
+          load_run<KL, false>(xrow[0], b, B, nok[0], xv[0][i]);
+          load_run<KL, false>(xrow[1], b, B, nok[1], xv[1][i]);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < BCH; ++i) {
+        if (s0 + i < nsteps) {
+          OT ah[KL], b0h[KL], b1h[KL];
+#pragma unroll
+          for (int q = 0; q < KL; ++q) {
+            ah[q] = cvt<OT>(av[i][q]);
+            b0h[q] = cvt<OT>(xv[0][i][q]);
+            b1h[q] = cvt<OT>(xv[1][i][q]);
+          }
+          acc[0] = MM::run(ah, b0h, acc[0]);
+          acc[1] = MM::run(ah, b1h, acc[1]);
+        }
       }
     }
 #pragma unroll
@@ -429,9 +507,9 @@ struct Narrow {
   }
 };
 
-template <typename OT, int SPLIT>
+template <typename OT, int SPLIT, int ACT>
 __global__ void __launch_bounds__(NT) narrow_kernel(const NarrowArgs p) {
-  using N = Narrow<OT, SPLIT>;
+  using N = Narrow<OT, SPLIT, ACT>;
   extern __shared__ __align__(16) char lds[];
   __shared__ NarrowLds layout;
   if (threadIdx.x == 0)
@@ -445,29 +523,73 @@ __global__ void __launch_bounds__(NT) narrow_kernel(const NarrowArgs p) {
     for (int cb = blockIdx.x; cb < ncb; cb += nb) k.forward(cb);
     return;
   }
-  if (p.mode == NMODE_PHASE_A) {
-    for (int cb = blockIdx.x; cb < ncb; cb += nb) k.phase_a(cb);
-    return;
-  }
-  if (p.mode == NMODE_PHASE_B) {
-    for (int t = blockIdx.x; t < ntile; t += nb) k.phase_b(t);
-    return;
-  }
+  // One loop serves the multi-step launch and the single-phase launches, so
+  // each phase's code exists once in the kernel.  In a multi-step launch in
+  // which every column block has its own workgroup, each workgroup stages its
+  // block once and keeps it LDS-resident for all steps.
+  const bool do_a = p.mode != NMODE_PHASE_B, do_b = p.mode != NMODE_PHASE_A;
+  const bool multi = p.mode == NMODE_STEPS;
+  const bool resident = multi && ncb <= nb;
+  if (resident && (int)blockIdx.x < ncb) k.stage_all(blockIdx.x);
+  const int steps = multi ? p.steps : 1;
   int nbar = 0;
-  for (int s = 0; s < p.steps; ++s) {
-    for (int cb = blockIdx.x; cb < ncb; cb += nb) k.phase_a(cb);
-    grid_barrier(p.bar, nb, nbar++, p.spin_limit);
-    for (int t = blockIdx.x; t < ntile; t += nb) k.phase_b(t);
-    if (s + 1 < p.steps) grid_barrier(p.bar, nb, nbar++, p.spin_limit);
+  for (int s = 0; s < steps; ++s) {
+    if (do_a)
+      for (int cb = blockIdx.x; cb < ncb; cb += nb) k.phase_a(cb, resident);
+    if (multi) grid_barrier(p.bar, nb, nbar++, p.spin_limit);
+    if (do_b)
+      for (int t = blockIdx.x; t < ntile; t += nb) k.phase_b(t);
+    if (multi && s + 1 < steps) grid_barrier(p.bar, nb, nbar++, p.spin_limit);
   }
-  barrier_exit(p.bar, nb);
+  if (multi) barrier_exit(p.bar, nb);
 }
 
-template <typename OT, int SPLIT>
-hipError_t set_lds(int bytes) {
-  return hipFuncSetAttribute(reinterpret_cast<const void*>(&narrow_kernel<OT, SPLIT>),
-                             hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+// ---------------------------------------------------------------- dispatch
+template <typename OT, int SPLIT, int ACT>
+struct KernelRef {
+  static const void* get() { return reinterpret_cast<const void*>(&narrow_kernel<OT, SPLIT, ACT>); }
+  static void launch(const NarrowArgs& p, dim3 g, dim3 b, size_t lds, hipStream_t s) {
+    hipLaunchKernelGGL((narrow_kernel<OT, SPLIT, ACT>), g, b, lds, s, p);
+  }
+};
+
+template <template <typename, int, int> class F, typename OT, int SPLIT, typename... Args>
+auto by_act(int act, Args&&... a) {
+  switch (act) {
+    case ACT_RELU: return F<OT, SPLIT, ACT_RELU>::run(a...);
+    case ACT_TANH: return F<OT, SPLIT, ACT_TANH>::run(a...);
+    case ACT_SIGMOID: return F<OT, SPLIT, ACT_SIGMOID>::run(a...);
+    case ACT_SILU: return F<OT, SPLIT, ACT_SILU>::run(a...);
+    case ACT_GELU: return F<OT, SPLIT, ACT_GELU>::run(a...);
+    default: return F<OT, SPLIT, ACT_IDENTITY>::run(a...);
+  }
 }
+
+template <template <typename, int, int> class F, typename... Args>
+auto by_type(int operand, int split, int act, Args&&... a) {
+  if (operand == DT_F32) return by_act<F, float, 1>(act, a...);
+  if (operand == DT_F16) {
+    if (split >= 3) return by_act<F, f16, 3>(act, a...);
+    return by_act<F, f16, 1>(act, a...);
+  }
+  if (split >= 3) return by_act<F, bf16, 3>(act, a...);
+  return by_act<F, bf16, 1>(act, a...);
+}
+
+template <typename OT, int SPLIT, int ACT>
+struct SetLds {
+  static hipError_t run(int bytes) {
+    return hipFuncSetAttribute(KernelRef<OT, SPLIT, ACT>::get(), hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  }
+};
+
+template <typename OT, int SPLIT, int ACT>
+struct Launch {
+  static hipError_t run(const NarrowArgs& p, hipStream_t s) {
+    KernelRef<OT, SPLIT, ACT>::launch(p, dim3(p.nblocks), dim3(NT), (size_t)p.lds_bytes, s);
+    return hipGetLastError();
+  }
+};
 
 }  // namespace
 
@@ -484,33 +606,12 @@ int narrow_lds_bytes(const int* dims, int L, int operand, int split) {
   return o.total;
 }
 
-hipError_t narrow_prepare(int operand, int split, int lds_bytes) {
-  if (operand == DT_F32) return set_lds<float, 1>(lds_bytes);
-  if (operand == DT_F16) {
-    if (split >= 3) return set_lds<f16, 3>(lds_bytes);
-    if (split == 2) return set_lds<f16, 2>(lds_bytes);
-    return set_lds<f16, 1>(lds_bytes);
-  }
-  if (split >= 3) return set_lds<bf16, 3>(lds_bytes);
-  if (split == 2) return set_lds<bf16, 2>(lds_bytes);
-  return set_lds<bf16, 1>(lds_bytes);
+hipError_t narrow_prepare(int operand, int split, int act, int lds_bytes) {
+  return by_type<SetLds>(operand, split, act, lds_bytes);
 }
 
 hipError_t launch_narrow(const NarrowArgs& p, int operand, int split, hipStream_t s) {
-  const dim3 grid(p.nblocks), block(NT);
-  const size_t lds = (size_t)p.lds_bytes;
-  if (operand == DT_F32) {
-    hipLaunchKernelGGL((narrow_kernel<float, 1>), grid, block, lds, s, p);
-  } else if (operand == DT_F16) {
-    if (split >= 3) hipLaunchKernelGGL((narrow_kernel<f16, 3>), grid, block, lds, s, p);
-    else if (split == 2) hipLaunchKernelGGL((narrow_kernel<f16, 2>), grid, block, lds, s, p);
-    else hipLaunchKernelGGL((narrow_kernel<f16, 1>), grid, block, lds, s, p);
-  } else {
-    if (split >= 3) hipLaunchKernelGGL((narrow_kernel<bf16, 3>), grid, block, lds, s, p);
-    else if (split == 2) hipLaunchKernelGGL((narrow_kernel<bf16, 2>), grid, block, lds, s, p);
-    else hipLaunchKernelGGL((narrow_kernel<bf16, 1>), grid, block, lds, s, p);
-  }
-  return hipGetLastError();
+  return by_type<Launch>(operand, split, p.act, p, s);
 }
 
 }  // namespace ipc
