@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define IPC_ABI_VERSION 1
+#define IPC_ABI_VERSION 2
 
 /* status codes */
 #define IPC_OK 0
@@ -154,27 +154,44 @@ int ipc_weight_update_outer(void* w, const void* e, const void* x_upper, int M, 
 typedef struct ipc_plan ipc_plan;
 
 /* split applies to the prediction phase and the forward initialisation.
- * fused: IPC_FUSED_AUTO picks the whole-step kernel when the net is narrow
- * (fp32 storage, every output width d_0..d_{L-1} <= 128, L <= 16, split 1 or 3,
- * one column block's buffers fit in LDS);
- * IPC_FUSED_OFF always uses one multi-layer launch per phase; IPC_FUSED_ON
- * requires the whole-step kernel (IPC_ERR_CONFIG if the net is not narrow). */
-#define IPC_FUSED_AUTO (-1)
-#define IPC_FUSED_OFF 0
-#define IPC_FUSED_ON 1
+ * path selects the kernels a plan runs:
+ *   IPC_PATH_AUTO    the whole-step kernel when the net is narrow (fp32
+ *                    storage, every output width d_0..d_{L-1} <= 128, L <= 16,
+ *                    split 1 or 3, one column block's buffers fit in LDS),
+ *                    else the wide GEMM path when eligible, else the phased path;
+ *   IPC_PATH_PHASED  one generic multi-layer launch per phase (any config);
+ *   IPC_PATH_NARROW  the whole-step kernel (IPC_ERR_CONFIG if not narrow);
+ *   IPC_PATH_WIDE    one LDS-DMA MFMA launch per phase over 16-bit operand
+ *                    copies kept in the workspace: fp32 storage, fp16/bf16
+ *                    operands, split 1 or 2, GEMM weight update (weight mode
+ *                    GEMM, or AUTO with B > 16); IPC_ERR_CONFIG otherwise.
+ * The IPC_FUSED_* names are the same values (AUTO, OFF = PHASED, ON = NARROW). */
+#define IPC_PATH_AUTO (-1)
+#define IPC_PATH_PHASED 0
+#define IPC_PATH_NARROW 1
+#define IPC_PATH_WIDE 2
+#define IPC_FUSED_AUTO IPC_PATH_AUTO
+#define IPC_FUSED_OFF IPC_PATH_PHASED
+#define IPC_FUSED_ON IPC_PATH_NARROW
 int ipc_plan_create(ipc_plan** out, int L, const int* dims, int B,
                     int storage, int operand, int split, int act, float alpha, float gamma,
-                    int recompute, int weight_mode, int fused);
+                    int recompute, int weight_mode, int path);
 
 /* 1 if the plan runs the whole-step kernel, 0 otherwise. */
 int ipc_plan_fused(const ipc_plan* plan);
 
-/* Bytes of zero-initialised device workspace ipc_plan_bind needs (0 when not
- * fused).  The whole-step kernel keeps its grid-barrier counters in the first
- * 256 bytes and leaves them zero after every launch (word 2 becomes non-zero
- * if a barrier wait ever ran past its spin limit); in recompute mode the rest
- * holds the f(x[l]) values phase A evaluates for the weight update. */
-int ipc_plan_workspace_bytes(const ipc_plan* plan);
+/* The path the plan runs (IPC_PATH_PHASED, _NARROW or _WIDE), -1 for NULL. */
+int ipc_plan_path(const ipc_plan* plan);
+
+/* Bytes of zero-initialised device workspace ipc_plan_bind needs (0 for the
+ * phased path).  The first 256 bytes hold the whole-step kernel's
+ * grid-barrier counters, which it leaves zero after every launch (word 2
+ * becomes non-zero if a barrier wait ever ran past its spin limit); in
+ * recompute mode the whole-step kernel keeps the f(x[l]) values phase A
+ * evaluates for the weight update after them.  The wide path keeps its
+ * 16-bit operand copies there (W and W^T, f(x) and eps in both layouts,
+ * zero padded); their padding must stay zero. */
+long long ipc_plan_workspace_bytes(const ipc_plan* plan);
 
 /* Binds the caller's buffers: x and e hold L+1 pointers ([d_l, B] each; e[L]
  * is unused and may be NULL), w holds L pointers ([d_l, d_{l+1}]), a holds
@@ -187,9 +204,15 @@ int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w
 int ipc_plan_step(ipc_plan* plan, int steps, void* stream);
 
 /* Enqueues the forward initialisation of the bound states: a[L] = f(x[L]) in
- * save mode, hidden x[l] = W[l] f(x[l+1]) for l = L-1..1 (trainer.py:509-515).
- * x[0] and x[L] are left to the caller. */
+ * save mode, hidden x[l] = W[l] f(x[l+1]) for l = L-1..1 (trainer.py:509-515),
+ * then (wide path) the refresh of the 16-bit operand copies.
+ * x[0] and x[L] are left to the caller; x[L] must be written before. */
 int ipc_plan_forward_init(ipc_plan* plan, void* stream);
+
+/* Wide path: re-derives the 16-bit operand copies from the fp32 masters x
+ * and W.  Needed only after the caller wrote x[1..L] or W outside
+ * ipc_plan_step / ipc_plan_forward_init; a no-op for the other paths. */
+int ipc_plan_sync(ipc_plan* plan, void* stream);
 
 /* Enqueues only one phase of the step `reps` times (0 = prediction+error,
  * 1 = inference update, 2 = weight update), so that each phase's kernel can

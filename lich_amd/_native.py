@@ -8,7 +8,7 @@ missing, every entry point raises.
 from __future__ import annotations
 
 import ctypes
-from ctypes import POINTER, c_char_p, c_float, c_int, c_void_p
+from ctypes import POINTER, c_char_p, c_float, c_int, c_longlong, c_void_p
 from pathlib import Path
 
 import torch  # noqa: F401  (loads the HIP runtime the library binds to)
@@ -26,7 +26,12 @@ TILE_AUTO = -1
 TILE_COUNT = 3
 WMODE = {"gemm": 0, "outer": 1, "auto": 2}
 SPLIT_NONE, SPLIT_W, SPLIT_WX = 1, 2, 3
-FUSED = {"auto": -1, "off": 0, "on": 1}
+PATH_AUTO, PATH_PHASED, PATH_NARROW, PATH_WIDE = -1, 0, 1, 2
+# plan path option (IPCConfig.fused): the IPC_PATH_* codes; "off"/"on" are the
+# IPC_FUSED_* spellings of phased / narrow
+FUSED = {"auto": PATH_AUTO, "off": PATH_PHASED, "phased": PATH_PHASED, "on": PATH_NARROW, "narrow": PATH_NARROW,
+         "wide": PATH_WIDE}
+PATH_NAMES = {PATH_PHASED: "phased", PATH_NARROW: "narrow", PATH_WIDE: "wide"}
 
 _DTYPE_CODES = {torch.float32: DT_F32, torch.float16: DT_F16, torch.bfloat16: DT_BF16}
 
@@ -72,10 +77,12 @@ def _declare(lib):
         "ipc_weight_update_outer": ([vp, vp, vp, i, i, i, i, f, i, i, i, vp], i),
         "ipc_plan_create": ([POINTER(vp), i, POINTER(c_int), i, i, i, i, i, f, f, i, i, i], i),
         "ipc_plan_fused": ([vp], i),
-        "ipc_plan_workspace_bytes": ([vp], i),
+        "ipc_plan_path": ([vp], i),
+        "ipc_plan_workspace_bytes": ([vp], c_longlong),
         "ipc_plan_bind": ([vp, POINTER(vp), POINTER(vp), POINTER(vp), POINTER(vp), vp], i),
         "ipc_plan_step": ([vp, i, vp], i),
         "ipc_plan_forward_init": ([vp, vp], i),
+        "ipc_plan_sync": ([vp, vp], i),
         "ipc_plan_phase": ([vp, i, i, vp], i),
         "ipc_plan_launch_count": ([vp], i),
         "ipc_plan_destroy": ([vp], None),

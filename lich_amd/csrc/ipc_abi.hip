@@ -18,6 +18,7 @@
 #include "../../include/ipc_hip.h"
 #include "ipc_launch.h"
 #include "ipc_narrow.h"
+#include "ipc_wide.h"
 
 using namespace ipc;
 
@@ -308,6 +309,11 @@ struct ipc_plan {
   // whole-step kernel for narrow nets
   bool narrow = false;
   NarrowArgs nargs{};
+  // wide GEMM path
+  bool wide = false;
+  std::vector<WideProblem> wpred, winfer, wweight, wfwd;  // wfwd: l = L-1 .. 1
+  std::vector<WideCopy> wsync, wsync_init;               // wsync_init: W and x[L] only
+  long long ws_bytes = 0;
 };
 
 namespace {
@@ -322,6 +328,45 @@ bool narrow_eligible(int L, const int* dims, int storage, int operand, int split
   // one column block's states, errors and staged activations must fit in LDS
   return narrow_lds_bytes(dims, L, operand, split) <= NARROW_LDS_LIMIT - 1024;
 }
+
+bool wide_eligible(int storage, int operand, int split, int wmode, int B) {
+  if (storage != IPC_DT_F32 || operand == IPC_DT_F32) return false;
+  if (split != IPC_SPLIT_NONE && split != IPC_SPLIT_W) return false;
+  return wmode == IPC_WMODE_GEMM || (wmode == IPC_WMODE_AUTO && B > 16);
+}
+
+// Workspace layout of the wide path: after the 256 bytes every plan reserves,
+// one 256-byte aligned buffer per 16-bit operand copy, rows padded to
+// WIDE_ROW_PAD and the contiguous (k) extent to WIDE_BK.
+struct WideLayout {
+  struct Buf { long long off = -1, ld = 0; };
+  std::vector<Buf> wh, wl, wt, f, ft, e, et;
+  long long total = 256;
+
+  Buf add(long long rows, long long cols) {
+    Buf b;
+    b.ld = wide_pad(cols, WIDE_BK);
+    b.off = total;
+    total += wide_pad(wide_pad(rows, WIDE_ROW_PAD) * b.ld * 2, 256);
+    return b;
+  }
+  WideLayout(const std::vector<int>& d, int L, int B, bool split2) {
+    wh.resize(L); wl.resize(L); wt.resize(L); f.resize(L + 1); ft.resize(L + 1); e.resize(L); et.resize(L);
+    for (int l = 0; l < L; ++l) {
+      wh[l] = add(d[l], d[l + 1]);                      // [d_l][d_{l+1}]   pred A
+      if (split2) wl[l] = add(d[l], d[l + 1]);          //                  pred A_lo
+      if (l <= L - 2) wt[l] = add(d[l + 1], d[l]);      // [d_{l+1}][d_l]   infer A (layer l+1)
+    }
+    for (int l = 1; l <= L; ++l) {
+      f[l] = add(d[l], B);                              // [d_l][B]         weight B (layer l-1)
+      ft[l] = add(B, d[l]);                             // [B][d_l]         pred B (layer l-1)
+    }
+    for (int l = 0; l < L; ++l) {
+      e[l] = add(d[l], B);                              // [d_l][B]         weight A
+      if (l <= L - 2) et[l] = add(B, d[l]);             // [B][d_l]         infer B (layer l+1)
+    }
+  }
+};
 
 int launch_narrow_mode(ipc_plan* plan, int mode, int steps, hipStream_t s) {
   NarrowArgs a = plan->nargs;
@@ -338,7 +383,7 @@ int launch_narrow_mode(ipc_plan* plan, int mode, int steps, hipStream_t s) {
 extern "C" {
 
 int ipc_plan_create(ipc_plan** out, int L, const int* dims, int B, int storage, int operand, int split, int act,
-                    float alpha, float gamma, int recompute, int weight_mode, int fused) {
+                    float alpha, float gamma, int recompute, int weight_mode, int path) {
   if (!out) return fail(IPC_ERR_NULL, "out is NULL");
   *out = nullptr;
   if (!dims) return fail(IPC_ERR_NULL, "dims is NULL");
@@ -351,36 +396,48 @@ int ipc_plan_create(ipc_plan** out, int L, const int* dims, int B, int storage, 
   for (int l = 0; l < L; ++l) TRY(check_dims(dims[l], dims[l + 1], B, 1));
   if (weight_mode == IPC_WMODE_OUTER && B > kOuterMaxB)
     return fail(IPC_ERR_SHAPE, "outer weight mode supports B <= %d (got %d)", kOuterMaxB, B);
-  if (fused < IPC_FUSED_AUTO || fused > IPC_FUSED_ON) return fail(IPC_ERR_CONFIG, "unknown fused option %d", fused);
-  const bool eligible = narrow_eligible(L, dims, storage, operand, effective_split(storage, operand, split));
-  if (fused == IPC_FUSED_ON && !eligible)
+  if (path < IPC_PATH_AUTO || path > IPC_PATH_WIDE) return fail(IPC_ERR_CONFIG, "unknown path %d", path);
+  const int esplit = effective_split(storage, operand, split);
+  const bool eligible = narrow_eligible(L, dims, storage, operand, esplit);
+  if (path == IPC_PATH_NARROW && !eligible)
     return fail(IPC_ERR_CONFIG,
                 "the whole-step kernel needs fp32 storage, L <= %d, widths d_0..d_{L-1} <= %d and a column "
                 "block that fits in LDS", NARROW_MAX_L, NARROW_MAX_WIDTH);
+  const bool weligible = wide_eligible(storage, operand, esplit, weight_mode, B);
+  if (path == IPC_PATH_WIDE && !weligible)
+    return fail(IPC_ERR_CONFIG,
+                "the wide path needs fp32 storage, fp16/bf16 operands, split 1 or 2 and the GEMM weight update");
   ipc_plan* p = new (std::nothrow) ipc_plan();
   if (!p) return fail(IPC_ERR_CONFIG, "out of host memory");
   p->L = L; p->B = B; p->storage = storage; p->operand = operand; p->act = act;
-  p->split = effective_split(storage, operand, split);
+  p->split = esplit;
   p->alpha = alpha; p->gamma = gamma; p->recompute = recompute ? 1 : 0;
   p->wmode = weight_mode;
   p->dims.assign(dims, dims + L + 1);
-  p->narrow = eligible && fused != IPC_FUSED_OFF;
+  p->narrow = path == IPC_PATH_NARROW || (path == IPC_PATH_AUTO && eligible);
+  p->wide = !p->narrow && (path == IPC_PATH_WIDE || (path == IPC_PATH_AUTO && weligible));
+  if (p->narrow) p->ws_bytes = narrow_workspace_bytes(dims, L, B, p->recompute != 0);
+  if (p->wide) p->ws_bytes = WideLayout(p->dims, L, B, p->split == IPC_SPLIT_W).total;
   *out = p;
   return ok();
 }
 
 int ipc_plan_fused(const ipc_plan* plan) { return plan && plan->narrow ? 1 : 0; }
 
-int ipc_plan_workspace_bytes(const ipc_plan* plan) {
-  if (!plan || !plan->narrow) return 0;
-  const long long b = narrow_workspace_bytes(plan->dims.data(), plan->L, plan->B, plan->recompute != 0);
-  return b > (1LL << 30) ? -1 : (int)b;
+int ipc_plan_path(const ipc_plan* plan) {
+  if (!plan) return -1;
+  return plan->narrow ? IPC_PATH_NARROW : plan->wide ? IPC_PATH_WIDE : IPC_PATH_PHASED;
 }
+
+long long ipc_plan_workspace_bytes(const ipc_plan* plan) { return plan ? plan->ws_bytes : 0; }
 
 int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w, void* const* a,
                   void* workspace) {
   if (!plan) return fail(IPC_ERR_NULL, "plan is NULL");
-  if (plan->narrow) TRY(check_ptr(workspace, "workspace", 4));
+  if (plan->ws_bytes) {
+    TRY(check_ptr(workspace, "workspace", 4));
+    if (reinterpret_cast<uintptr_t>(workspace) % 256) return fail(IPC_ERR_ALIGN, "workspace must be 256-byte aligned");
+  }
   if (!x || !e || !w) return fail(IPC_ERR_NULL, "x, e and w pointer arrays are required");
   if (!plan->recompute && !a) return fail(IPC_ERR_NULL, "save-activation plan needs the a[] array");
   const int L = plan->L, B = plan->B, es = elem_size(plan->storage);
@@ -477,6 +534,84 @@ int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w
     TRY(launch_rc(narrow_prepare(plan->operand, plan->split, plan->act, na.lds_bytes), "whole-step kernel LDS limit"));
     plan->launches = 1;
   }
+  if (plan->wide) {
+    const WideLayout lay(d, L, B, plan->split == IPC_SPLIT_W);
+    char* ws = static_cast<char*>(workspace);
+    auto buf = [&](const WideLayout::Buf& b) -> void* { return b.off < 0 ? nullptr : ws + b.off; };
+    auto a16 = [](const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
+    plan->wpred.clear(); plan->winfer.clear(); plan->wweight.clear(); plan->wsync.clear();
+    for (int l = 0; l < L; ++l) {
+      WideProblem q{};
+      q.M = d[l]; q.N = B; q.K = (int)wide_pad(d[l + 1], WIDE_BK);
+      q.a = buf(lay.wh[l]); q.a_lo = buf(lay.wl[l]); q.lda = lay.wh[l].ld;
+      q.b = buf(lay.ft[l + 1]); q.ldb = lay.ft[l + 1].ld;
+      q.out = static_cast<float*>(e[l]); q.ldo = B;
+      q.aux = static_cast<const float*>(x[l]); q.ldx = B;
+      q.h = buf(lay.e[l]); q.ldh = lay.e[l].ld;
+      q.t = buf(lay.et[l]); q.ldt = lay.et[l].ld;
+      q.vec = B % 4 == 0 && a16(e[l]) && a16(x[l]);
+      plan->wpred.push_back(q);
+    }
+    for (int l = 1; l < L; ++l) {
+      WideProblem q{};
+      q.M = d[l]; q.N = B; q.K = (int)wide_pad(d[l - 1], WIDE_BK);
+      q.a = buf(lay.wt[l - 1]); q.lda = lay.wt[l - 1].ld;
+      q.b = buf(lay.et[l - 1]); q.ldb = lay.et[l - 1].ld;
+      q.out = static_cast<float*>(x[l]); q.ldo = B;
+      q.aux = static_cast<const float*>(e[l]); q.ldx = B;
+      q.h = buf(lay.f[l]); q.ldh = lay.f[l].ld;
+      q.t = buf(lay.ft[l]); q.ldt = lay.ft[l].ld;
+      q.out2 = plan->recompute ? nullptr : static_cast<float*>(a[l]); q.ld2 = B;
+      q.scal = plan->gamma;
+      q.vec = B % 4 == 0 && a16(x[l]) && a16(e[l]) && (!q.out2 || a16(q.out2));
+      plan->winfer.push_back(q);
+    }
+    for (int l = 0; l < L; ++l) {
+      WideProblem q{};
+      q.M = d[l]; q.N = d[l + 1]; q.K = (int)wide_pad(B, WIDE_BK);
+      q.a = buf(lay.e[l]); q.lda = lay.e[l].ld;
+      q.b = buf(lay.f[l + 1]); q.ldb = lay.f[l + 1].ld;
+      q.out = static_cast<float*>(w[l]); q.ldo = d[l + 1];
+      q.h = buf(lay.wh[l]); q.ldh = lay.wh[l].ld;
+      q.hl = buf(lay.wl[l]); q.ldhl = lay.wl[l].ld;
+      q.t = buf(lay.wt[l]); q.ldt = lay.wt[l].ld;
+      q.scal = plan->alpha;
+      q.vec = d[l + 1] % 4 == 0 && a16(w[l]);
+      plan->wweight.push_back(q);
+    }
+    for (int l = 0; l < L; ++l) {
+      WideCopy c{};
+      c.src = static_cast<const float*>(w[l]); c.lds = d[l + 1];
+      c.rows = d[l]; c.cols = d[l + 1]; c.act = IPC_ACT_IDENTITY;
+      c.dst = buf(lay.wh[l]); c.ldd = lay.wh[l].ld;
+      c.dst_lo = buf(lay.wl[l]); c.ldl = lay.wl[l].ld;
+      c.dst_t = buf(lay.wt[l]); c.ldt = lay.wt[l].ld;
+      plan->wsync.push_back(c);
+    }
+    for (int l = 1; l <= L; ++l) {
+      WideCopy c{};
+      c.src = static_cast<const float*>(x[l]); c.lds = B;
+      c.rows = d[l]; c.cols = B; c.act = plan->act;
+      c.dst = buf(lay.f[l]); c.ldd = lay.f[l].ld;
+      c.dst_t = buf(lay.ft[l]); c.ldt = lay.ft[l].ld;
+      plan->wsync.push_back(c);
+    }
+    plan->wsync_init.assign(plan->wsync.begin(), plan->wsync.begin() + L);  // W copies
+    plan->wsync_init.push_back(plan->wsync.back());                         // x[L] copies
+    plan->wfwd.clear();
+    for (int l = L - 1; l >= 1; --l) {
+      WideProblem q = plan->wpred[l];
+      q.out = static_cast<float*>(x[l]); q.ldo = B;
+      q.aux = nullptr; q.ldx = 0;
+      q.h = buf(lay.f[l]); q.ldh = lay.f[l].ld;
+      q.t = buf(lay.ft[l]); q.ldt = lay.ft[l].ld;
+      q.vec = B % 4 == 0 && a16(x[l]);
+      plan->wfwd.push_back(q);
+    }
+    TRY(launch_rc(wide_prepare(), "wide path LDS limit"));
+    auto chunks = [](int n) { return (n + WIDE_MAX_BATCH - 1) / WIDE_MAX_BATCH; };
+    plan->launches = 2 * chunks(L) + chunks(L - 1);
+  }
   plan->bound = true;
   return ok();
 }
@@ -486,6 +621,19 @@ int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w
 namespace {
 
 int run_phase(ipc_plan* plan, int phase, hipStream_t s) {
+  if (plan->wide) {
+    switch (phase) {
+      case IPC_PHASE_PRED:
+        return launch_rc(launch_wide(WIDE_PRED, plan->wpred.data(), (int)plan->wpred.size(), plan->operand,
+                                     plan->split == IPC_SPLIT_W ? 2 : 1, plan->act, s), "wide prediction phase");
+      case IPC_PHASE_INFER:
+        return launch_rc(launch_wide(WIDE_INFER, plan->winfer.data(), (int)plan->winfer.size(), plan->operand, 1,
+                                     plan->act, s), "wide inference phase");
+      default:
+        return launch_rc(launch_wide(WIDE_WEIGHT, plan->wweight.data(), (int)plan->wweight.size(), plan->operand, 1,
+                                     plan->act, s), "wide weight phase");
+    }
+  }
   switch (phase) {
     case IPC_PHASE_PRED:
       return launch_rc(launch_gemm(plan->pred.data(), (int)plan->pred.size(), plan->storage, plan->operand,
@@ -542,11 +690,29 @@ int ipc_plan_forward_init(ipc_plan* plan, void* stream) {
     const long long n = (long long)plan->dims[plan->L] * plan->B;
     TRY(launch_rc(launch_act(plan->act_src, plan->act_dst, n, plan->act, plan->storage, s), "plan a[L] = f(x[L])"));
   }
+  if (plan->wide) {
+    // W and f(x[L]) copies, then the layers top-down with the prediction
+    // kernel (its epilogue writes x[l] and the f(x[l]) copies the next layer reads)
+    TRY(launch_rc(launch_wide_copy(plan->wsync_init.data(), (int)plan->wsync_init.size(), plan->operand, s),
+                  "wide operand copies"));
+    for (auto& q : plan->wfwd)
+      TRY(launch_rc(launch_wide(WIDE_FWD, &q, 1, plan->operand, plan->split == IPC_SPLIT_W ? 2 : 1, plan->act, s),
+                    "wide forward init"));
+    return ok();
+  }
   for (auto& q : plan->fwd) {
     const int tile = pick_tile(q.M, q.N, 1);
     TRY(launch_rc(launch_gemm(&q, 1, plan->storage, plan->operand, plan->split, tile, s), "plan forward init"));
   }
   return ok();
+}
+
+int ipc_plan_sync(ipc_plan* plan, void* stream) {
+  if (!plan) return fail(IPC_ERR_NULL, "plan is NULL");
+  if (!plan->bound) return fail(IPC_ERR_STATE, "plan has no bound buffers");
+  if (!plan->wide) return ok();
+  return launch_rc(launch_wide_copy(plan->wsync.data(), (int)plan->wsync.size(), plan->operand, (hipStream_t)stream),
+                   "wide operand copies");
 }
 
 int ipc_plan_launch_count(const ipc_plan* plan) { return plan ? plan->launches : 0; }

@@ -62,10 +62,13 @@ class IPCConfig:
     init: str = "kaiming_a_sqrt5"
     # Prediction-phase operand split for 16-bit operands over fp32 master
     # data: 1 plain, 2 = W as hi + lo terms, 3 = W and f(x) both split.  None
-    # picks 3 for narrow nets (every width <= 1024, latency-bound, the extra
-    # MFMAs are free) and 2 otherwise.
+    # picks 3 for narrow nets (every output width <= 128, L <= 16: the
+    # latency-bound whole-step kernel, where the extra MFMAs are free) and 2
+    # otherwise (the MFMA-bound wide path).
     pred_split: int | None = None
-    # Whole-step kernel for narrow nets: "auto" (when eligible), "on", "off".
+    # Kernel path: "auto" (whole-step kernel for narrow nets, else the wide
+    # GEMM path when eligible, else phased), "narrow" / "on", "wide",
+    # "phased" / "off".
     fused: str = "auto"
 
 
@@ -126,7 +129,8 @@ class HipIPC:
         if cfg.pred_split is not None:
             self.pred_split = int(cfg.pred_split)
         elif self._storage == nat.DT_F32 and self._operand != nat.DT_F32:
-            self.pred_split = 3 if max(int(d) for d in cfg.dims) <= 1024 else 2
+            narrow = len(cfg.dims) - 1 <= 16 and max(int(d) for d in cfg.dims[:-1]) <= 128
+            self.pred_split = 3 if narrow else 2
         else:
             self.pred_split = 1
         mode = str(cfg.weight_update_mode).lower()
@@ -187,6 +191,8 @@ class HipIPC:
             self._fused))
         self._plan = handle
         nbytes = int(nat.lib().ipc_plan_workspace_bytes(handle))
+        # zero-initialised (the wide path relies on zero padding); torch's
+        # allocations are 256-byte aligned as the plan requires
         self._workspace = (torch.zeros(((nbytes + 3) // 4,), dtype=torch.int32, device=self.device)
                            if nbytes else None)
         a = None if self.a is None else _ptr_array(self.a)
@@ -204,6 +210,20 @@ class HipIPC:
     def fused(self) -> bool:
         """True when the step runs as the whole-step kernel."""
         return self._plan is not None and bool(nat.lib().ipc_plan_fused(self._plan))
+
+    @property
+    def path(self) -> str | None:
+        """Kernel path of the bound plan: "narrow" (whole-step kernel), "wide"
+        (LDS-DMA MFMA phases over 16-bit operand copies) or "phased"."""
+        if self._plan is None:
+            return None
+        return nat.PATH_NAMES[int(nat.lib().ipc_plan_path(self._plan))]
+
+    def sync_operand_copies(self) -> None:
+        """Re-derive the wide path's 16-bit operand copies after ``x`` or ``w``
+        were written outside a step (no-op for the other paths)."""
+        if self._plan is not None:
+            nat.check(nat.lib().ipc_plan_sync(self._plan, nat.current_stream_handle(self.device)))
 
     def barrier_timeouts(self) -> int:
         """Non-zero if a grid-barrier wait of the whole-step kernel ever hit its
@@ -331,6 +351,8 @@ class HipIPC:
             raise RuntimeError("Call initialize_batch before precompile")
         backup = [[t.clone() for t in ts] for ts in (self.w, self.x, self.e)]
         a_backup = None if self.a is None else [t.clone() for t in self.a]
+        # the workspace holds the wide path's 16-bit operand copies
+        ws_backup = None if self._workspace is None else self._workspace.clone()
         self.step_initialized(collect_metrics=False)
         torch.cuda.synchronize(self.device)
         for dst_list, src_list in zip((self.w, self.x, self.e), backup):
@@ -339,6 +361,8 @@ class HipIPC:
         if a_backup is not None:
             for dst, src in zip(self.a, a_backup):
                 dst.copy_(src)
+        if ws_backup is not None:
+            self._workspace.copy_(ws_backup)
         torch.cuda.synchronize(self.device)
 
     def capture_graph(self, steps: int):

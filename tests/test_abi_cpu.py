@@ -19,7 +19,7 @@ HEADER = ROOT / "include" / "ipc_hip.h"
 
 def _declared_functions():
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^(?:int|void|const char\*)\s+(ipc_\w+)\s*\(", text, flags=re.M)))
+    return sorted(set(re.findall(r"^(?:int|void|long long|const char\*)\s+(ipc_\w+)\s*\(", text, flags=re.M)))
 
 
 def test_library_exports_every_declared_symbol():
@@ -135,6 +135,80 @@ def test_plan_validation():
     assert lib.ipc_plan_create(ctypes.byref(h), 3, dims, 128, 1, 1, 1, 2, 1e-4, 0.5, 1, 0, 1) == nat.ERR_CONFIG
     assert lib.ipc_plan_step(None, 1, None) == nat.ERR_NULL
     lib.ipc_plan_destroy(None)  # no-op
+
+
+def _wide_layout_bytes(dims, B, split2):
+    """The wide path's workspace layout restated: 256 bytes, then one 256-byte
+    aligned 16-bit buffer per operand copy, rows padded to 256, k to 64."""
+    pad = lambda v, m: (v + m - 1) // m * m  # noqa: E731
+    L = len(dims) - 1
+    total = 256
+
+    def add(rows, cols):
+        nonlocal total
+        total += pad(pad(rows, 256) * pad(cols, 64) * 2, 256)
+
+    for l in range(L):
+        add(dims[l], dims[l + 1])
+        if split2:
+            add(dims[l], dims[l + 1])
+        if l <= L - 2:
+            add(dims[l + 1], dims[l])
+    for l in range(1, L + 1):
+        add(dims[l], B)
+        add(B, dims[l])
+    for l in range(L):
+        add(dims[l], B)
+        if l <= L - 2:
+            add(B, dims[l])
+    return total
+
+
+def test_plan_path_selection_and_wide_workspace():
+    lib = _lib()
+    h = ctypes.c_void_p()
+    wide = (ctypes.c_int * 4)(1000, 4096, 4096, 4096)
+    # AUTO on a wide fp32-master / bf16-operand net with split 2 takes the wide path
+    assert lib.ipc_plan_create(ctypes.byref(h), 3, wide, 1024, 0, 2, 2, 2, 1e-4, 0.5, 1, 0, -1) == nat.IPC_OK
+    try:
+        assert lib.ipc_plan_path(h) == nat.PATH_WIDE and lib.ipc_plan_fused(h) == 0
+        assert lib.ipc_plan_workspace_bytes(h) == _wide_layout_bytes((1000, 4096, 4096, 4096), 1024, True)
+        assert lib.ipc_plan_sync(h, None) == nat.ERR_STATE  # unbound
+        arr = (ctypes.c_void_p * 4)(P, P, P, P)
+        assert lib.ipc_plan_bind(h, arr, arr, arr, None, None) == nat.ERR_NULL
+        assert "workspace" in nat.last_error()
+        assert lib.ipc_plan_bind(h, arr, arr, arr, None, P + 16) == nat.ERR_ALIGN
+    finally:
+        lib.ipc_plan_destroy(h)
+    # split 1 drops the W_lo copies; ragged sizes pad rows to 256 and k to 64
+    ragged = (7, 130, 65, 257)
+    rd = (ctypes.c_int * 4)(*ragged)
+    assert lib.ipc_plan_create(ctypes.byref(h), 3, rd, 37, 0, 1, 1, 1, 1e-4, 0.5, 1, 0, 2) == nat.IPC_OK
+    try:
+        assert lib.ipc_plan_path(h) == nat.PATH_WIDE
+        assert lib.ipc_plan_workspace_bytes(h) == _wide_layout_bytes(ragged, 37, False)
+    finally:
+        lib.ipc_plan_destroy(h)
+    # the wide path is refused for fp32 operands, split 3, the outer-product update and 16-bit storage
+    assert lib.ipc_plan_create(ctypes.byref(h), 3, wide, 1024, 0, 0, 1, 2, 1e-4, 0.5, 1, 0, 2) == nat.ERR_CONFIG
+    assert lib.ipc_plan_create(ctypes.byref(h), 3, wide, 1024, 0, 2, 3, 2, 1e-4, 0.5, 1, 0, 2) == nat.ERR_CONFIG
+    assert lib.ipc_plan_create(ctypes.byref(h), 3, wide, 8, 0, 2, 2, 2, 1e-4, 0.5, 1, 1, 2) == nat.ERR_CONFIG
+    assert lib.ipc_plan_create(ctypes.byref(h), 3, wide, 1024, 2, 2, 1, 2, 1e-4, 0.5, 1, 0, 2) == nat.ERR_CONFIG
+    assert lib.ipc_plan_create(ctypes.byref(h), 3, wide, 1024, 0, 2, 2, 2, 1e-4, 0.5, 1, 0, 3) == nat.ERR_CONFIG
+    # AUTO with split 3 falls back to the phased path (no workspace)
+    assert lib.ipc_plan_create(ctypes.byref(h), 3, wide, 1024, 0, 2, 3, 2, 1e-4, 0.5, 1, 0, -1) == nat.IPC_OK
+    try:
+        assert lib.ipc_plan_path(h) == nat.PATH_PHASED and lib.ipc_plan_workspace_bytes(h) == 0
+    finally:
+        lib.ipc_plan_destroy(h)
+    # a narrow net keeps the whole-step kernel under AUTO
+    narrow = (ctypes.c_int * 4)(10, 64, 64, 784)
+    assert lib.ipc_plan_create(ctypes.byref(h), 3, narrow, 128, 0, 1, 3, 2, 1e-4, 0.5, 1, 0, -1) == nat.IPC_OK
+    try:
+        assert lib.ipc_plan_path(h) == nat.PATH_NARROW
+    finally:
+        lib.ipc_plan_destroy(h)
+    assert lib.ipc_plan_path(None) == -1
 
 
 def test_check_maps_codes_to_exceptions():

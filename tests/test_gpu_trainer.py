@@ -166,6 +166,7 @@ def test_c4_wide_bf16_operands(seed):
     w0, x_in, y = _setup(dims, B, seed=seed, input_dist="normal")
     _x0, x_t, w_t, _e = _oracle_run(w0, x_in, y, "tanh", T)
     model, _ = _gpu_run(dims, w0, x_in, y, "tanh", T, torch.bfloat16)
+    assert model.path == "wide"
     s_err, dw_err = _errors(model, w0, x_t, w_t)
     print(f"c4 bf16 seed={seed} split={model.pred_split}: state_err={s_err:.3e} dW_err={dw_err:.3e}")
     assert s_err <= 2e-2 and dw_err <= 5e-3
