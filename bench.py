@@ -216,12 +216,20 @@ def main() -> int:
         tflops = flops_step / (w_ms * 1e-3) / 1e12
         wphase = time_phases(wmodel, reps=5, replays=3)
         wbf = phase_bytes_flops(wdims, WB)
+        wphases = {k: {"us": round(v, 2), "TFLOP/s": round(wbf[k][1] / (v * 1e-6) / 1e12, 2)}
+                   for k, v in wphase.items()}
+        wdom = max(wphase, key=wphase.get)
         wide = {"workload": "wide iPC MLP dims (1000,4096x4,4096), B=1024, tanh, bf16 operands, fp32 master, T=4",
+                "path": wmodel.path, "pred_split": wmodel.pred_split,
                 "ms_per_step": round(w_ms, 4), "samples_per_s": round(WB / (w_ms * 1e-3), 1),
                 "gflop_per_step": round(flops_step / 1e9, 3), "tflops": round(tflops, 2),
                 "frac_of_bf16_peak": round(tflops / BF16_PEAK_TFLOPS, 4),
-                "phases": {k: {"us": round(v, 2), "TFLOP/s": round(wbf[k][1] / (v * 1e-6) / 1e12, 2)}
-                           for k, v in wphase.items()}}
+                "phases": wphases,
+                # the dominant phase kernel against the dense bf16 MFMA peak
+                "roofline": {"bound": "mfma", "kernel": f"wide {wdom} phase", "achieved": wphases[wdom]["TFLOP/s"],
+                             "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                             "frac": round(wphases[wdom]["TFLOP/s"] / BF16_PEAK_TFLOPS, 4),
+                             "algorithmic_flops_per_launch": wbf[wdom][1], "avg_launch_us": wphases[wdom]["us"]}}
         log(f"wide: {wide}")
         del wmodel
 
