@@ -147,6 +147,98 @@ def cpu_baseline(dims, B, act, threads, warmup=20, steps=200, repeats=5):
     return B / med, med
 
 
+def sweep_point_bytes_flops(kind, M, K, B, save=False, s=2):
+    """Algorithmic HBM bytes and GEMM flops of one standalone kernel launch at
+    storage size s: P s(MK+KB+2MB), I s(MK+KB+3MB) (+MB with A_out),
+    W s(2MK+MB+KB)."""
+    flops = 2 * M * K * B
+    if kind == "pred":
+        return s * (M * K + K * B + 2 * M * B), flops
+    if kind == "infer":
+        return s * (M * K + K * B + 3 * M * B + (M * B if save else 0)), flops
+    return s * (2 * M * K + M * B + K * B), flops
+
+
+def time_launch(fn, reps, replays=3):
+    """Microseconds per launch of `fn` (one enqueue on the current stream),
+    from HIP events around graph replays of `reps` back-to-back launches."""
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(reps):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(replays):
+        graph.replay()
+    end.record(stream)
+    end.synchronize()
+    us = start.elapsed_time(end) * 1e3 / (reps * replays)
+    del graph
+    return us
+
+
+def kernel_sweep(sizes=(1024, 4096, 8192), batches=(256, 2048, 8192), acts=("tanh", "relu")):
+    """Per-kernel roofline sweep: prediction+error, transposed inference update
+    and weight update, each standalone at M=K in `sizes`, B in `batches`, bf16
+    storage and operands (fp32 accumulation), W ~ N(0, 1/K), states and errors
+    ~ N(0, 1), tanh/relu fused; the inference update with and without the saved
+    activation output, the weight update recomputing f(X) and reading a saved
+    A.  Each point's bound is min(MFMA peak, AI x HBM peak)."""
+    import torch
+
+    from lich_amd import kernels as K_
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device="cpu").manual_seed(0)
+    bf = torch.bfloat16
+    rows = []
+    for n in sizes:
+        for B in batches:
+            M = K = n
+            w = (torch.randn((M, K), generator=g) / K ** 0.5).to(dev, bf)
+            xu = torch.randn((K, B), generator=g).to(dev, bf)
+            xl = torch.randn((M, B), generator=g).to(dev, bf)
+            e = torch.randn((M, B), generator=g).to(dev, bf)
+            el = torch.randn((K, B), generator=g).to(dev, bf)
+            aout = torch.empty((M, B), device=dev, dtype=bf)
+            big = 2 * M * K * B > 2e11
+            reps = 3 if big else (10 if 2 * M * K * B > 1e10 else 50)
+            for act in acts:
+                cases = [("pred", False, lambda: K_.build_prediction_error(M, K, B, act, bf)(xu, w, xl, e))]
+                for save in (False, True):
+                    kern = K_.build_inference_update(M, K, B, act, bf, None, 0.5, save)
+                    wl = w  # W_lower is [K, M]; M == K here
+                    cases.append(("infer", save, (lambda kern=kern, save=save:
+                                                  kern(xl, e, wl, el, aout if save else None))))
+                for rec in (True, False):
+                    kern = K_.build_weight_update(M, K, B, act, bf, None, 1e-4, rec)
+                    cases.append(("weight", not rec, (lambda kern=kern: kern(w, e, xu))))
+                for kind, save, fn in cases:
+                    us = time_launch(fn, reps)
+                    nbytes, flops = sweep_point_bytes_flops(kind, M, K, B, save=save and kind == "infer")
+                    ai = flops / nbytes
+                    attain = min(BF16_PEAK_TFLOPS, ai * HBM_PEAK_GBS / 1e3)
+                    tf = flops / (us * 1e-6) / 1e12
+                    row = {"kernel": kind, "M": M, "K": K, "B": B, "act": act,
+                           "variant": ("save A_out" if save else "no A_out") if kind == "infer" else
+                           (("saved A" if save else "recompute f(X)") if kind == "weight" else "-"),
+                           "us": round(us, 2), "TFLOP/s": round(tf, 2), "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1),
+                           "AI": round(ai, 1), "bound": "mfma" if attain >= BF16_PEAK_TFLOPS else "hbm",
+                           "attainable_TFLOP/s": round(attain, 1), "frac": round(tf / attain, 4)}
+                    rows.append(row)
+                    log(f"sweep: {row}")
+            del w, xu, xl, e, el, aout
+            torch.cuda.empty_cache()
+    return rows
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -154,11 +246,20 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=400)
     ap.add_argument("--no-wide", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--sweep", action="store_true",
+                    help="run only the per-kernel roofline sweep (M=K in {1024,4096,8192}, "
+                         "B in {256,2048,8192}, bf16) and print it as one JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
               "(this build has no multi-GPU path)", file=sys.stderr)
         return 2
+    if args.sweep:
+        rows = kernel_sweep()
+        print(json.dumps({"sweep": "per-kernel roofline, bf16 storage/operands, fp32 accumulation",
+                          "peaks": {"bf16_TFLOP/s": BF16_PEAK_TFLOPS, "hbm_GB/s": HBM_PEAK_GBS},
+                          "rows": rows}), flush=True)
+        return 0
 
     import torch
 
