@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define IPC_ABI_VERSION 2
+#define IPC_ABI_VERSION 3
 
 /* status codes */
 #define IPC_OK 0
@@ -56,12 +56,20 @@ extern "C" {
 #define IPC_ACT_SILU 4
 #define IPC_ACT_GELU 5
 
-/* tile configurations of the MFMA GEMM family; IPC_TILE_AUTO picks by shape */
+/* tile configurations of the MFMA GEMM family; IPC_TILE_AUTO picks by shape.
+ * IPC_TILE_DMA_256x128 is the LDS-DMA kernel (256 x 128 tiles, 4 waves of
+ * 128 x 64, operands streamed HBM -> LDS without VGPR staging, transposed
+ * operands read with the LDS transpose read).  It serves 16-bit storage
+ * (storage == operand == fp16/bf16) with a contraction that is a multiple of
+ * 64, 16-byte aligned tensors and, for operands read transposed, a contiguous
+ * extent that is a multiple of 8; IPC_TILE_AUTO picks it whenever those hold,
+ * and asking for it otherwise is IPC_ERR_CONFIG. */
 #define IPC_TILE_AUTO (-1)
 #define IPC_TILE_32x32 0
 #define IPC_TILE_64x64 1
 #define IPC_TILE_128x128 2
-#define IPC_TILE_COUNT 3
+#define IPC_TILE_DMA_256x128 3
+#define IPC_TILE_COUNT 4
 
 /* weight-update backends of a plan */
 #define IPC_WMODE_GEMM 0
@@ -189,8 +197,8 @@ int ipc_plan_path(const ipc_plan* plan);
  * becomes non-zero if a barrier wait ever ran past its spin limit); in
  * recompute mode the whole-step kernel keeps the f(x[l]) values phase A
  * evaluates for the weight update after them.  The wide path keeps its
- * 16-bit operand copies there (W and W^T, f(x) and eps in both layouts,
- * zero padded); their padding must stay zero. */
+ * 16-bit operand copies there (W as hi and lo terms, W^T, f(x) and eps in
+ * both layouts, zero padded); their padding must stay zero. */
 long long ipc_plan_workspace_bytes(const ipc_plan* plan);
 
 /* Binds the caller's buffers: x and e hold L+1 pointers ([d_l, B] each; e[L]

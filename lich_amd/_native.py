@@ -23,7 +23,8 @@ ERR_NULL, ERR_SHAPE, ERR_DTYPE, ERR_ACT, ERR_ALIGN, ERR_DEVICE, ERR_LAUNCH, ERR_
 DT_F32, DT_F16, DT_BF16 = 0, 1, 2
 ACT_CODES = {"identity": 0, "linear": 0, "relu": 1, "tanh": 2, "sigmoid": 3, "silu": 4, "gelu": 5}
 TILE_AUTO = -1
-TILE_COUNT = 3
+TILE_DMA = 3
+TILE_COUNT = 4
 WMODE = {"gemm": 0, "outer": 1, "auto": 2}
 SPLIT_NONE, SPLIT_W, SPLIT_WX = 1, 2, 3
 PATH_AUTO, PATH_PHASED, PATH_NARROW, PATH_WIDE = -1, 0, 1, 2

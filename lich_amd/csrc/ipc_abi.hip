@@ -7,6 +7,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <initializer_list>
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
@@ -182,6 +183,55 @@ OuterProblem make_outer(void* w, const void* e, const void* xu, int M, int K, in
 
 constexpr int kOuterMaxB = 32;
 
+bool al16(const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; }
+bool al8(const void* q) { return q == nullptr || reinterpret_cast<uintptr_t>(q) % 8 == 0; }
+
+// The LDS-DMA kernel serves 16-bit storage whose contraction is a multiple of
+// WIDE_BK and whose operands stream in 16-byte chunks: aligned bases, row
+// strides (in elements) that are multiples of 8.
+bool dma_eligible(int storage, int contraction, std::initializer_list<const void*> operands,
+                  std::initializer_list<long long> strides) {
+  if (storage == IPC_DT_F32 || contraction % WIDE_BK != 0) return false;
+  for (const void* q : operands)
+    if (!al16(q)) return false;
+  for (long long ld : strides)
+    if (ld % 8 != 0) return false;
+  return true;
+}
+
+// Tile selection of a standalone call: returns 1 if the LDS-DMA kernel runs
+// it, 0 for the generic kernel (tile resolved), or an error.
+int select_tile(int& tile, bool eligible, long long M, long long N, long long groups) {
+  if (tile == IPC_TILE_DMA_256x128 && !eligible)
+    return fail(IPC_ERR_CONFIG,
+                "tile %d (LDS-DMA) needs 16-bit storage, a contraction that is a multiple of %d, 16-byte "
+                "aligned tensors and row lengths that are multiples of 8", IPC_TILE_DMA_256x128, WIDE_BK);
+  if (eligible && (tile == IPC_TILE_AUTO || tile == IPC_TILE_DMA_256x128)) return 1;
+  if (tile == IPC_TILE_AUTO) tile = pick_tile(M, N, groups);
+  return 0;
+}
+
+// One WideProblem per group of a standalone 16-bit call.
+std::vector<WideProblem> s16_groups(const WideProblem& q, int groups, long long a_gs, long long b_gs,
+                                    long long o_gs, long long x_gs, long long o2_gs) {
+  std::vector<WideProblem> v((size_t)groups, q);
+  for (int g = 0; g < groups; ++g) {
+    WideProblem& r = v[(size_t)g];
+    r.a = static_cast<const char*>(q.a) + 2 * g * a_gs;
+    r.b = static_cast<const char*>(q.b) + 2 * g * b_gs;
+    r.out = static_cast<char*>(q.out) + 2 * g * o_gs;
+    if (q.aux) r.aux = static_cast<const char*>(q.aux) + 2 * g * x_gs;
+    if (q.out2) r.out2 = static_cast<char*>(q.out2) + 2 * g * o2_gs;
+  }
+  return v;
+}
+
+int run_s16(int mode, const WideProblem& q, int groups, long long a_gs, long long b_gs, long long o_gs,
+            long long x_gs, long long o2_gs, int operand, int act, void* stream, const char* what) {
+  const std::vector<WideProblem> v = s16_groups(q, groups, a_gs, b_gs, o_gs, x_gs, o2_gs);
+  return launch_rc(launch_s16(mode, v.data(), groups, operand, act, (hipStream_t)stream), what);
+}
+
 }  // namespace
 
 // =========================================================================== C ABI
@@ -217,8 +267,19 @@ int ipc_pred_err(const void* x_upper, const void* w, const void* x_lower, void* 
   TRY(check_ptr(w, "w", es));
   TRY(check_ptr(x_lower, "x_lower", es));
   TRY(check_ptr(e, "e", es));
+  const int use_dma = select_tile(tile, dma_eligible(storage, K, {x_upper, w}, {K, B}), M, B, groups);
+  if (use_dma < 0) return use_dma;
+  if (use_dma) {
+    WideProblem q{};
+    q.M = M; q.N = B; q.K = K;
+    q.a = w; q.lda = K; q.a_lim = M;
+    q.b = x_upper; q.ldb = B; q.b_lim = B;
+    q.out = e; q.ldo = B; q.aux = x_lower; q.ldx = B;
+    q.vec = B % 4 == 0 && al8(e) && al8(x_lower);
+    return run_s16(S16_PRED, q, groups, (long long)M * K, (long long)K * B, (long long)M * B, (long long)M * B, 0,
+                   operand, act, stream, "ipc_pred_err");
+  }
   GemmProblem p = make_pf(KIND_PRED, x_upper, w, x_lower, e, M, K, B, groups, act, es);
-  if (tile == IPC_TILE_AUTO) tile = pick_tile(M, B, groups);
   return launch_rc(launch_gemm(&p, 1, storage, operand, effective_split(storage, operand, split), tile,
                                (hipStream_t)stream), "ipc_pred_err");
 }
@@ -234,8 +295,19 @@ int ipc_forward(const void* x_upper, const void* w, void* out, int M, int K, int
   TRY(check_ptr(x_upper, "x_upper", es));
   TRY(check_ptr(w, "w", es));
   TRY(check_ptr(out, "out", es));
+  const int use_dma = select_tile(tile, dma_eligible(storage, K, {x_upper, w}, {K, B}), M, B, groups);
+  if (use_dma < 0) return use_dma;
+  if (use_dma) {
+    WideProblem q{};
+    q.M = M; q.N = B; q.K = K;
+    q.a = w; q.lda = K; q.a_lim = M;
+    q.b = x_upper; q.ldb = B; q.b_lim = B;
+    q.out = out; q.ldo = B;
+    q.vec = B % 4 == 0 && al8(out);
+    return run_s16(S16_FWD, q, groups, (long long)M * K, (long long)K * B, (long long)M * B, 0, 0, operand, act,
+                   stream, "ipc_forward");
+  }
   GemmProblem p = make_pf(KIND_FWD, x_upper, w, nullptr, out, M, K, B, groups, act, es);
-  if (tile == IPC_TILE_AUTO) tile = pick_tile(M, B, groups);
   return launch_rc(launch_gemm(&p, 1, storage, operand, effective_split(storage, operand, split), tile,
                                (hipStream_t)stream), "ipc_forward");
 }
@@ -253,8 +325,21 @@ int ipc_infer_update(void* x, const void* e, const void* w_lower, const void* e_
   TRY(check_ptr(w_lower, "w_lower", es));
   TRY(check_ptr(e_lower, "e_lower", es));
   if (a_out) TRY(check_ptr(a_out, "a_out", es));
+  const int use_dma = select_tile(tile, dma_eligible(storage, K, {w_lower, e_lower}, {M, B}), M, B, groups);
+  if (use_dma < 0) return use_dma;
+  if (use_dma) {
+    WideProblem q{};
+    q.M = M; q.N = B; q.K = K;
+    q.a = w_lower; q.lda = M; q.a_lim = M;
+    q.b = e_lower; q.ldb = B; q.b_lim = B;
+    q.out = x; q.ldo = B; q.aux = e; q.ldx = B;
+    q.out2 = a_out; q.ld2 = B;
+    q.scal = gamma;
+    q.vec = B % 4 == 0 && al8(x) && al8(e) && al8(a_out);
+    return run_s16(S16_INFER, q, groups, (long long)K * M, (long long)K * B, (long long)M * B, (long long)M * B,
+                   (long long)M * B, operand, act, stream, "ipc_infer_update");
+  }
   GemmProblem p = make_inf(x, e, w_lower, e_lower, a_out, M, K, B, groups, gamma, act, es);
-  if (tile == IPC_TILE_AUTO) tile = pick_tile(M, B, groups);
   return launch_rc(launch_gemm(&p, 1, storage, operand, IPC_SPLIT_NONE, tile, (hipStream_t)stream),
                    "ipc_infer_update");
 }
@@ -269,8 +354,20 @@ int ipc_weight_update(void* w, const void* e, const void* x_upper, int M, int K,
   TRY(check_ptr(w, "w", es));
   TRY(check_ptr(e, "e", es));
   TRY(check_ptr(x_upper, "x_upper", es));
+  const int use_dma = select_tile(tile, dma_eligible(storage, B, {e, x_upper}, {B}), M, K, groups);
+  if (use_dma < 0) return use_dma;
+  if (use_dma) {
+    WideProblem q{};
+    q.M = M; q.N = K; q.K = B;
+    q.a = e; q.lda = B; q.a_lim = M;
+    q.b = x_upper; q.ldb = B; q.b_lim = K;
+    q.out = w; q.ldo = K;
+    q.scal = alpha;
+    q.vec = K % 4 == 0 && al8(w);
+    return run_s16(S16_WEIGHT, q, groups, (long long)M * B, (long long)K * B, (long long)M * K, 0, 0, operand,
+                   recompute ? act : IPC_ACT_IDENTITY, stream, "ipc_weight_update");
+  }
   GemmProblem p = make_wgt(w, e, x_upper, M, K, B, groups, alpha, recompute, act, es);
-  if (tile == IPC_TILE_AUTO) tile = pick_tile(M, K, groups);
   return launch_rc(launch_gemm(&p, 1, storage, operand, IPC_SPLIT_NONE, tile, (hipStream_t)stream),
                    "ipc_weight_update");
 }
@@ -336,34 +433,36 @@ bool wide_eligible(int storage, int operand, int split, int wmode, int B) {
 }
 
 // Workspace layout of the wide path: after the 256 bytes every plan reserves,
-// one 256-byte aligned buffer per 16-bit operand copy, rows padded to
-// WIDE_ROW_PAD and the contiguous (k) extent to WIDE_BK.
+// one 256-byte aligned buffer per 16-bit operand copy, rows and columns
+// padded to WIDE_PAD with zeros; every operand has a k-contiguous copy for
+// each GEMM that reads it.
 struct WideLayout {
-  struct Buf { long long off = -1, ld = 0; };
+  struct Buf { long long off = -1, ld = 0, rows = 0; };
   std::vector<Buf> wh, wl, wt, f, ft, e, et;
   long long total = 256;
 
   Buf add(long long rows, long long cols) {
     Buf b;
-    b.ld = wide_pad(cols, WIDE_BK);
+    b.ld = wide_pad(cols, WIDE_PAD);
+    b.rows = wide_pad(rows, WIDE_PAD);
     b.off = total;
-    total += wide_pad(wide_pad(rows, WIDE_ROW_PAD) * b.ld * 2, 256);
+    total += wide_pad(b.rows * b.ld * 2, 256);
     return b;
   }
   WideLayout(const std::vector<int>& d, int L, int B, bool split2) {
     wh.resize(L); wl.resize(L); wt.resize(L); f.resize(L + 1); ft.resize(L + 1); e.resize(L); et.resize(L);
     for (int l = 0; l < L; ++l) {
-      wh[l] = add(d[l], d[l + 1]);                      // [d_l][d_{l+1}]   pred A
-      if (split2) wl[l] = add(d[l], d[l + 1]);          //                  pred A_lo
-      if (l <= L - 2) wt[l] = add(d[l + 1], d[l]);      // [d_{l+1}][d_l]   infer A (layer l+1)
+      wh[l] = add(d[l], d[l + 1]);                  // [d_l][d_{l+1}]  pred A
+      if (split2) wl[l] = add(d[l], d[l + 1]);      //                 pred A_lo
+      if (l <= L - 2) wt[l] = add(d[l + 1], d[l]);  // [d_{l+1}][d_l]  infer A (layer l+1)
     }
     for (int l = 1; l <= L; ++l) {
-      f[l] = add(d[l], B);                              // [d_l][B]         weight B (layer l-1)
-      ft[l] = add(B, d[l]);                             // [B][d_l]         pred B (layer l-1)
+      f[l] = add(d[l], B);                      // [d_l][B]        weight B (layer l-1)
+      ft[l] = add(B, d[l]);                     // [B][d_l]        pred B (layer l-1)
     }
     for (int l = 0; l < L; ++l) {
-      e[l] = add(d[l], B);                              // [d_l][B]         weight A
-      if (l <= L - 2) et[l] = add(B, d[l]);             // [B][d_l]         infer B (layer l+1)
+      e[l] = add(d[l], B);                      // [d_l][B]        weight A
+      if (l <= L - 2) et[l] = add(B, d[l]);     // [B][d_l]        infer B (layer l+1)
     }
   }
 };
@@ -542,11 +641,11 @@ int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w
     plan->wpred.clear(); plan->winfer.clear(); plan->wweight.clear(); plan->wsync.clear();
     for (int l = 0; l < L; ++l) {
       WideProblem q{};
-      q.M = d[l]; q.N = B; q.K = (int)wide_pad(d[l + 1], WIDE_BK);
-      q.a = buf(lay.wh[l]); q.a_lo = buf(lay.wl[l]); q.lda = lay.wh[l].ld;
-      q.b = buf(lay.ft[l + 1]); q.ldb = lay.ft[l + 1].ld;
-      q.out = static_cast<float*>(e[l]); q.ldo = B;
-      q.aux = static_cast<const float*>(x[l]); q.ldx = B;
+      q.M = d[l]; q.N = B; q.K = (int)lay.wh[l].ld;
+      q.a = buf(lay.wh[l]); q.a_lo = buf(lay.wl[l]); q.lda = lay.wh[l].ld; q.a_lim = (int)lay.wh[l].rows;
+      q.b = buf(lay.ft[l + 1]); q.ldb = lay.ft[l + 1].ld; q.b_lim = (int)lay.ft[l + 1].rows;
+      q.out = e[l]; q.ldo = B;
+      q.aux = x[l]; q.ldx = B;
       q.h = buf(lay.e[l]); q.ldh = lay.e[l].ld;
       q.t = buf(lay.et[l]); q.ldt = lay.et[l].ld;
       q.vec = B % 4 == 0 && a16(e[l]) && a16(x[l]);
@@ -554,24 +653,24 @@ int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w
     }
     for (int l = 1; l < L; ++l) {
       WideProblem q{};
-      q.M = d[l]; q.N = B; q.K = (int)wide_pad(d[l - 1], WIDE_BK);
-      q.a = buf(lay.wt[l - 1]); q.lda = lay.wt[l - 1].ld;
-      q.b = buf(lay.et[l - 1]); q.ldb = lay.et[l - 1].ld;
-      q.out = static_cast<float*>(x[l]); q.ldo = B;
-      q.aux = static_cast<const float*>(e[l]); q.ldx = B;
+      q.M = d[l]; q.N = B; q.K = (int)lay.wt[l - 1].ld;
+      q.a = buf(lay.wt[l - 1]); q.lda = lay.wt[l - 1].ld; q.a_lim = (int)lay.wt[l - 1].rows;
+      q.b = buf(lay.et[l - 1]); q.ldb = lay.et[l - 1].ld; q.b_lim = (int)lay.et[l - 1].rows;
+      q.out = x[l]; q.ldo = B;
+      q.aux = e[l]; q.ldx = B;
       q.h = buf(lay.f[l]); q.ldh = lay.f[l].ld;
       q.t = buf(lay.ft[l]); q.ldt = lay.ft[l].ld;
-      q.out2 = plan->recompute ? nullptr : static_cast<float*>(a[l]); q.ld2 = B;
+      q.out2 = plan->recompute ? nullptr : a[l]; q.ld2 = B;
       q.scal = plan->gamma;
       q.vec = B % 4 == 0 && a16(x[l]) && a16(e[l]) && (!q.out2 || a16(q.out2));
       plan->winfer.push_back(q);
     }
     for (int l = 0; l < L; ++l) {
       WideProblem q{};
-      q.M = d[l]; q.N = d[l + 1]; q.K = (int)wide_pad(B, WIDE_BK);
-      q.a = buf(lay.e[l]); q.lda = lay.e[l].ld;
-      q.b = buf(lay.f[l + 1]); q.ldb = lay.f[l + 1].ld;
-      q.out = static_cast<float*>(w[l]); q.ldo = d[l + 1];
+      q.M = d[l]; q.N = d[l + 1]; q.K = (int)lay.e[l].ld;
+      q.a = buf(lay.e[l]); q.lda = lay.e[l].ld; q.a_lim = (int)lay.e[l].rows;
+      q.b = buf(lay.f[l + 1]); q.ldb = lay.f[l + 1].ld; q.b_lim = (int)lay.f[l + 1].rows;
+      q.out = w[l]; q.ldo = d[l + 1];
       q.h = buf(lay.wh[l]); q.ldh = lay.wh[l].ld;
       q.hl = buf(lay.wl[l]); q.ldhl = lay.wl[l].ld;
       q.t = buf(lay.wt[l]); q.ldt = lay.wt[l].ld;
@@ -601,7 +700,7 @@ int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w
     plan->wfwd.clear();
     for (int l = L - 1; l >= 1; --l) {
       WideProblem q = plan->wpred[l];
-      q.out = static_cast<float*>(x[l]); q.ldo = B;
+      q.out = x[l]; q.ldo = B;
       q.aux = nullptr; q.ldx = 0;
       q.h = buf(lay.f[l]); q.ldh = lay.f[l].ld;
       q.t = buf(lay.ft[l]); q.ldt = lay.ft[l].ld;

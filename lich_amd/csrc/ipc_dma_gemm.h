@@ -1,0 +1,549 @@
+// ipc_dma_gemm.h - the LDS-DMA MFMA GEMM kernel template (gfx950).
+//
+// One workgroup = WGM x WGN waves = one BM x BN output tile; each wave owns
+// (BM/WGM) x (BN/WGN) of it as 32x32 fp32 MFMA blocks
+// (v_mfma_f32_32x32x16_{f16,bf16}).  Main loop, per k-step of 64:
+//
+//   * operands move HBM -> LDS with global_load_lds_dwordx4 (LDS DMA: no VGPR
+//     staging), S stages deep; one wave instruction fills 1 KB of LDS.  An
+//     operand that needs its activation applied (f(X_upper) of the
+//     standalone pred / weight kernels) instead goes global -> VGPR ->
+//     f -> LDS, loaded one stage ahead and stored after the current stage's
+//     MFMAs;
+//   * a k-contiguous operand block is EDGE rows of 128 bytes, 16-byte chunk c
+//     of row r stored at chunk c ^ ((r >> 1) & 7): a 16-byte fragment read by
+//     16 lanes of 16 consecutive rows touches each of the 64 LDS banks once;
+//   * an m/n-contiguous block is 64 k-rows of 2*EDGE bytes, chunk c of k-row
+//     r at chunk c ^ ((r & 3) << 2); its fragments come from two
+//     ds_read_b64_tr_b16 (16 lanes read a 4 x 16 block, one 8-byte row piece
+//     each, and get its columns back), and the swizzle spreads the 4 k-rows of
+//     a half-wave over distinct banks;
+//   * one workgroup barrier per k-step without the fence of __syncthreads
+//     (that fence would make the compiler wait for every outstanding DMA
+//     load): a wave waits for its own loads of the step it is about to read
+//     (s_waitcnt vmcnt), the barrier publishes everybody's, then it refills
+//     the stage everybody has finished with;
+//   * fragments of the next 16-k slice are read while the current slice's
+//     MFMAs run; split 2 adds the A_lo B products (error compensation);
+//   * workgroups are renumbered so that the tiles one XCD runs are consecutive
+//     (the tiles sharing rows of A share that XCD's L2).
+//
+// Epilogue: the accumulator tile goes through LDS (the stages are free by
+// then) so that every global access is a coalesced row-major 4-column group;
+// the fp32 input the epilogue updates is fetched into registers before the
+// main loop.  Reference semantics: src/ipc_tilelang/tilelang_kernels.py:173
+// (prediction error), :227-231 (inference update), :319-320 (weight update);
+// the fp32 rounding sequence is that of src/ipc_tilelang/reference.py:49-57,
+// every operation rounded on its own (no FMA contraction).
+#pragma once
+
+#include "ipc_device.h"
+#include "ipc_launch.h"
+#include "ipc_wide.h"
+
+namespace ipc {
+namespace dma {
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) void glb_void;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Workgroup barrier without the fence of __syncthreads.
+__device__ __forceinline__ void wg_barrier() {
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Operand layouts: A is m-contiguous (read transposed) for the standalone
+// inference update (W_lower [K][M]), k-contiguous otherwise; B is
+// n-contiguous for the standalone prediction / forward / inference kernels
+// (X_upper, E_lower [K][B]), k-contiguous for the weight update.  The wide
+// path keeps k-contiguous copies of every operand (WT, FT, ET next to W, F,
+// E), so all of its reads are plain 16-byte fragment reads.
+constexpr bool a_mn(int mode) { return mode == S16_INFER; }
+constexpr bool b_mn(int mode) { return mode == S16_PRED || mode == S16_FWD || mode == S16_INFER; }
+constexpr bool is_s16(int mode) { return mode >= S16_PRED; }
+
+// chunk position of chunk c in row r
+__device__ __forceinline__ int kc_swz(int r, int c) { return c ^ ((r >> 1) & 7); }
+__device__ __forceinline__ int mn_swz(int r, int c) { return c ^ ((r & 3) << 2); }
+
+// Global source of LDS slot `slot` (16 bytes) of an operand block.
+//   KC: rows e0 .. e0+EDGE-1 (clamped to lim-1), k0 .. k0+63
+//   MN: k-rows k0 .. k0+63, columns e0 .. e0+EDGE-1 (chunk starts clamped to lim-8)
+template <typename OT, bool MN, int EDGE>
+__device__ __forceinline__ const OT* slot_src(const OT* g, long long ld, int e0, int lim, int k0, int slot) {
+  if (!MN) {
+    const int r = slot >> 3, c = kc_swz(r, slot & 7);
+    const int row = e0 + r < lim ? e0 + r : lim - 1;
+    return g + (long long)row * ld + k0 + c * 8;
+  } else {
+    constexpr int CPR = EDGE / 8;  // chunks per k-row
+    const int r = slot / CPR, c = mn_swz(r, slot % CPR);
+    const int col = e0 + c * 8 <= lim - 8 ? e0 + c * 8 : lim - 8;
+    return g + (long long)(k0 + r) * ld + col;
+  }
+}
+
+template <typename OT>
+__device__ __forceinline__ unsigned pack2(OT a, OT b) {
+  return (unsigned)__builtin_bit_cast(unsigned short, a) | ((unsigned)__builtin_bit_cast(unsigned short, b) << 16);
+}
+
+template <typename OT>
+__device__ __forceinline__ float lo16(unsigned v) {
+  return to_f32(__builtin_bit_cast(OT, (unsigned short)(v & 0xffffu)));
+}
+template <typename OT>
+__device__ __forceinline__ float hi16(unsigned v) {
+  return to_f32(__builtin_bit_cast(OT, (unsigned short)(v >> 16)));
+}
+
+// Dynamic LDS of a configuration: the pipeline stages, reused by the fp32
+// epilogue tile (BM rows of BN + 1 floats).
+constexpr int smem_bytes(int BM, int BN, int S, bool LO) {
+  return S * (BM * 128 * (LO ? 2 : 1) + BN * 128) > BM * (BN + 1) * 4 ? S * (BM * 128 * (LO ? 2 : 1) + BN * 128)
+                                                                     : BM * (BN + 1) * 4;
+}
+
+struct Batch {
+  WideProblem p[WIDE_MAX_BATCH];
+  int start[WIDE_MAX_BATCH + 1];  // first tile of each problem
+  int count;
+};
+
+// ACT: the epilogue activation (WIDE_INFER, WIDE_FWD, S16_INFER) or the
+// activation of the register-path B operand (BREG: S16_PRED, S16_FWD,
+// S16_WEIGHT recompute); ACT_IDENTITY otherwise.
+template <typename OT, int MODE, int SPLIT, int ACT, bool BREG, int BM, int BN, int S, int WGM, int WGN>
+__global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  constexpr bool LO = SPLIT == 2;
+  constexpr bool AMN = a_mn(MODE), BMN = b_mn(MODE), S16 = is_s16(MODE);
+  constexpr int NW = WGM * WGN, NT = NW * 64;
+  constexpr int A_BYTES = BM * 128, B_BYTES = BN * 128;
+  constexpr int STAGE = A_BYTES * (LO ? 2 : 1) + B_BYTES;
+  constexpr int IA = A_BYTES / 1024 / NW, IB = B_BYTES / 1024 / NW;  // DMA instructions per wave and stage
+  constexpr int LPS = IA * (LO ? 2 : 1) + (BREG ? 0 : IB);
+  constexpr int RB = B_BYTES / 16 / NT;                               // register-path chunks per thread
+  constexpr int WTM = BM / WGM, WTN = BN / WGN, RM = WTM / 32, RN = WTN / 32;
+  using MF = Mfma32<OT>;
+  typedef typename MF::operand V;
+  static_assert(S >= 2 && IA * 1024 * NW == A_BYTES && IB * 1024 * NW == B_BYTES && RB * 16 * NT == B_BYTES,
+                "tile / wave count");
+  static_assert(WTM % 32 == 0 && WTN % 32 == 0 && BM % 128 == 0 && BN % 128 == 0, "tile");
+  static_assert(!BREG || S16, "register-path operands belong to the standalone kernels");
+
+  // XCD-aware renumbering: workgroup b runs on XCD b % 8; give every XCD a
+  // contiguous range of tiles.
+  const int G = gridDim.x, b = blockIdx.x;
+  const int xcd = b & 7, per = G >> 3, rem = G & 7;
+  const int tile = xcd * per + (xcd < rem ? xcd : rem) + (b >> 3);
+  int pi = 0;
+#pragma unroll 1
+  while (pi + 1 < bt.count && tile >= bt.start[pi + 1]) ++pi;
+  const WideProblem& p = bt.p[pi];
+  const int tn = (p.N + BN - 1) / BN;
+  const int local = tile - bt.start[pi];
+  const int m0 = (local / tn) * BM, n0 = (local % tn) * BN;
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int wm = w / WGN, wn = w % WGN;
+  const OT* A = reinterpret_cast<const OT*>(p.a);
+  const OT* Al = reinterpret_cast<const OT*>(p.a_lo);
+  const OT* Bg = reinterpret_cast<const OT*>(p.b);
+  const long long lda = p.lda, ldb = p.ldb;
+  const int alim = p.a_lim, blim = p.b_lim;
+  const int nk = p.K / WIDE_BK;
+
+  auto issue_dma = [&](int kt, int stage) {
+    unsigned char* st = smem + stage * STAGE;
+    const int k0 = kt * WIDE_BK;
+#pragma unroll
+    for (int q = 0; q < IA; ++q) {
+      const int blk = q * NW + w;
+      const OT* src = slot_src<OT, AMN, BM>(A, lda, m0, alim, k0, blk * 64 + lane);
+      __builtin_amdgcn_global_load_lds((glb_void*)src, (lds_void*)(st + blk * 1024), 16, 0, 0);
+      if (LO) {
+        const OT* srl = slot_src<OT, AMN, BM>(Al, lda, m0, alim, k0, blk * 64 + lane);
+        __builtin_amdgcn_global_load_lds((glb_void*)srl, (lds_void*)(st + A_BYTES + blk * 1024), 16, 0, 0);
+      }
+    }
+    if (!BREG) {
+#pragma unroll
+      for (int q = 0; q < IB; ++q) {
+        const int blk = q * NW + w;
+        const OT* src = slot_src<OT, BMN, BN>(Bg, ldb, n0, blim, k0, blk * 64 + lane);
+        __builtin_amdgcn_global_load_lds((glb_void*)src, (lds_void*)(st + A_BYTES * (LO ? 2 : 1) + blk * 1024),
+                                         16, 0, 0);
+      }
+    }
+  };
+  // register path of the B operand: 16-byte chunks of the stage's B block
+  uint4 breg[BREG ? RB : 1];
+  auto issue_breg = [&](int kt) {
+    if (BREG) {
+#pragma unroll
+      for (int i = 0; i < RB; ++i)
+        breg[i] = *reinterpret_cast<const uint4*>(
+            slot_src<OT, BMN, BN>(Bg, ldb, n0, blim, kt * WIDE_BK, i * NT + tid));
+    }
+  };
+  auto store_breg = [&](int stage) {
+    if (BREG) {
+      unsigned char* sb = smem + stage * STAGE + A_BYTES * (LO ? 2 : 1);
+#pragma unroll
+      for (int i = 0; i < RB; ++i) {
+        const unsigned in[4] = {breg[i].x, breg[i].y, breg[i].z, breg[i].w};
+        unsigned o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          o[j] = pack2(cvt<OT>(act_t<ACT>(lo16<OT>(in[j]))), cvt<OT>(act_t<ACT>(hi16<OT>(in[j]))));
+        *reinterpret_cast<uint4*>(sb + (i * NT + tid) * 16) = make_uint4(o[0], o[1], o[2], o[3]);
+      }
+    }
+  };
+
+  // The epilogue's input (x for pred / infer, W for weight) is fetched now,
+  // ahead of the main loop, in the row-major 4-column groups the epilogue
+  // walks: its latency hides behind the MFMAs.
+  constexpr int IT = BM * BN / 4 / NT, CH = IT < 8 ? IT : 8;
+  static_assert(IT % CH == 0 && IT * 4 * NT == BM * BN, "epilogue groups");
+  const int M = p.M, N = p.N;
+  const bool vec = p.vec != 0;
+  auto load_group = [&](const void* basev, long long ld, int u, float (&o)[4]) {
+    const int idx = u * NT + tid;
+    const int r = idx / (BN / 4), col = (idx % (BN / 4)) * 4;
+    const int m = m0 + r, n = n0 + col;
+    const int nv = (m < M && n < N) ? (N - n < 4 ? N - n : 4) : 0;
+    if (S16) {
+      const OT* src = reinterpret_cast<const OT*>(basev) + (long long)m * ld + n;
+      if (vec && nv == 4) {
+        const uint2 t2 = *reinterpret_cast<const uint2*>(src);
+        o[0] = lo16<OT>(t2.x); o[1] = hi16<OT>(t2.x); o[2] = lo16<OT>(t2.y); o[3] = hi16<OT>(t2.y);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) o[q] = q < nv ? to_f32(src[q]) : 0.0f;
+      }
+    } else {
+      const float* src = reinterpret_cast<const float*>(basev) + (long long)m * ld + n;
+      if (vec && nv == 4) {
+        const float4 t4 = *reinterpret_cast<const float4*>(src);
+        o[0] = t4.x; o[1] = t4.y; o[2] = t4.z; o[3] = t4.w;
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) o[q] = q < nv ? src[q] : 0.0f;
+      }
+    }
+  };
+  constexpr bool PRE = MODE != WIDE_FWD && MODE != S16_FWD;
+  const bool pre_from_aux = MODE == WIDE_PRED || MODE == S16_PRED;
+  float pre[PRE ? IT : 1][4];
+  if (PRE) {
+#pragma unroll
+    for (int u = 0; u < IT; ++u)
+      load_group(pre_from_aux ? p.aux : p.out, pre_from_aux ? p.ldx : p.ldo, u, pre[PRE ? u : 0]);
+  }
+
+  f32x16 acc[RM][RN];
+#pragma unroll
+  for (int i = 0; i < RM; ++i)
+#pragma unroll
+    for (int j = 0; j < RN; ++j)
+#pragma unroll
+      for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.0f;
+
+  // prologue: stages 0 .. S-2
+#pragma unroll
+  for (int s = 0; s < S - 1; ++s) {
+    if (s < nk) {
+      issue_breg(s);
+      issue_dma(s, s);
+      if (BREG) {
+        wait_vmcnt<LPS>();
+        store_breg(s);
+      }
+    }
+  }
+
+  // lane-constant parts of the fragment addresses
+  const int lr = lane & 31, lk = lane >> 5;         // k-contiguous reads: row, 8-k half
+  const int kc_sw = (lr >> 1) & 7;
+  const int g4 = lane >> 4, li = lane & 15;          // transposing reads: 16-lane group, lane in group
+  const int tr_row = 8 * (g4 >> 1) + (li >> 2);      // k-row within the 16-k slice (+4 for the second read)
+  const int tr_low = 2 * (g4 & 1) + ((li & 3) >> 1); // chunk within the 4-chunk group of a 32-wide block
+  const int tr_half = (li & 1) * 8, tr_x = li >> 2;  // byte in chunk, swizzle of the 4-chunk group
+  auto frag_kc = [&](const unsigned char* blk, int row0, int kk) -> V {
+    return *reinterpret_cast<const V*>(blk + (row0 + lr) * 128 + (((kk * 2 + lk) ^ kc_sw) << 4));
+  };
+  auto frag_mn = [&](const unsigned char* blk, int rowb, int col0, int kk) -> V {
+    // col0: first column of the 32-wide block (multiple of 32)
+    const int chunk = ((((col0 >> 5) ^ tr_x)) << 2) | tr_low;
+    const unsigned char* p0 = blk + (kk * 16 + tr_row) * rowb + (chunk << 4) + tr_half;
+    const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p0));
+    const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p0 + 4 * rowb));
+    const s16x8 v = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_bit_cast(V, v);
+  };
+  auto frag_a = [&](const unsigned char* blk, int i, int kk) -> V {
+    if (AMN) return frag_mn(blk, BM * 2, wm * WTM + i * 32, kk);
+    return frag_kc(blk, wm * WTM + i * 32, kk);
+  };
+  auto frag_b = [&](const unsigned char* blk, int j, int kk) -> V {
+    if (BMN) return frag_mn(blk, BN * 2, wn * WTN + j * 32, kk);
+    return frag_kc(blk, wn * WTN + j * 32, kk);
+  };
+
+  int stage = 0, fill = S - 1;
+#pragma unroll 1
+  for (int kt = 0; kt < nk; ++kt) {
+    // this wave's DMA loads of step kt are done once at most S-2 later steps are in flight
+    if (kt + S - 2 < nk) wait_vmcnt<(S - 2) * LPS>();
+    else wait_vmcnt<0>();
+    wg_barrier();
+    const bool refill = kt + S - 1 < nk;
+    if (refill) {
+      issue_breg(kt + S - 1);
+      issue_dma(kt + S - 1, fill);
+    }
+
+    const unsigned char* sa = smem + stage * STAGE;
+    const unsigned char* sal = sa + A_BYTES;
+    const unsigned char* sb = sa + A_BYTES * (LO ? 2 : 1);
+    V af[2][RM], bf[2][RN], alf[2][LO ? RM : 1];
+    // Software pipeline over the 16-k slices of the stage: the reads of
+    // slice kk+1 go out while slice kk's MFMAs run.  A scheduling barrier
+    // between slices keeps the compiler from sinking the reads next to their
+    // first use (which would expose the LDS latency once per MFMA pair).
+#pragma unroll
+    for (int j = 0; j < RN; ++j) bf[0][j] = frag_b(sb, j, 0);
+#pragma unroll
+    for (int i = 0; i < RM; ++i) {
+      af[0][i] = frag_a(sa, i, 0);
+      if (LO) alf[0][i] = frag_a(sal, i, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int kk = 0; kk < WIDE_BK / 16; ++kk) {
+      const int cur = kk & 1, nxt = cur ^ 1;
+      if (kk + 1 < WIDE_BK / 16) {
+#pragma unroll
+        for (int j = 0; j < RN; ++j) bf[nxt][j] = frag_b(sb, j, kk + 1);
+#pragma unroll
+        for (int i = 0; i < RM; ++i) {
+          af[nxt][i] = frag_a(sa, i, kk + 1);
+          if (LO) alf[nxt][i] = frag_a(sal, i, kk + 1);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < RM; ++i)
+#pragma unroll
+        for (int j = 0; j < RN; ++j) acc[i][j] = MF::run(af[cur][i], bf[cur][j], acc[i][j]);
+      if (LO) {
+#pragma unroll
+        for (int i = 0; i < RM; ++i)
+#pragma unroll
+          for (int j = 0; j < RN; ++j) acc[i][j] = MF::run(alf[cur][i], bf[cur][j], acc[i][j]);
+      }
+      if (kk + 1 < WIDE_BK / 16) {
+        // one LDS read between consecutive MFMAs, as far as the reads go
+        constexpr int NLD = RM * (LO ? 2 : 1) * (AMN ? 2 : 1) + RN * (BMN ? 2 : 1);
+        constexpr int NMF = RM * RN * (LO ? 2 : 1);
+#pragma unroll
+        for (int q = 0; q < NMF; ++q) {
+          if (q < NLD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        }
+        if (NLD > NMF) __builtin_amdgcn_sched_group_barrier(0x100, NLD > NMF ? NLD - NMF : 1, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (BREG && refill) {
+      // the register loads were issued before this step's DMA loads
+      wait_vmcnt<LPS>();
+      store_breg(fill);
+    }
+    stage = stage + 1 == S ? 0 : stage + 1;
+    fill = fill + 1 == S ? 0 : fill + 1;
+  }
+
+  // ------------------------------------------------------------ epilogue
+  // The accumulator tile goes through LDS (the pipeline stages are free now)
+  // so that every global access of the epilogue is coalesced: pass 1 walks
+  // the tile row-major, 4 columns per thread (fp32 master, natural 16-bit
+  // copy), pass 2 column-major (the transposed 16-bit copy of the wide path).
+  constexpr int CS = BN + 1;  // fp32 row stride: conflict-free column walk in pass 2
+  static_assert(BM * CS * 4 <= smem_bytes(BM, BN, S, LO), "epilogue tile exceeds the LDS");
+  float* cs = reinterpret_cast<float*>(smem);
+  wait_vmcnt<0>();
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < RM; ++i)
+#pragma unroll
+    for (int j = 0; j < RN; ++j)
+#pragma unroll
+      for (int q = 0; q < 16; ++q)
+        cs[(wm * WTM + i * 32 + 8 * (q >> 2) + 4 * lk + (q & 3)) * CS + wn * WTN + j * 32 + lr] = acc[i][j][q];
+  __syncthreads();
+
+#pragma unroll
+  for (int c0 = 0; c0 < IT; c0 += CH) {
+    float ein[CH][4];
+    if (MODE == WIDE_INFER || MODE == S16_INFER) {
+#pragma unroll
+      for (int u = 0; u < CH; ++u) load_group(p.aux, p.ldx, c0 + u, ein[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const int idx = (c0 + u) * NT + tid;
+      const int r = idx / (BN / 4), col = (idx % (BN / 4)) * 4;
+      const int m = m0 + r, n = n0 + col;
+      if (m >= M || n >= N) continue;
+      const int nv = N - n < 4 ? N - n : 4;
+      float* cr = cs + r * CS + col;
+      float v[4], fv[4];
+      OT hv[4], lv[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+#pragma clang fp contract(off)
+        const float a = cr[q];
+        const float x = PRE ? pre[PRE ? c0 + u : 0][q] : 0.0f;
+        if (MODE == WIDE_PRED) {
+          v[q] = x - a;                                              // eps
+          hv[q] = cvt<OT>(v[q]);
+        } else if (MODE == WIDE_INFER) {
+          v[q] = x + p.scal * (-ein[u][q] + dact_t<ACT>(x) * a);    // x_new
+          fv[q] = act_t<ACT>(v[q]);
+          hv[q] = cvt<OT>(fv[q]);
+        } else if (MODE == WIDE_FWD) {
+          v[q] = a;                                                  // x = W f(x_upper)
+          fv[q] = act_t<ACT>(v[q]);
+          hv[q] = cvt<OT>(fv[q]);
+        } else if (MODE == WIDE_WEIGHT) {
+          v[q] = x + p.scal * a;                                     // W_new
+          hv[q] = cvt<OT>(v[q]);
+          lv[q] = cvt<OT>(v[q] - to_f32(hv[q]));
+        } else if (MODE == S16_PRED) {
+          // tilelang_kernels.py:173: E = cast(X_lower) - cast(acc) in storage precision
+          hv[q] = cvt<OT>(x - to_f32(cvt<OT>(a)));
+        } else if (MODE == S16_FWD) {
+          hv[q] = cvt<OT>(a);
+        } else if (MODE == S16_INFER) {
+          const float xn = x + p.scal * (-ein[u][q] + dact_t<ACT>(x) * a);
+          hv[q] = cvt<OT>(xn);
+          lv[q] = cvt<OT>(act_t<ACT>(xn));                            // A_out
+        } else {
+          // tilelang_kernels.py:319-320: W = cast(float(W) + alpha * acc)
+          hv[q] = cvt<OT>(x + p.scal * a);
+        }
+        if (!S16) cr[q] = to_f32(hv[q]);  // the value the transposed copy takes
+      }
+      if (!S16) {
+        float* op = reinterpret_cast<float*>(p.out) + (long long)m * p.ldo + n;
+        OT* hp = reinterpret_cast<OT*>(p.h) + (long long)m * p.ldh + n;
+        if (vec && nv == 4) {
+          *reinterpret_cast<float4*>(op) = make_float4(v[0], v[1], v[2], v[3]);
+          uint2 hh; hh.x = pack2(hv[0], hv[1]); hh.y = pack2(hv[2], hv[3]);
+          *reinterpret_cast<uint2*>(hp) = hh;
+          if (MODE == WIDE_WEIGHT && p.hl) {
+            uint2 ll; ll.x = pack2(lv[0], lv[1]); ll.y = pack2(lv[2], lv[3]);
+            *reinterpret_cast<uint2*>(reinterpret_cast<OT*>(p.hl) + (long long)m * p.ldhl + n) = ll;
+          }
+          if (MODE == WIDE_INFER && p.out2)
+            *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.out2) + (long long)m * p.ld2 + n) =
+                make_float4(fv[0], fv[1], fv[2], fv[3]);
+        } else {
+          for (int q = 0; q < nv; ++q) {
+            op[q] = v[q];
+            hp[q] = hv[q];
+            if (MODE == WIDE_WEIGHT && p.hl) reinterpret_cast<OT*>(p.hl)[(long long)m * p.ldhl + n + q] = lv[q];
+            if (MODE == WIDE_INFER && p.out2) reinterpret_cast<float*>(p.out2)[(long long)m * p.ld2 + n + q] = fv[q];
+          }
+        }
+      } else {
+        OT* op = reinterpret_cast<OT*>(p.out) + (long long)m * p.ldo + n;
+        OT* o2 = MODE == S16_INFER && p.out2 ? reinterpret_cast<OT*>(p.out2) + (long long)m * p.ld2 + n : nullptr;
+        if (vec && nv == 4) {
+          uint2 hh; hh.x = pack2(hv[0], hv[1]); hh.y = pack2(hv[2], hv[3]);
+          *reinterpret_cast<uint2*>(op) = hh;
+          if (o2) {
+            uint2 ll; ll.x = pack2(lv[0], lv[1]); ll.y = pack2(lv[2], lv[3]);
+            *reinterpret_cast<uint2*>(o2) = ll;
+          }
+        } else {
+          for (int q = 0; q < nv; ++q) {
+            op[q] = hv[q];
+            if (o2) o2[q] = lv[q];
+          }
+        }
+      }
+    }
+  }
+  if (S16 || !p.t) return;
+  __syncthreads();
+  OT* tcopy = reinterpret_cast<OT*>(p.t);
+  // Pass 2: two consecutive rows per thread -> one 4-byte store along m.
+#pragma unroll 4
+  for (int idx = tid; idx < BM * BN / 2; idx += NT) {
+    const int c = idx / (BM / 2), r = (idx % (BM / 2)) * 2;
+    const int m = m0 + r, n = n0 + c;
+    if (m < M && n < N) {
+      const OT h0 = cvt<OT>(cs[r * CS + c]);
+      const OT h1 = cvt<OT>(m + 1 < M ? cs[(r + 1) * CS + c] : 0.0f);
+      *reinterpret_cast<unsigned*>(tcopy + (long long)n * p.ldt + m) = pack2(h0, h1);
+    }
+  }
+}
+
+// One kernel configuration: LDS limit set once per process, launch over a
+// ragged batch of up to WIDE_MAX_BATCH problems.
+template <typename OT, int MODE, int SPLIT, int ACT, bool BREG, int BM, int BN, int S, int WGM, int WGN>
+struct Cfg {
+  static constexpr int smem = smem_bytes(BM, BN, S, SPLIT == 2);
+  static const void* fn() {
+    return reinterpret_cast<const void*>(&dma_gemm_kernel<OT, MODE, SPLIT, ACT, BREG, BM, BN, S, WGM, WGN>);
+  }
+  static hipError_t prepare() {
+    static const hipError_t e = hipFuncSetAttribute(fn(), hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+    return e;
+  }
+  static hipError_t launch(const WideProblem* probs, int count, hipStream_t s) {
+    const hipError_t pe = prepare();
+    if (pe != hipSuccess) return pe;
+    Batch bt;
+    bt.count = count;
+    int total = 0;
+    for (int i = 0; i < count; ++i) {
+      bt.p[i] = probs[i];
+      bt.start[i] = total;
+      total += ((probs[i].M + BM - 1) / BM) * ((probs[i].N + BN - 1) / BN);
+    }
+    for (int i = count; i <= WIDE_MAX_BATCH; ++i) bt.start[i] = total;
+    if (total == 0) return hipSuccess;
+    void* args[] = {&bt};
+    return hipLaunchKernel(fn(), dim3(total), dim3(WGM * WGN * 64), args, smem, s);
+  }
+};
+
+// Calls F<ACT>::run(args...) for the runtime activation code.
+template <template <int> class F, typename... Args>
+hipError_t by_act(int act, Args... a) {
+  switch (act) {
+    case ACT_RELU: return F<ACT_RELU>::run(a...);
+    case ACT_TANH: return F<ACT_TANH>::run(a...);
+    case ACT_SIGMOID: return F<ACT_SIGMOID>::run(a...);
+    case ACT_SILU: return F<ACT_SILU>::run(a...);
+    case ACT_GELU: return F<ACT_GELU>::run(a...);
+    default: return F<ACT_IDENTITY>::run(a...);
+  }
+}
+
+}  // namespace dma
+}  // namespace ipc

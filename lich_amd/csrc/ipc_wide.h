@@ -1,28 +1,40 @@
-// ipc_wide.h - host interface of the GEMM path for wide nets (gfx950).
+// ipc_wide.h - host interface of the LDS-DMA MFMA GEMM family (gfx950).
 //
-// Wide layers (hundreds to thousands of units, batch in the hundreds or
-// more) are MFMA-bound.  This path keeps the fp32 masters x, eps and W of the
-// plan and, next to them, 16-bit operand copies laid out k-contiguous for
-// every GEMM that reads them, so each GEMM streams both operands straight
-// from HBM into LDS (global_load_lds) with no conversion, transpose or
-// activation in its loaders:
+// One kernel template (ipc_dma_gemm.h) serves two callers:
 //
-//   pred   eps[l] = x[l] - W[l] f(x[l+1])       A = Wh[l] (+ Wl[l])  [d_l][d_{l+1}]
-//                                               B = FT[l+1]          [B][d_{l+1}]
-//   infer  x[l] += g(-eps[l] + f'(x[l]) W[l-1]^T eps[l-1])
-//                                               A = WT[l-1]          [d_l][d_{l-1}]
-//                                               B = ET[l-1]          [B][d_{l-1}]
-//   weight W[l] += a eps[l] f(x[l+1])^T         A = E[l]             [d_l][B]
-//                                               B = F[l+1]           [d_{l+1}][B]
+// * the GEMM path of wide nets (modes WIDE_*): the plan keeps the fp32
+//   masters x, eps and W and, next to them, 16-bit operand copies of W, f(x)
+//   and eps that the GEMMs stream straight from HBM into LDS
+//   (global_load_lds, no VGPR staging), and fused epilogues that update the
+//   masters and rewrite the copies:
 //
-// Each epilogue writes the copies that later GEMMs read: pred writes E and
-// ET, infer writes F and FT of the updated states, weight writes Wh, Wl
-// (W - Wh, the error-compensation term) and WT.  The forward initialisation
-// x[l] = W[l] f(x[l+1]) (one layer per launch, l = L-1 .. 1) is the pred GEMM
-// with an epilogue that writes x[l], F[l] and FT[l], so that the first step's
-// prediction reproduces it exactly.  Every copy has its rows
-// padded to WIDE_ROW_PAD and its k extent to WIDE_BK with zeros, which the
-// kernel relies on: its main loop has no bounds checks.
+//     pred   eps[l] = x[l] - W[l] f(x[l+1])    A = Wh[l] (+ Wl[l])  [d_l][d_{l+1}]
+//                                              B = FT[l+1]           [B][d_{l+1}]
+//     infer  x[l] += g(-eps[l] + f'(x[l]) W[l-1]^T eps[l-1])
+//                                              A = WT[l-1]           [d_l][d_{l-1}]
+//                                              B = ET[l-1]           [B][d_{l-1}]
+//     weight W[l] += a eps[l] f(x[l+1])^T      A = E[l]              [d_l][B]
+//                                              B = F[l+1]            [d_{l+1}][B]
+//
+//   Every copy is k-contiguous for the GEMM that reads it, so all fragment
+//   reads are plain 16-byte LDS reads (measured faster here than reading a
+//   copy transposed with ds_read_b64_tr_b16, whose 8-byte reads need twice
+//   the LDS instructions, even after paying the weight epilogue's extra W^T
+//   write).  pred writes eps, E and ET, infer x, F and FT, weight W, Wh, Wl
+//   (W - Wh, the error-compensation term of split 2) and WT; the forward
+//   initialisation x[l] = W[l] f(x[l+1]) (one layer per launch, l = L-1 .. 1)
+//   is the pred GEMM with an epilogue that writes x[l], F[l] and FT[l].
+//   Every copy has its rows and columns padded to WIDE_PAD with zeros, which
+//   the main loop relies on (it has no k bounds checks).
+//
+// * the standalone kernels of the operator API with 16-bit storage (modes
+//   S16_*; src/ipc_tilelang/tilelang_kernels.py:114-349 semantics, rounding as
+//   there): operands are the caller's tensors, k contiguous or not as above
+//   (S16_WEIGHT's B is X_upper [K][B] read as [n][k]); operands whose
+//   contraction index is not the contiguous one (W_lower, X_upper and E_lower
+//   of pred / infer) are read from LDS with gfx950's transposing LDS read
+//   (ds_read_b64_tr_b16); f(X_upper) goes through registers (global load,
+//   activation, LDS store) instead of the DMA.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -30,46 +42,50 @@
 namespace ipc {
 
 constexpr int WIDE_BK = 64;         // k per pipeline stage (16-bit elements, 128-byte rows)
-constexpr int WIDE_ROW_PAD = 256;   // row padding of every operand copy (largest tile edge)
-constexpr int WIDE_MAX_BATCH = 16;  // layers per launch
+constexpr int WIDE_PAD = 64;        // row and column padding of every operand copy
+constexpr int WIDE_MAX_BATCH = 16;  // problems per launch
 
-enum { WIDE_PRED = 0, WIDE_INFER = 1, WIDE_WEIGHT = 2, WIDE_FWD = 3 };
+enum {
+  WIDE_PRED = 0, WIDE_INFER = 1, WIDE_WEIGHT = 2, WIDE_FWD = 3,
+  S16_PRED = 4, S16_FWD = 5, S16_INFER = 6, S16_WEIGHT = 7,
+};
 
 inline long long wide_pad(long long v, long long m) { return (v + m - 1) / m * m; }
 
-// One layer's GEMM C[M][N] = sum_k A[m][k] B[n][k] with its fused epilogue.
-// K is a multiple of WIDE_BK; A (and A_lo) hold >= wide_pad(M, 256) rows and
-// B >= wide_pad(N, 256) rows, zero beyond M / N / the true contraction.
+// One GEMM C[M][N] = sum_k A(m, k) B(n, k) with its fused epilogue.
+// K is a multiple of WIDE_BK and every operand element with k < K is
+// readable (zero beyond the true contraction).  a_lim / b_lim bound the
+// other index of each operand: the rows that may be read of a k-contiguous
+// operand, the columns (a multiple of 8, <= its ld) of an m/n-contiguous one;
+// tiles that reach past M or N clamp their loads there and mask their stores.
 struct WideProblem {
   int M, N, K;
-  const void* a; const void* a_lo; long long lda;  // a_lo: split-2 term (pred) or nullptr
-  const void* b; long long ldb;
-  float* out; long long ldo;        // pred: eps[l], fwd: x[l] (written); infer: x[l], weight: W[l] (updated)
-  const float* aux; long long ldx;  // pred: x[l], infer: eps[l]
-  void* h; long long ldh;           // 16-bit copy [M][ldh]: pred E, infer/fwd F, weight Wh
-  void* hl; long long ldhl;         // weight: Wl [M][ldhl]
-  void* t; long long ldt;           // 16-bit transposed copy [N][ldt]: pred ET, infer/fwd FT, weight WT; may be null
-  float* out2; long long ld2;       // infer, save mode: f(x_new) fp32 [M][ld2], or null
-  float scal;                       // infer: gamma, weight: alpha
-  int vec;                          // 1: out/aux/out2 rows 16-byte aligned, h/hl rows 8-byte aligned
+  const void* a; const void* a_lo; long long lda; int a_lim;  // a_lo: split-2 term (pred) or nullptr
+  const void* b; long long ldb; int b_lim;
+  void* out; long long ldo;        // WIDE: pred eps[l], fwd x[l] (written); infer x[l], weight W[l] (updated), fp32
+                                   // S16:  pred E, fwd OUT (written); infer X, weight W (updated), 16-bit
+  const void* aux; long long ldx;  // WIDE pred: x[l], infer: eps[l] (fp32); S16 pred: X_lower, infer: E (16-bit)
+  void* h; long long ldh;          // WIDE: 16-bit copy [M][ldh]: pred E, infer/fwd F, weight Wh
+  void* hl; long long ldhl;        // WIDE weight: Wl [M][ldhl]
+  void* t; long long ldt;          // WIDE: transposed 16-bit copy [N][ldt] (pred ET, infer/fwd FT, weight WT), or null
+  void* out2; long long ld2;       // infer, save mode: f(x_new) (fp32 for WIDE, 16-bit for S16), or null
+  float scal;                      // infer: gamma, weight: alpha
+  int vec;                         // 1: out/aux/out2 rows allow 4-element vector access, h/hl rows 8-byte aligned
 };
 
-struct WideBatch {
-  WideProblem p[WIDE_MAX_BATCH];
-  int start[WIDE_MAX_BATCH + 1];  // first tile of each problem
-  int count, act;
-};
-
-// Tile edge (rows of A, rows of B) the launch of `mode` uses.
-void wide_tile(int mode, int split, int* bm, int* bn);
-
-// Launches one phase over `count` layers (one launch per WIDE_MAX_BATCH layers).
-// `operand` is DT_F16 or DT_BF16, `split` 1 or 2 (pred and fwd).
+// Launches one phase of the wide path over `count` layers (one launch per
+// WIDE_MAX_BATCH layers).  `operand` is DT_F16 or DT_BF16, `split` 1 or 2
+// (pred and fwd), `act` the activation of the infer / fwd epilogues.
 hipError_t launch_wide(int mode, const WideProblem* probs, int count, int operand, int split, int act,
                        hipStream_t s);
 
-// Raises the dynamic-LDS limit of every wide kernel instantiation.
+// Raises the dynamic-LDS limit of every wide-path kernel instantiation.
 hipError_t wide_prepare();
+
+// Standalone 16-bit-storage launches (modes S16_*) over `count` problems.
+// `act`: the loader activation of S16_PRED / S16_FWD / S16_WEIGHT (ACT_IDENTITY
+// for a saved activation), the epilogue activation of S16_INFER.
+hipError_t launch_s16(int mode, const WideProblem* probs, int count, int operand, int act, hipStream_t s);
 
 // Refresh of the 16-bit copies from the fp32 masters (after the masters were
 // written outside a step):

@@ -139,14 +139,16 @@ def test_plan_validation():
 
 def _wide_layout_bytes(dims, B, split2):
     """The wide path's workspace layout restated: 256 bytes, then one 256-byte
-    aligned 16-bit buffer per operand copy, rows padded to 256, k to 64."""
+    aligned 16-bit buffer per operand copy, rows and columns padded to 64:
+    W hi [and lo] and its transpose (for l < L-1), f(x[l]) and its transpose
+    for l = 1..L, eps[l] for l < L and its transpose for l < L-1."""
     pad = lambda v, m: (v + m - 1) // m * m  # noqa: E731
     L = len(dims) - 1
     total = 256
 
     def add(rows, cols):
         nonlocal total
-        total += pad(pad(rows, 256) * pad(cols, 64) * 2, 256)
+        total += pad(pad(rows, 64) * pad(cols, 64) * 2, 256)
 
     for l in range(L):
         add(dims[l], dims[l + 1])
@@ -180,7 +182,7 @@ def test_plan_path_selection_and_wide_workspace():
         assert lib.ipc_plan_bind(h, arr, arr, arr, None, P + 16) == nat.ERR_ALIGN
     finally:
         lib.ipc_plan_destroy(h)
-    # split 1 drops the W_lo copies; ragged sizes pad rows to 256 and k to 64
+    # split 1 drops the W_lo copies; ragged sizes pad rows and columns to 64
     ragged = (7, 130, 65, 257)
     rd = (ctypes.c_int * 4)(*ragged)
     assert lib.ipc_plan_create(ctypes.byref(h), 3, rd, 37, 0, 1, 1, 1, 1e-4, 0.5, 1, 0, 2) == nat.IPC_OK
