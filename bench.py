@@ -16,6 +16,7 @@ The same run also reports
 * the CPU baseline: the oracle's fp32 step on this host's cores.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-wide] [--no-cpu]
+       python bench.py --wide-only | --sweep | --copy-calibration
 """
 from __future__ import annotations
 
@@ -31,6 +32,12 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 METRIC = "iPC train samples/sec (L=6,h=64,B=128); fused-GEMM TFLOP/s vs MFMA peak"
+# HBM bytes that one launch of the dominant kernel moves, measured with
+# rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes (one counter per pass) over
+# `bench.py --no-cpu --no-wide`, each scaled by the same counter's reading for
+# a plain device copy of known size (`bench.py --copy-calibration`: FETCH_SIZE
+# x 2.0, WRITE_SIZE x 1.0).  Keyed by kernel; re-measure after a kernel change.
+MEASURED_TRAFFIC = {"whole-step kernel, 4 steps per launch": 13_065_152 + 3_926_848}
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0  # dense, no sparsity
 FP16_PEAK_TFLOPS = 2500.0
@@ -239,21 +246,73 @@ def kernel_sweep(sizes=(1024, 4096, 8192), batches=(256, 2048, 8192), acts=("tan
     return rows
 
 
+def wide_config(T):
+    """The MFMA-bound wide configuration (1000, 4096 x 4, 4096), B=1024, bf16
+    operands: ms/step, TFLOP/s, per-phase launch times and the roofline of the
+    dominant phase kernel."""
+    import torch
+
+    wdims = (1000,) + (4096,) * 4 + (4096,)
+    WB = 1024
+    wmodel, wx, wy = make_model(wdims, WB, "tanh", torch.bfloat16, seed=0, input_dist="normal")
+    w_elapsed, w_done, _w_replay_us = run_steady(wmodel, wx, wy, T, 2 * T, 5 * T)
+    w_ms = w_elapsed * 1e3 / w_done
+    flops_step = sum(v[1] for v in phase_bytes_flops(wdims, WB).values())
+    tflops = flops_step / (w_ms * 1e-3) / 1e12
+    wphase = time_phases(wmodel, reps=5, replays=3)
+    wbf = phase_bytes_flops(wdims, WB)
+    wphases = {k: {"us": round(v, 2), "TFLOP/s": round(wbf[k][1] / (v * 1e-6) / 1e12, 2)}
+               for k, v in wphase.items()}
+    wdom = max(wphase, key=wphase.get)
+    wide = {"workload": "wide iPC MLP dims (1000,4096x4,4096), B=1024, tanh, bf16 operands, fp32 master, T=4",
+            "path": wmodel.path, "pred_split": wmodel.pred_split,
+            "ms_per_step": round(w_ms, 4), "samples_per_s": round(WB / (w_ms * 1e-3), 1),
+            "gflop_per_step": round(flops_step / 1e9, 3), "tflops": round(tflops, 2),
+            "frac_of_bf16_peak": round(tflops / BF16_PEAK_TFLOPS, 4),
+            "phases": wphases,
+            # the dominant phase kernel against the dense bf16 MFMA peak
+            "roofline": {"bound": "mfma", "kernel": f"wide {wdom} phase", "achieved": wphases[wdom]["TFLOP/s"],
+                         "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(wphases[wdom]["TFLOP/s"] / BF16_PEAK_TFLOPS, 4),
+                         "algorithmic_flops_per_launch": wbf[wdom][1], "avg_launch_us": wphases[wdom]["us"]}}
+    log(f"wide: {wide}")
+    del wmodel
+
+    return wide
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20000)
     ap.add_argument("--warmup", type=int, default=400)
     ap.add_argument("--no-wide", action="store_true")
+    ap.add_argument("--wide-only", action="store_true",
+                    help="run only the wide configuration and print its JSON object")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--sweep", action="store_true",
                     help="run only the per-kernel roofline sweep (M=K in {1024,4096,8192}, "
                          "B in {256,2048,8192}, bf16) and print it as one JSON line")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a plain device copy of a known size (the reference point that scales the "
+                         "FETCH_SIZE / WRITE_SIZE counters of a rocprofv3 --pmc run to bytes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
               "(this build has no multi-GPU path)", file=sys.stderr)
         return 2
+    if args.copy_calibration:
+        import torch
+
+        nbytes = 256 << 20
+        src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration": {"bytes_read_per_copy": nbytes, "bytes_written_per_copy": nbytes,
+                                               "copies": 10}}), flush=True)
+        return 0
     if args.sweep:
         rows = kernel_sweep()
         print(json.dumps({"sweep": "per-kernel roofline, bf16 storage/operands, fp32 accumulation",
@@ -272,6 +331,9 @@ def main() -> int:
     warmup = max(T, args.warmup)
     log(f"device {torch.cuda.get_device_name(0)} arch {nat.device_arch(0)}")
 
+    if args.wide_only:
+        print(json.dumps({"wide": wide_config(T)}), flush=True)
+        return 0
     model, x, y = make_model(dims, B, "tanh", torch.float16, seed=0)
     elapsed, done, replay_us = run_steady(model, x, y, T, warmup, steps)
     ms_per_step = elapsed * 1e3 / done
@@ -301,38 +363,12 @@ def main() -> int:
         launch_bytes, launch_flops = bf[dom]
     achieved = launch_bytes / (launch_us * 1e-6) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None, "kernel": kernel,
+                "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": MEASURED_TRAFFIC.get(kernel), "kernel": kernel,
                 "algorithmic_bytes_per_launch": launch_bytes, "avg_launch_us": round(launch_us, 3),
                 "achieved_tflops": round(launch_flops / (launch_us * 1e-6) / 1e12, 4)}
     del pmodel
 
-    wide = None
-    if not args.no_wide:
-        wdims = (1000,) + (4096,) * 4 + (4096,)
-        WB = 1024
-        wmodel, wx, wy = make_model(wdims, WB, "tanh", torch.bfloat16, seed=0, input_dist="normal")
-        w_elapsed, w_done, _w_replay_us = run_steady(wmodel, wx, wy, T, 2 * T, 5 * T)
-        w_ms = w_elapsed * 1e3 / w_done
-        flops_step = sum(v[1] for v in phase_bytes_flops(wdims, WB).values())
-        tflops = flops_step / (w_ms * 1e-3) / 1e12
-        wphase = time_phases(wmodel, reps=5, replays=3)
-        wbf = phase_bytes_flops(wdims, WB)
-        wphases = {k: {"us": round(v, 2), "TFLOP/s": round(wbf[k][1] / (v * 1e-6) / 1e12, 2)}
-                   for k, v in wphase.items()}
-        wdom = max(wphase, key=wphase.get)
-        wide = {"workload": "wide iPC MLP dims (1000,4096x4,4096), B=1024, tanh, bf16 operands, fp32 master, T=4",
-                "path": wmodel.path, "pred_split": wmodel.pred_split,
-                "ms_per_step": round(w_ms, 4), "samples_per_s": round(WB / (w_ms * 1e-3), 1),
-                "gflop_per_step": round(flops_step / 1e9, 3), "tflops": round(tflops, 2),
-                "frac_of_bf16_peak": round(tflops / BF16_PEAK_TFLOPS, 4),
-                "phases": wphases,
-                # the dominant phase kernel against the dense bf16 MFMA peak
-                "roofline": {"bound": "mfma", "kernel": f"wide {wdom} phase", "achieved": wphases[wdom]["TFLOP/s"],
-                             "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                             "frac": round(wphases[wdom]["TFLOP/s"] / BF16_PEAK_TFLOPS, 4),
-                             "algorithmic_flops_per_launch": wbf[wdom][1], "avg_launch_us": wphases[wdom]["us"]}}
-        log(f"wide: {wide}")
-        del wmodel
+    wide = None if args.no_wide else wide_config(T)
 
     cpu = None
     if not args.no_cpu:
