@@ -512,10 +512,18 @@ __global__ void __launch_bounds__(NT) narrow_kernel(const NarrowArgs p) {
   using N = Narrow<OT, SPLIT, ACT>;
   extern __shared__ __align__(16) char lds[];
   __shared__ NarrowLds layout;
+  // The argument block (unit lists, dimensions, per-layer pointers) is read
+  // with layer / unit indices known only at run time, which the compiler
+  // serves from the kernel-argument segment in memory: a memory round trip in
+  // front of every unit's loads.  A copy in LDS answers in LDS latency.
+  __shared__ NarrowArgs sp;
+  static_assert(sizeof(NarrowArgs) % 4 == 0, "argument block copy");
+  for (int i = threadIdx.x; i < (int)(sizeof(NarrowArgs) / 4); i += NT)
+    reinterpret_cast<int*>(&sp)[i] = reinterpret_cast<const int*>(&p)[i];
   if (threadIdx.x == 0)
     narrow_lds_layout(p.dims, p.L, N::KS, N::PAD, (int)sizeof(OT), N::SB, layout);
   __syncthreads();
-  N k(p, layout, lds);
+  N k(sp, layout, lds);
   const int ncb = (p.B + NC - 1) / NC;
   const int ntile = p.wtile_start[p.L];
   const int nb = gridDim.x;
