@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define IPC_ABI_VERSION 3
+#define IPC_ABI_VERSION 4
 
 /* status codes */
 #define IPC_OK 0
@@ -163,12 +163,24 @@ typedef struct ipc_plan ipc_plan;
 
 /* split applies to the prediction phase and the forward initialisation.
  * path selects the kernels a plan runs:
- *   IPC_PATH_AUTO    the whole-step kernel when the net is narrow (fp32
- *                    storage, every output width d_0..d_{L-1} <= 128, L <= 16,
- *                    split 1 or 3, one column block's buffers fit in LDS),
- *                    else the wide GEMM path when eligible, else the phased path;
+ *   IPC_PATH_AUTO    the layer-resident whole-step kernel when eligible (see
+ *                    IPC_PATH_RESIDENT), else the column-block whole-step
+ *                    kernel when the net is narrow (fp32 storage, every output
+ *                    width d_0..d_{L-1} <= 128, L <= 16, split 1 or 3, one
+ *                    column block's buffers fit in LDS), else the wide GEMM
+ *                    path when eligible, else the phased path;
  *   IPC_PATH_PHASED  one generic multi-layer launch per phase (any config);
- *   IPC_PATH_NARROW  the whole-step kernel (IPC_ERR_CONFIG if not narrow);
+ *   IPC_PATH_NARROW  the column-block whole-step kernel (IPC_ERR_CONFIG if
+ *                    not narrow);
+ *   IPC_PATH_RESIDENT  multi-step launches on the layer-resident whole-step
+ *                    kernel (every workgroup keeps one layer's W, or a column
+ *                    chunk of the top layer's, on chip for all steps and
+ *                    exchanges only eps and W^T eps with its neighbours): a
+ *                    narrow net with fp16/bf16 operands, split 1 or 3, L >= 2,
+ *                    d_0..d_{L-1} <= 64, B <= 128 and the GEMM weight update
+ *                    (weight mode GEMM, or AUTO with B > 16); IPC_ERR_CONFIG
+ *                    otherwise.  Single-phase launches and the forward
+ *                    initialisation of such a plan run on the column kernel;
  *   IPC_PATH_WIDE    one LDS-DMA MFMA launch per phase over 16-bit operand
  *                    copies kept in the workspace: fp32 storage, fp16/bf16
  *                    operands, split 1 or 2, GEMM weight update (weight mode
@@ -178,6 +190,7 @@ typedef struct ipc_plan ipc_plan;
 #define IPC_PATH_PHASED 0
 #define IPC_PATH_NARROW 1
 #define IPC_PATH_WIDE 2
+#define IPC_PATH_RESIDENT 3
 #define IPC_FUSED_AUTO IPC_PATH_AUTO
 #define IPC_FUSED_OFF IPC_PATH_PHASED
 #define IPC_FUSED_ON IPC_PATH_NARROW
@@ -185,10 +198,10 @@ int ipc_plan_create(ipc_plan** out, int L, const int* dims, int B,
                     int storage, int operand, int split, int act, float alpha, float gamma,
                     int recompute, int weight_mode, int path);
 
-/* 1 if the plan runs the whole-step kernel, 0 otherwise. */
+/* 1 if the plan runs a whole-step kernel (column-block or layer-resident), 0 otherwise. */
 int ipc_plan_fused(const ipc_plan* plan);
 
-/* The path the plan runs (IPC_PATH_PHASED, _NARROW or _WIDE), -1 for NULL. */
+/* The path the plan runs (IPC_PATH_PHASED, _NARROW, _WIDE or _RESIDENT), -1 for NULL. */
 int ipc_plan_path(const ipc_plan* plan);
 
 /* Bytes of zero-initialised device workspace ipc_plan_bind needs (0 for the
@@ -196,7 +209,9 @@ int ipc_plan_path(const ipc_plan* plan);
  * grid-barrier counters, which it leaves zero after every launch (word 2
  * becomes non-zero if a barrier wait ever ran past its spin limit); in
  * recompute mode the whole-step kernel keeps the f(x[l]) values phase A
- * evaluates for the weight update after them.  The wide path keeps its
+ * evaluates for the weight update after them, and a layer-resident plan its
+ * per-workgroup step flags (also left zero after every launch) and the
+ * double-buffered eps / W^T eps exchange after those.  The wide path keeps its
  * 16-bit operand copies there (W as hi and lo terms, W^T, f(x) and eps in
  * both layouts, zero padded); their padding must stay zero. */
 long long ipc_plan_workspace_bytes(const ipc_plan* plan);

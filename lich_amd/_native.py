@@ -27,12 +27,12 @@ TILE_DMA = 3
 TILE_COUNT = 4
 WMODE = {"gemm": 0, "outer": 1, "auto": 2}
 SPLIT_NONE, SPLIT_W, SPLIT_WX = 1, 2, 3
-PATH_AUTO, PATH_PHASED, PATH_NARROW, PATH_WIDE = -1, 0, 1, 2
+PATH_AUTO, PATH_PHASED, PATH_NARROW, PATH_WIDE, PATH_RESIDENT = -1, 0, 1, 2, 3
 # plan path option (IPCConfig.fused): the IPC_PATH_* codes; "off"/"on" are the
 # IPC_FUSED_* spellings of phased / narrow
 FUSED = {"auto": PATH_AUTO, "off": PATH_PHASED, "phased": PATH_PHASED, "on": PATH_NARROW, "narrow": PATH_NARROW,
-         "wide": PATH_WIDE}
-PATH_NAMES = {PATH_PHASED: "phased", PATH_NARROW: "narrow", PATH_WIDE: "wide"}
+         "wide": PATH_WIDE, "resident": PATH_RESIDENT}
+PATH_NAMES = {PATH_PHASED: "phased", PATH_NARROW: "narrow", PATH_WIDE: "wide", PATH_RESIDENT: "resident"}
 
 _DTYPE_CODES = {torch.float32: DT_F32, torch.float16: DT_F16, torch.bfloat16: DT_BF16}
 

@@ -403,9 +403,12 @@ struct ipc_plan {
   const void* act_src = nullptr;  // x[L]
   void* act_dst = nullptr;        // a[L] in save mode
   int launches = 0;
-  // whole-step kernel for narrow nets
+  // whole-step kernels for narrow nets (column-block; layer-resident for multi-step launches)
   bool narrow = false;
   NarrowArgs nargs{};
+  bool resident = false;
+  ResidentArgs rargs{};
+  long long res_ws_off = 0;
   // wide GEMM path
   bool wide = false;
   std::vector<WideProblem> wpred, winfer, wweight, wfwd;  // wfwd: l = L-1 .. 1
@@ -467,7 +470,24 @@ struct WideLayout {
   }
 };
 
+bool narrow_outer(int B, int wmode) {
+  return B <= NARROW_OUTER_MAX_B && (wmode == IPC_WMODE_OUTER || (wmode == IPC_WMODE_AUTO && B <= 16));
+}
+
+// Layer-resident kernel eligibility; fills `ra` and returns its workspace bytes, or -1.
+long long resident_eligible(int L, const int* dims, int B, int operand, int split, int wmode, bool narrow,
+                            ResidentArgs& ra) {
+  if (!narrow || operand == IPC_DT_F32 || narrow_outer(B, wmode)) return -1;
+  if (split != IPC_SPLIT_NONE && split != IPC_SPLIT_WX) return -1;
+  return resident_plan(dims, L, B, split == IPC_SPLIT_WX ? 3 : 1, ra);
+}
+
 int launch_narrow_mode(ipc_plan* plan, int mode, int steps, hipStream_t s) {
+  if (mode == NMODE_STEPS && plan->resident) {
+    ResidentArgs a = plan->rargs;
+    a.steps = steps;
+    return launch_rc(launch_resident(a, plan->operand, plan->split, plan->act, s), "layer-resident whole-step kernel");
+  }
   NarrowArgs a = plan->nargs;
   a.mode = mode;
   a.steps = steps;
@@ -495,9 +515,15 @@ int ipc_plan_create(ipc_plan** out, int L, const int* dims, int B, int storage, 
   for (int l = 0; l < L; ++l) TRY(check_dims(dims[l], dims[l + 1], B, 1));
   if (weight_mode == IPC_WMODE_OUTER && B > kOuterMaxB)
     return fail(IPC_ERR_SHAPE, "outer weight mode supports B <= %d (got %d)", kOuterMaxB, B);
-  if (path < IPC_PATH_AUTO || path > IPC_PATH_WIDE) return fail(IPC_ERR_CONFIG, "unknown path %d", path);
+  if (path < IPC_PATH_AUTO || path > IPC_PATH_RESIDENT) return fail(IPC_ERR_CONFIG, "unknown path %d", path);
   const int esplit = effective_split(storage, operand, split);
   const bool eligible = narrow_eligible(L, dims, storage, operand, esplit);
+  ResidentArgs ra{};
+  const long long res_bytes = resident_eligible(L, dims, B, operand, esplit, weight_mode, eligible, ra);
+  if (path == IPC_PATH_RESIDENT && res_bytes < 0)
+    return fail(IPC_ERR_CONFIG,
+                "the layer-resident kernel needs a narrow net with fp16/bf16 operands, split 1 or 3, L >= 2, "
+                "widths d_0..d_{L-1} <= %d, B <= %d and the GEMM weight update", RES_MAX_WIDTH, RES_MAX_B);
   if (path == IPC_PATH_NARROW && !eligible)
     return fail(IPC_ERR_CONFIG,
                 "the whole-step kernel needs fp32 storage, L <= %d, widths d_0..d_{L-1} <= %d and a column "
@@ -513,9 +539,15 @@ int ipc_plan_create(ipc_plan** out, int L, const int* dims, int B, int storage, 
   p->alpha = alpha; p->gamma = gamma; p->recompute = recompute ? 1 : 0;
   p->wmode = weight_mode;
   p->dims.assign(dims, dims + L + 1);
-  p->narrow = path == IPC_PATH_NARROW || (path == IPC_PATH_AUTO && eligible);
+  p->resident = path == IPC_PATH_RESIDENT || (path == IPC_PATH_AUTO && res_bytes >= 0);
+  p->narrow = p->resident || path == IPC_PATH_NARROW || (path == IPC_PATH_AUTO && eligible);
   p->wide = !p->narrow && (path == IPC_PATH_WIDE || (path == IPC_PATH_AUTO && weligible));
   if (p->narrow) p->ws_bytes = narrow_workspace_bytes(dims, L, B, p->recompute != 0);
+  if (p->resident) {
+    p->rargs = ra;
+    p->res_ws_off = (p->ws_bytes + 255) / 256 * 256;
+    p->ws_bytes = p->res_ws_off + res_bytes;
+  }
   if (p->wide) p->ws_bytes = WideLayout(p->dims, L, B, p->split == IPC_SPLIT_W).total;
   *out = p;
   return ok();
@@ -525,6 +557,7 @@ int ipc_plan_fused(const ipc_plan* plan) { return plan && plan->narrow ? 1 : 0; 
 
 int ipc_plan_path(const ipc_plan* plan) {
   if (!plan) return -1;
+  if (plan->resident) return IPC_PATH_RESIDENT;
   return plan->narrow ? IPC_PATH_NARROW : plan->wide ? IPC_PATH_WIDE : IPC_PATH_PHASED;
 }
 
@@ -592,8 +625,7 @@ int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w
     na.L = L; na.B = B; na.act = plan->act;
     na.alpha = plan->alpha; na.gamma = plan->gamma;
     na.spin_limit = kNarrowSpinLimit;
-    na.outer = (B <= NARROW_OUTER_MAX_B) &&
-               (plan->wmode == IPC_WMODE_OUTER || (plan->wmode == IPC_WMODE_AUTO && B <= 16));
+    na.outer = narrow_outer(B, plan->wmode);
     int tiles = 0;
     for (int l = 0; l <= L; ++l) {
       na.dims[l] = d[l];
@@ -631,6 +663,21 @@ int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w
       }
     }
     TRY(launch_rc(narrow_prepare(plan->operand, plan->split, plan->act, na.lds_bytes), "whole-step kernel LDS limit"));
+    if (plan->resident) {
+      ResidentArgs& ra = plan->rargs;
+      ra.alpha = plan->alpha; ra.gamma = plan->gamma;
+      ra.spin_limit = kNarrowSpinLimit;
+      for (int l = 0; l <= L; ++l) {
+        ra.x[l] = na.x[l];
+        ra.e[l] = na.e[l];
+        ra.fx[l] = na.fx[l];
+        if (l < L) ra.w[l] = na.w[l];
+      }
+      ra.bar = na.bar;
+      resident_bind(ra, static_cast<char*>(workspace) + plan->res_ws_off);
+      TRY(launch_rc(resident_prepare(plan->operand, plan->split, plan->act, ra.lds_bytes),
+                    "layer-resident kernel LDS limit"));
+    }
     plan->launches = 1;
   }
   if (plan->wide) {

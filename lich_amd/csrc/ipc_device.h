@@ -25,10 +25,20 @@ __device__ __forceinline__ float to_f32(float v) { return v; }
 __device__ __forceinline__ float to_f32(f16 v) { return (float)v; }
 __device__ __forceinline__ float to_f32(bf16 v) { return (float)v; }
 
+// Rounds the fp32 value v to the operand type.  v is pinned in a register
+// first: otherwise the compiler may fold the multiply that produced v into the
+// conversion (v_fma_mix*, one rounding of the exact product), and the same
+// source would then round differently in different kernels.
 template <typename T> __device__ __forceinline__ T cvt(float v);
 template <> __device__ __forceinline__ float cvt<float>(float v) { return v; }
-template <> __device__ __forceinline__ f16 cvt<f16>(float v) { return (f16)v; }
-template <> __device__ __forceinline__ bf16 cvt<bf16>(float v) { return (bf16)v; }
+template <> __device__ __forceinline__ f16 cvt<f16>(float v) {
+  asm("" : "+v"(v));
+  return (f16)v;
+}
+template <> __device__ __forceinline__ bf16 cvt<bf16>(float v) {
+  asm("" : "+v"(v));
+  return (bf16)v;
+}
 
 // Loads 4 consecutive elements (aligned to 4 elements) and widens them to fp32.
 __device__ __forceinline__ void load4(const float* p, float o[4]) {
@@ -54,10 +64,17 @@ __device__ __forceinline__ void load4(const bf16* p, float o[4]) { load4_16(p, o
 
 // ---------------------------------------------------------------- activations
 // fp32 evaluation as in tilelang_kernels.py:61-96.  tanh/exp are the HIP
-// device library's tanhf/expf.
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
+// device library's tanhf/expf.  Contraction into FMA is off in every
+// activation, so that a function gives the same bits in every kernel it is
+// inlined into (the whole-step kernels keep copies of one state in several
+// workgroups and must agree on them exactly).
+__device__ __forceinline__ float sigmoidf_(float x) {
+#pragma clang fp contract(off)
+  return 1.0f / (1.0f + expf(-x));
+}
 
 __device__ __forceinline__ float act_f(int act, float x) {
+#pragma clang fp contract(off)
   switch (act) {
     case ACT_RELU: return x > 0.0f ? x : 0.0f;
     case ACT_TANH: return tanhf(x);
@@ -72,6 +89,7 @@ __device__ __forceinline__ float act_f(int act, float x) {
 }
 
 __device__ __forceinline__ float act_df(int act, float x) {
+#pragma clang fp contract(off)
   switch (act) {
     case ACT_RELU: return x > 0.0f ? 1.0f : 0.0f;
     case ACT_TANH: { const float y = tanhf(x); return 1.0f - y * y; }
@@ -91,6 +109,7 @@ __device__ __forceinline__ float act_df(int act, float x) {
 // Compile-time forms of the same activations, for kernels instantiated per
 // activation (no switch in their inner loops).
 template <int ACT> __device__ __forceinline__ float act_t(float x) {
+#pragma clang fp contract(off)
   if (ACT == ACT_RELU) return x > 0.0f ? x : 0.0f;
   if (ACT == ACT_TANH) return tanhf(x);
   if (ACT == ACT_SIGMOID) return sigmoidf_(x);
@@ -103,6 +122,7 @@ template <int ACT> __device__ __forceinline__ float act_t(float x) {
 }
 
 template <int ACT> __device__ __forceinline__ float dact_t(float x) {
+#pragma clang fp contract(off)
   if (ACT == ACT_RELU) return x > 0.0f ? 1.0f : 0.0f;
   if (ACT == ACT_TANH) { const float y = tanhf(x); return 1.0f - y * y; }
   if (ACT == ACT_SIGMOID) { const float y = sigmoidf_(x); return y * (1.0f - y); }

@@ -11,6 +11,10 @@ constexpr int NARROW_OUTER_MAX_B = 16;  // batch limit of the rank-B outer-produ
 constexpr int NARROW_NC = 16;           // batch columns per column block
 constexpr int NARROW_MAX_UNITS = NARROW_MAX_L * (NARROW_MAX_WIDTH / 16);
 constexpr int NARROW_LDS_LIMIT = 160 * 1024;
+// Both whole-step kernels accumulate a prediction contraction in partials of
+// this many columns, summed in order (one layer-resident workgroup per
+// partial of the top layer).
+constexpr int NARROW_KCHUNK = 128;
 
 enum { NMODE_STEPS = 0, NMODE_PHASE_A = 1, NMODE_PHASE_B = 2, NMODE_FORWARD = 3 };
 
@@ -80,6 +84,80 @@ __host__ __device__ inline void narrow_lds_layout(const int* dims, int L, int KS
   o.outer_base = o.es_base + ((e * esize + 15) / 16) * 16;
   o.total = o.outer_base + 2 * 64 * (NARROW_NC + 1) * 4;
 }
+
+// ---------------------------------------------------------------- layer-resident kernel
+// Multi-step launches of 16-bit-operand plans whose hidden widths are <= 64
+// and whose batch is <= 128 run a second whole-step kernel in which every
+// workgroup owns one layer's W for all steps (the top layer's W, with its
+// long input-width contraction, is split into column chunks owned by one
+// workgroup each) and exchanges only eps and W^T eps with its neighbours.
+constexpr int RES_MAX_WIDTH = 64;   // d_0 .. d_{L-1}
+constexpr int RES_MAX_B = 128;
+constexpr int RES_MAX_WG = 64;
+constexpr int RES_TILE = 256;       // floats per exchanged 16x16 tile (64 lanes x 4)
+
+struct ResidentArgs {
+  int L, B, steps, nwg, chunks, kc, spin_limit, lds_bytes;
+  float alpha, gamma;
+  int dims[NARROW_MAX_L + 1];
+  float* x[NARROW_MAX_L + 1];
+  float* e[NARROW_MAX_L + 1];
+  float* w[NARROW_MAX_L];
+  float* fx[NARROW_MAX_L + 1];  // f(x[l]) written at the end (a[l] in save mode)
+  float* xe[NARROW_MAX_L];      // eps[l], l = 1..L-2:        [2][tiles(d_l)][RES_TILE]
+  float* xg[NARROW_MAX_L];      // W[l]^T eps[l], l = 0..L-2: [2][tiles(d_{l+1})][RES_TILE]
+  float* xp;                    // top-layer partial products: [2][chunks][tiles(d_{L-1})][RES_TILE]
+  unsigned* flags;              // [nwg] last step each workgroup has published
+  unsigned* bar;                // [1] exit counter, [2] wait timeout flag (shared with the column kernel)
+};
+
+// LDS layout of one workgroup (element offsets, 16-bit elements).  M x K is
+// the workgroup's block of W; `hidden` workgroups also hold W^T and eps in
+// the inference operand layout.  Contraction extents are padded to 32 and
+// output extents to 16; every row is padded by 8 elements.
+//   wh, wl  [M16][K32+8]   W hi / lo          (prediction A)
+//   wt      [K16][M32+8]   W^T hi             (inference A, hidden only)
+//   fh, fl  [B16][K32+8]   f(x upper) hi / lo (prediction B)
+//   ft      [K16][B32+8]   f(x upper) hi      (weight-update B)
+//   eb      [B16][M32+8]   eps                (inference B, hidden only)
+//   ea      [M16][B32+8]   eps                (weight-update A)
+struct ResidentLds {
+  int ldw, ldwt, ldf, ldft, lde, lda;
+  int wh, wl, wt, fh, fl, ft, eb, ea, bytes;
+};
+
+__host__ __device__ inline int res_round(int v, int m) { return (v + m - 1) / m * m; }
+
+__host__ __device__ inline void resident_lds_layout(int M, int K, int B, bool hidden, bool split3, ResidentLds& o) {
+  const int M16 = res_round(M, 16), M32 = res_round(M, 32), K16 = res_round(K, 16), K32 = res_round(K, 32);
+  const int B16 = res_round(B, 16), B32 = res_round(B, 32);
+  o.ldw = K32 + 8; o.ldwt = M32 + 8; o.ldf = K32 + 8; o.ldft = B32 + 8; o.lde = M32 + 8; o.lda = B32 + 8;
+  int at = 0;
+  o.wh = at; at += M16 * o.ldw;
+  o.wl = at; if (split3) at += M16 * o.ldw;
+  o.wt = at; if (hidden) at += K16 * o.ldwt;
+  o.fh = at; at += B16 * o.ldf;
+  o.fl = at; if (split3) at += B16 * o.ldf;
+  o.ft = at; at += K16 * o.ldft;
+  o.eb = at; if (hidden) at += B16 * o.lde;
+  o.ea = at; at += M16 * o.lda;
+  o.bytes = at * 2;
+}
+
+// Exchanged 16x16 tiles of a [d][B] matrix.
+inline int resident_tiles(int d, int B) { return ((d + 15) / 16) * ((B + 15) / 16); }
+
+// Plan of the layer-resident kernel for dims / B (16-bit operands, split 1
+// or 3): fills chunks (NARROW_KCHUNK columns of the top layer each), kc, nwg
+// and lds_bytes of `a` and returns the workspace bytes its flags and
+// exchange buffers need, or -1 when the net is not eligible.
+long long resident_plan(const int* dims, int L, int B, int split, ResidentArgs& a);
+
+// Lays the flags and exchange buffers out in `ws` (resident_plan's bytes).
+void resident_bind(ResidentArgs& a, char* ws);
+
+hipError_t resident_prepare(int operand, int split, int act, int lds_bytes);
+hipError_t launch_resident(const ResidentArgs& a, int operand, int split, int act, hipStream_t s);
 
 // Number of 64x64 weight-update tiles of all layers.
 int narrow_tiles(const int* dims, int L);

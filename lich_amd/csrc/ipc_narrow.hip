@@ -209,10 +209,15 @@ struct Narrow {
     }
   }
 
+  // The contraction is accumulated in partials of NARROW_KCHUNK columns that
+  // are summed in order, the order in which the layer-resident kernel adds
+  // its top-layer column chunks: a forward initialisation by this kernel then
+  // leaves that kernel's first prediction errors exactly zero as well.
   template <bool VEC, int CH>
   __device__ __forceinline__ f32x4 pred_loop(const float* wrow, bool rok, int K, const OT* fh, const OT* fl,
                                              int nsteps) {
-    f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+    constexpr int KPC = NARROW_KCHUNK / KS;  // k-steps per partial
+    f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f}, sum = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int s0 = 0; s0 < nsteps; s0 += CH) {
       float av[CH][KL];
 #pragma unroll
@@ -221,6 +226,11 @@ struct Narrow {
 #pragma unroll
       for (int i = 0; i < CH; ++i) {
         if (s0 + i < nsteps) {
+          if (s0 + i > 0 && (s0 + i) % KPC == 0) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) sum[q] = sum[q] + c[q];
+            c = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+          }
           const int kk = (s0 + i) * KS;
           OT ah[KL], al[KL], bh[KL], bl[KL];
 #pragma unroll
@@ -236,7 +246,9 @@ struct Narrow {
         }
       }
     }
-    return c;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) sum[q] = sum[q] + c[q];
+    return sum;
   }
 
   // One prediction unit: acc = W[l][rt*16 .. +16][:] f(x[l+1])[:, cols] from the staged fs block.

@@ -1,0 +1,689 @@
+// ipc_resident.hip - layer-resident whole-step kernel for narrow iPC nets (gfx950).
+//
+// The column-block whole-step kernel re-reads every W from memory in each
+// phase of each step: its grid barriers write back and invalidate the L2, and
+// a 64-wide net leaves each of those reads a serial memory round trip.  This
+// kernel keeps the weights still instead (reference trainer.py:601-679
+// semantics, T steps per launch):
+//
+//   workgroup l (l = 0 .. L-2) owns W[l] (d_l x d_{l+1}, fp32 master in MFMA
+//   result registers, 16-bit hi / lo / transposed operand copies in LDS),
+//   x[l] and x[l+1] for the whole batch; the top layer's W[L-1], whose
+//   contraction runs over the input width, is split into column chunks, one
+//   workgroup each, every one holding f(x[L]) for its chunk (x[L] is clamped).
+//
+// A step, per workgroup:
+//   1. P = W f(x[l+1]) with split-3 16-bit MFMA (hi*hi + lo*hi + hi*lo);
+//      eps[l] = x[l] - P; g = W[l]^T eps[l] (the inference term of layer l+1).
+//      Top chunks publish their partial P instead.
+//   2. publish eps[l] and g (16x16 tiles stored as each lane's four result
+//      registers, so every access is one 16-byte record) and raise the
+//      workgroup's flag; wait for the flags of the workgroups it exchanges
+//      with (the same set both ways, so a double-buffered exchange is safe).
+//   3. x[l] += gamma(-eps[l] + f'(x[l]) g[l]) with g[l] from workgroup l-1 and
+//      x[l+1] += gamma(-eps[l+1] + f'(x[l+1]) g) with eps[l+1] from workgroup
+//      l+1 (or x[L-1] minus the top chunks' partials, summed in chunk order).
+//      Both neighbours evaluate every shared state with the same operands in
+//      the same order, so their copies stay bit-identical without a second
+//      exchange.
+//   4. W[l] += alpha eps[l] f(x_new[l+1])^T over the batch with MFMA, operand
+//      copies restaged in LDS.
+// One flag exchange per step replaces the two grid barriers; W, the states
+// and the staged operands never leave the chip between steps.  The launch ends
+// by writing e, x, f(x) and W, as the column kernel's multi-step launch does.
+//
+// Every wait is bounded by a spin limit that raises the timeout flag shared
+// with the column kernel instead of hanging.
+#include "ipc_device.h"
+#include "ipc_launch.h"
+#include "ipc_narrow.h"
+
+namespace ipc {
+
+namespace {
+
+constexpr int NT = 512;  // threads per workgroup (8 waves)
+constexpr int MAXT = 4;  // output tiles per wave and phase
+
+template <typename OT> struct Vec8;
+template <> struct Vec8<f16> { typedef f16x8 T; };
+template <> struct Vec8<bf16> { typedef bf16x8 T; };
+
+__device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x4 zero4() { return f32x4{0.0f, 0.0f, 0.0f, 0.0f}; }
+
+__device__ __forceinline__ f32x4 ld4(const float* q) { return *reinterpret_cast<const f32x4*>(q); }
+__device__ __forceinline__ void st4(float* q, f32x4 v) { *reinterpret_cast<f32x4*>(q) = v; }
+
+// x + gamma(-e + f'(x) g), evaluated without contraction so that every
+// workgroup holding a copy of the state computes the same bits.
+template <int ACT>
+__device__ __forceinline__ float state_update(float x, float e, float g, float gamma) {
+#pragma clang fp contract(off)
+  return x + gamma * (-e + dact_t<ACT>(x) * g);
+}
+
+template <typename OT, int SPLIT, int ACT>
+struct Resident {
+  typedef typename Vec8<OT>::T V8;
+  static constexpr bool S3 = SPLIT >= 3;
+
+  const ResidentArgs& p;
+  OT* lds;
+  ResidentLds lay;
+  const int tid, lane, wave, lr, lg;
+  int wg, L, B, l, j, M, K, k0, ldw_g;  // ldw_g: row stride of W[l] in memory
+  bool hidden;
+  int nbt, n_pred, n_inf, n_upd, ktl, ks_k, ks_m, ks_b;
+
+  __device__ __forceinline__ Resident(const ResidentArgs& a, char* base)
+      : p(a), lds(reinterpret_cast<OT*>(base)), tid(threadIdx.x), lane(threadIdx.x & 63), wave(threadIdx.x >> 6),
+        lr(threadIdx.x & 15), lg((threadIdx.x & 63) >> 4) {
+    wg = blockIdx.x;
+    L = p.L;
+    B = p.B;
+    hidden = wg < L - 1;
+    l = hidden ? wg : L - 1;
+    j = hidden ? 0 : wg - (L - 1);
+    M = p.dims[l];
+    k0 = hidden ? 0 : j * p.kc;
+    K = hidden ? p.dims[l + 1] : min(p.kc, p.dims[L] - k0);
+    ldw_g = p.dims[l + 1];
+    resident_lds_layout(M, K, B, hidden, S3, lay);
+    nbt = (B + 15) / 16;
+    const int mtl = (M + 15) / 16;
+    ktl = (K + 15) / 16;
+    n_pred = mtl * nbt;
+    n_inf = hidden ? ktl * nbt : 0;
+    n_upd = mtl * ktl;
+    ks_k = (K + 31) / 32;
+    ks_m = (M + 31) / 32;
+    ks_b = (B + 31) / 32;
+  }
+
+  __device__ __forceinline__ V8 ld8(int off) const { return *reinterpret_cast<const V8*>(lds + off); }
+
+  // f(v) as 16-bit hi (and lo) terms into the prediction B operand [b][k] and
+  // hi into the weight-update B operand [k][b]; (k, b) outside K x B is left zero.
+  __device__ __forceinline__ void stage_f(int k, int b, float v) {
+    if (k < K && b < B) {
+      const float f = act_t<ACT>(v);
+      const OT hi = cvt<OT>(f);
+      lds[lay.fh + b * lay.ldf + k] = hi;
+      if (S3) lds[lay.fl + b * lay.ldf + k] = cvt<OT>(f - to_f32(hi));
+      lds[lay.ft + k * lay.ldft + b] = hi;
+    }
+  }
+
+  // W element (m, k) of the block into its operand copies.
+  __device__ __forceinline__ void stage_w(int m, int k, float w) {
+    const OT hi = cvt<OT>(w);
+    lds[lay.wh + m * lay.ldw + k] = hi;
+    if (S3) lds[lay.wl + m * lay.ldw + k] = cvt<OT>(w - to_f32(hi));
+    if (hidden) lds[lay.wt + k * lay.ldwt + m] = hi;
+  }
+
+  // Tile t of a [rows][B] matrix: row of result element i of this lane, and its column.
+  __device__ __forceinline__ int trow(int t, int i) const { return (t / nbt) * 16 + 4 * lg + i; }
+  __device__ __forceinline__ int tcol(int t) const { return (t % nbt) * 16 + lr; }
+  __device__ __forceinline__ int rec(int t) const { return t * RES_TILE + lane * 4; }
+
+  // acc = W_block f(x upper) for prediction tile t
+  __device__ __forceinline__ f32x4 pred_tile(int t) const {
+    const int rt = t / nbt, ct = t % nbt;
+    const int a0 = (rt * 16 + lr) * lay.ldw + lg * 8;
+    const int b0 = (ct * 16 + lr) * lay.ldf + lg * 8;
+    f32x4 c = zero4();
+    for (int ks = 0; ks < ks_k; ++ks) {
+      const V8 ah = ld8(lay.wh + a0 + ks * 32);
+      const V8 bh = ld8(lay.fh + b0 + ks * 32);
+      c = mfma16(ah, bh, c);
+      if (S3) {
+        const V8 al = ld8(lay.wl + a0 + ks * 32);
+        const V8 bl = ld8(lay.fl + b0 + ks * 32);
+        c = mfma16(al, bh, c);
+        c = mfma16(ah, bl, c);
+      }
+    }
+    return c;
+  }
+
+  // acc = W^T eps for inference tile t (rows over K)
+  __device__ __forceinline__ f32x4 infer_tile(int t) const {
+    const int rt = t / nbt, ct = t % nbt;
+    const int a0 = lay.wt + (rt * 16 + lr) * lay.ldwt + lg * 8;
+    const int b0 = lay.eb + (ct * 16 + lr) * lay.lde + lg * 8;
+    f32x4 c = zero4();
+    for (int ks = 0; ks < ks_m; ++ks) c = mfma16(ld8(a0 + ks * 32), ld8(b0 + ks * 32), c);
+    return c;
+  }
+
+  // acc = eps f(x upper)^T over the batch for update tile t (rows over M, columns over K)
+  __device__ __forceinline__ f32x4 update_tile(int t) const {
+    const int rt = t / ktl, ct = t % ktl;
+    const int a0 = lay.ea + (rt * 16 + lr) * lay.lda + lg * 8;
+    const int b0 = lay.ft + (ct * 16 + lr) * lay.ldft + lg * 8;
+    f32x4 c = zero4();
+    for (int ks = 0; ks < ks_b; ++ks) c = mfma16(ld8(a0 + ks * 32), ld8(b0 + ks * 32), c);
+    return c;
+  }
+};
+
+// Publishes step `value` for this workgroup: every store of the workgroup
+// before it becomes visible at agent scope before the flag does.
+__device__ __forceinline__ void publish(unsigned* flag, unsigned value) {
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __threadfence();
+    __hip_atomic_store(flag, value, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// Waits until every peer's flag reaches `value` (one lane of wave 0 per peer).
+__device__ __forceinline__ void wait_peers(const ResidentArgs& p, const int* peers, int npeers, unsigned value) {
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    const unsigned* f = lane < npeers ? &p.flags[peers[lane]] : nullptr;
+    int spins = 0;
+    while (true) {
+      bool ok = true;
+      if (f) ok = __hip_atomic_load(f, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) >= value;
+      if (__all(ok)) break;
+      __builtin_amdgcn_s_sleep(1);
+      if (++spins > p.spin_limit) {
+        if (lane == 0) __hip_atomic_store(&p.bar[2], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+    }
+    __threadfence();
+  }
+  __syncthreads();
+}
+
+// Hidden layer l (0 <= l <= L-2): W[l] at the update tiles, x[l] at the
+// prediction tiles, x[l+1] at the inference tiles, all resident for the launch.
+template <typename OT, int SPLIT, int ACT>
+__device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const ResidentArgs& p, const int* peers,
+                                           int npeers) {
+  constexpr int MU = 2;  // update tiles per wave: d_l x d_{l+1} <= 64 x 64 is at most 16 tiles
+  const int L = k.L, B = k.B, C = p.chunks, l = k.l, wave = k.wave, lg = k.lg, lr = k.lr;
+  const int npr = k.n_pred, ninf = k.n_inf;
+  const float gamma = p.gamma, alpha = p.alpha;
+  f32x4 xa[MAXT], ea[MAXT], xb[MAXT], gb[MAXT], wr[MU];
+#pragma unroll
+  for (int i = 0; i < MAXT; ++i) {
+    const int t = wave + 8 * i;
+    xa[i] = zero4(); xb[i] = zero4(); ea[i] = zero4(); gb[i] = zero4();
+    const int b = k.tcol(t);
+    if (t < npr)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = k.trow(t, q);
+        if (r < k.M && b < B) xa[i][q] = p.x[l][(long long)r * B + b];
+      }
+    if (t < ninf)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = k.trow(t, q);
+        if (r < k.K && b < B) xb[i][q] = p.x[l + 1][(long long)r * B + b];
+      }
+  }
+#pragma unroll
+  for (int i = 0; i < MU; ++i) {
+    const int t = wave + 8 * i;
+    wr[i] = zero4();
+    if (t < k.n_upd) {
+      const int c = (t % k.ktl) * 16 + lr;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = (t / k.ktl) * 16 + 4 * lg + q;
+        if (r < k.M && c < k.K) wr[i][q] = p.w[l][(long long)r * k.ldw_g + c];
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < MAXT; ++i) {
+    const int t = wave + 8 * i;
+    if (t < ninf)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) k.stage_f(k.trow(t, q), k.tcol(t), xb[i][q]);
+  }
+#pragma unroll
+  for (int i = 0; i < MU; ++i) {
+    const int t = wave + 8 * i;
+    if (t < k.n_upd) {
+      const int c = (t % k.ktl) * 16 + lr;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = (t / k.ktl) * 16 + 4 * lg + q;
+        if (r < k.M && c < k.K) k.stage_w(r, c, wr[i][q]);
+      }
+    }
+  }
+  __syncthreads();
+
+  const bool from_top = l + 1 == L - 1;
+  for (int s = 0; s < p.steps; ++s) {
+    const int buf = s & 1;
+    // ---- 1. eps[l] = x[l] - W f(x[l+1]); g = W^T eps[l]
+    float* xe = l >= 1 ? p.xe[l] + (long long)buf * npr * RES_TILE : nullptr;
+#pragma unroll
+    for (int i = 0; i < MAXT; ++i) {
+      const int t = wave + 8 * i;
+      if (t < npr) {
+        const f32x4 c = k.pred_tile(t);
+        const int b = k.tcol(t);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int r = k.trow(t, q);
+          const bool in = r < k.M && b < B;
+          const float ev = in ? xa[i][q] - c[q] : 0.0f;
+          ea[i][q] = ev;
+          if (in) {
+            const OT eo = cvt<OT>(ev);
+            k.lds[k.lay.eb + b * k.lay.lde + r] = eo;
+            k.lds[k.lay.ea + r * k.lay.lda + b] = eo;
+          }
+        }
+        if (xe) st4(xe + k.rec(t), ea[i]);
+      }
+    }
+    __syncthreads();
+    float* xg = p.xg[l] + (long long)buf * ninf * RES_TILE;
+#pragma unroll
+    for (int i = 0; i < MAXT; ++i) {
+      const int t = wave + 8 * i;
+      if (t < ninf) {
+        gb[i] = k.infer_tile(t);
+        st4(xg + k.rec(t), gb[i]);
+      }
+    }
+    // ---- 2. exchange
+    publish(&p.flags[k.wg], (unsigned)(s + 1));
+    wait_peers(p, peers, npeers, (unsigned)(s + 1));
+    // ---- 3. x[l] with g[l] from workgroup l-1; x[l+1] with eps[l+1] from above
+    if (l >= 1) {
+      const float* xgl = p.xg[l - 1] + (long long)buf * npr * RES_TILE;
+#pragma unroll
+      for (int i = 0; i < MAXT; ++i) {
+        const int t = wave + 8 * i;
+        if (t < npr) {
+          const f32x4 g = ld4(xgl + k.rec(t));
+#pragma unroll
+          for (int q = 0; q < 4; ++q) xa[i][q] = state_update<ACT>(xa[i][q], ea[i][q], g[q], gamma);
+        }
+      }
+    }
+    const float* xeu = from_top ? p.xp + (long long)buf * C * ninf * RES_TILE
+                                : p.xe[l + 1] + (long long)buf * ninf * RES_TILE;
+#pragma unroll
+    for (int i = 0; i < MAXT; ++i) {
+      const int t = wave + 8 * i;
+      if (t < ninf) {
+        f32x4 eu = ld4(xeu + k.rec(t));
+        if (from_top) {
+          // eps[L-1] = x[L-1] - (P_0 + P_1 + ...), the top chunks' partials in chunk order
+          for (int c = 1; c < C; ++c) {
+            const f32x4 v = ld4(xeu + (long long)c * ninf * RES_TILE + k.rec(t));
+#pragma unroll
+            for (int q = 0; q < 4; ++q) eu[q] = eu[q] + v[q];
+          }
+#pragma unroll
+          for (int q = 0; q < 4; ++q) eu[q] = xb[i][q] - eu[q];
+        }
+        const int b = k.tcol(t);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          xb[i][q] = state_update<ACT>(xb[i][q], eu[q], gb[i][q], gamma);
+          k.stage_f(k.trow(t, q), b, xb[i][q]);
+        }
+      }
+    }
+    __syncthreads();
+    // ---- 4. W[l] += alpha eps[l] f(x_new[l+1])^T
+#pragma unroll
+    for (int i = 0; i < MU; ++i) {
+      const int t = wave + 8 * i;
+      if (t < k.n_upd) {
+        const f32x4 c = k.update_tile(t);
+        const int col = (t % k.ktl) * 16 + lr;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int r = (t / k.ktl) * 16 + 4 * lg + q;
+          if (r < k.M && col < k.K) {
+#pragma clang fp contract(off)
+            wr[i][q] = wr[i][q] + alpha * c[q];
+            k.stage_w(r, col, wr[i][q]);
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  // ---- results: eps[l] of the last step, x[l] and f(x[l]) (l >= 1), W[l]
+  float* E = p.e[l];
+  float* X = l >= 1 ? p.x[l] : nullptr;
+  float* FX = l >= 1 ? p.fx[l] : nullptr;
+#pragma unroll
+  for (int i = 0; i < MAXT; ++i) {
+    const int t = wave + 8 * i;
+    if (t < npr) {
+      const int b = k.tcol(t);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = k.trow(t, q);
+        if (r < k.M && b < B) {
+          const long long o = (long long)r * B + b;
+          E[o] = ea[i][q];
+          if (X) X[o] = xa[i][q];
+          if (FX) FX[o] = act_t<ACT>(xa[i][q]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < MU; ++i) {
+    const int t = wave + 8 * i;
+    if (t < k.n_upd) {
+      const int c = (t % k.ktl) * 16 + lr;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = (t / k.ktl) * 16 + 4 * lg + q;
+        if (r < k.M && c < k.K) p.w[l][(long long)r * k.ldw_g + c] = wr[i][q];
+      }
+    }
+  }
+}
+
+// Top-layer chunk j: columns [k0, k0 + K) of W[L-1] at the update tiles,
+// x[L-1] at the prediction tiles, f(x[L]) of the chunk in LDS.
+template <typename OT, int SPLIT, int ACT>
+__device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const ResidentArgs& p, const int* peers,
+                                        int npeers) {
+  const int L = k.L, B = k.B, C = p.chunks, l = k.l, j = k.j, wave = k.wave, lg = k.lg, lr = k.lr;
+  const int npr = k.n_pred;
+  const float gamma = p.gamma, alpha = p.alpha;
+  f32x4 xa[MAXT], pc[MAXT], wr[MAXT];
+#pragma unroll
+  for (int i = 0; i < MAXT; ++i) {
+    const int t = wave + 8 * i;
+    xa[i] = zero4(); wr[i] = zero4(); pc[i] = zero4();
+    if (t < npr) {
+      const int b = k.tcol(t);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = k.trow(t, q);
+        if (r < k.M && b < B) xa[i][q] = p.x[l][(long long)r * B + b];
+      }
+    }
+    if (t < k.n_upd) {
+      const int c = (t % k.ktl) * 16 + lr;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = (t / k.ktl) * 16 + 4 * lg + q;
+        if (r < k.M && c < k.K) wr[i][q] = p.w[l][(long long)r * k.ldw_g + k.k0 + c];
+      }
+    }
+  }
+  {
+    // f(x[L]) of the chunk (x[L] is clamped: staged once); also written to fx[L]
+    const float* XL = p.x[L];
+    float* FL = p.fx[L];
+    for (int idx = threadIdx.x; idx < k.K * B; idx += NT) {
+      const int kk = idx / B, b = idx - kk * B;
+      const long long o = (long long)(k.k0 + kk) * B + b;
+      const float v = XL[o];
+      k.stage_f(kk, b, v);
+      if (FL) FL[o] = act_t<ACT>(v);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < MAXT; ++i) {
+    const int t = wave + 8 * i;
+    if (t < k.n_upd) {
+      const int c = (t % k.ktl) * 16 + lr;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = (t / k.ktl) * 16 + 4 * lg + q;
+        if (r < k.M && c < k.K) k.stage_w(r, c, wr[i][q]);
+      }
+    }
+  }
+  __syncthreads();
+
+  const bool writes_rows = j == 0;  // chunk 0 writes e, x and f(x) of layer L-1
+  for (int s = 0; s < p.steps; ++s) {
+    const int buf = s & 1;
+    const bool last = s + 1 == p.steps;
+    // ---- 1. partial product of the chunk
+    float* xp = p.xp + (long long)buf * C * npr * RES_TILE;
+#pragma unroll
+    for (int i = 0; i < MAXT; ++i) {
+      const int t = wave + 8 * i;
+      if (t < npr) {
+        pc[i] = k.pred_tile(t);
+        st4(xp + (long long)j * npr * RES_TILE + k.rec(t), pc[i]);
+      }
+    }
+    // ---- 2. exchange
+    publish(&p.flags[k.wg], (unsigned)(s + 1));
+    wait_peers(p, peers, npeers, (unsigned)(s + 1));
+    // ---- 3. eps[L-1] = x[L-1] - (P_0 + P_1 + ...) in chunk order, x[L-1] with g from workgroup L-2
+    const float* xg = p.xg[L - 2] + (long long)buf * npr * RES_TILE;
+#pragma unroll
+    for (int i = 0; i < MAXT; ++i) {
+      const int t = wave + 8 * i;
+      if (t < npr) {
+        f32x4 sum = j == 0 ? pc[i] : ld4(xp + k.rec(t));
+        for (int c = 1; c < C; ++c) {
+          const f32x4 v = c == j ? pc[i] : ld4(xp + (long long)c * npr * RES_TILE + k.rec(t));
+#pragma unroll
+          for (int q = 0; q < 4; ++q) sum[q] = sum[q] + v[q];
+        }
+        const f32x4 g = ld4(xg + k.rec(t));
+        const int b = k.tcol(t);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int r = k.trow(t, q);
+          const bool in = r < k.M && b < B;
+          const float ev = in ? xa[i][q] - sum[q] : 0.0f;
+          if (in) k.lds[k.lay.ea + r * k.lay.lda + b] = cvt<OT>(ev);
+          xa[i][q] = state_update<ACT>(xa[i][q], ev, g[q], gamma);
+          if (last && writes_rows && in) {
+            const long long o = (long long)r * B + b;
+            p.e[l][o] = ev;
+            p.x[l][o] = xa[i][q];
+            if (p.fx[l]) p.fx[l][o] = act_t<ACT>(xa[i][q]);
+          }
+        }
+      }
+    }
+    __syncthreads();
+    // ---- 4. W[L-1][:, chunk] += alpha eps[L-1] f(x[L])[chunk]^T
+#pragma unroll
+    for (int i = 0; i < MAXT; ++i) {
+      const int t = wave + 8 * i;
+      if (t < k.n_upd) {
+        const f32x4 c = k.update_tile(t);
+        const int col = (t % k.ktl) * 16 + lr;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int r = (t / k.ktl) * 16 + 4 * lg + q;
+          if (r < k.M && col < k.K) {
+#pragma clang fp contract(off)
+            wr[i][q] = wr[i][q] + alpha * c[q];
+            k.stage_w(r, col, wr[i][q]);
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < MAXT; ++i) {
+    const int t = wave + 8 * i;
+    if (t < k.n_upd) {
+      const int c = (t % k.ktl) * 16 + lr;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = (t / k.ktl) * 16 + 4 * lg + q;
+        if (r < k.M && c < k.K) p.w[l][(long long)r * k.ldw_g + k.k0 + c] = wr[i][q];
+      }
+    }
+  }
+}
+
+template <typename OT, int SPLIT, int ACT>
+__global__ void __launch_bounds__(NT) resident_kernel(const ResidentArgs args) {
+  using R = Resident<OT, SPLIT, ACT>;
+  extern __shared__ __align__(16) char lds_raw[];
+  // The argument block is indexed with run-time layer numbers; a copy in LDS
+  // serves those reads at LDS latency instead of a memory round trip each.
+  __shared__ ResidentArgs p;
+  __shared__ int peers[RES_MAX_WG];
+  __shared__ int npeers;
+  static_assert(sizeof(ResidentArgs) % 4 == 0, "argument block copy");
+  for (int i = threadIdx.x; i < (int)(sizeof(ResidentArgs) / 4); i += NT)
+    reinterpret_cast<int*>(&p)[i] = reinterpret_cast<const int*>(&args)[i];
+  for (int i = threadIdx.x; i < args.lds_bytes / 16; i += NT)
+    reinterpret_cast<uint4*>(lds_raw)[i] = uint4{0u, 0u, 0u, 0u};
+  __syncthreads();
+  R k(p, lds_raw);
+  if (threadIdx.x == 0) {
+    // the workgroups this one exchanges with, in both directions
+    const int L = k.L, C = p.chunks, top0 = L - 1;
+    int n = 0;
+    if (k.hidden) {
+      if (k.l >= 1) peers[n++] = k.l - 1;
+      if (k.l + 1 <= L - 2) peers[n++] = k.l + 1;
+      else
+        for (int c = 0; c < C; ++c) peers[n++] = top0 + c;
+    } else {
+      peers[n++] = L - 2;
+      for (int c = 0; c < C; ++c)
+        if (c != k.j) peers[n++] = top0 + c;
+    }
+    npeers = n;
+  }
+  __syncthreads();
+  if (k.hidden) run_hidden(k, p, peers, npeers);
+  else run_top(k, p, peers, npeers);
+
+  // last workgroup out clears the flags and the exit counter for the next launch
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned prev = __hip_atomic_fetch_add(&p.bar[1], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    if (prev == (unsigned)p.nwg - 1) {
+      for (int w = 0; w < p.nwg; ++w) __hip_atomic_store(&p.flags[w], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&p.bar[1], 0u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+// ---------------------------------------------------------------- dispatch
+template <typename OT, int SPLIT, int ACT>
+struct ResLaunch {
+  static hipError_t prepare(int bytes) {
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(&resident_kernel<OT, SPLIT, ACT>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  }
+  static hipError_t launch(const ResidentArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL((resident_kernel<OT, SPLIT, ACT>), dim3(a.nwg), dim3(NT), (size_t)a.lds_bytes, s, a);
+    return hipGetLastError();
+  }
+};
+
+template <typename OT, int SPLIT>
+hipError_t by_act(int act, bool prep, int bytes, const ResidentArgs* a, hipStream_t s) {
+#define IPC_RES_CASE(A)                                                                  \
+  case A:                                                                                \
+    return prep ? ResLaunch<OT, SPLIT, A>::prepare(bytes) : ResLaunch<OT, SPLIT, A>::launch(*a, s);
+  switch (act) {
+    IPC_RES_CASE(ACT_RELU)
+    IPC_RES_CASE(ACT_TANH)
+    IPC_RES_CASE(ACT_SIGMOID)
+    IPC_RES_CASE(ACT_SILU)
+    IPC_RES_CASE(ACT_GELU)
+    default:
+      return prep ? ResLaunch<OT, SPLIT, ACT_IDENTITY>::prepare(bytes) : ResLaunch<OT, SPLIT, ACT_IDENTITY>::launch(*a, s);
+  }
+#undef IPC_RES_CASE
+}
+
+hipError_t dispatch(int operand, int split, int act, bool prep, int bytes, const ResidentArgs* a, hipStream_t s) {
+  if (operand == DT_F16) return split >= 3 ? by_act<f16, 3>(act, prep, bytes, a, s) : by_act<f16, 1>(act, prep, bytes, a, s);
+  if (operand == DT_BF16)
+    return split >= 3 ? by_act<bf16, 3>(act, prep, bytes, a, s) : by_act<bf16, 1>(act, prep, bytes, a, s);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+long long resident_plan(const int* dims, int L, int B, int split, ResidentArgs& a) {
+  if (L < 2 || L > NARROW_MAX_L || B < 1 || B > RES_MAX_B) return -1;
+  for (int l = 0; l < L; ++l)
+    if (dims[l] < 1 || dims[l] > RES_MAX_WIDTH) return -1;
+  const bool s3 = split >= 3;
+  const int limit = NARROW_LDS_LIMIT - 2048;  // static LDS: argument copy and peer list
+  int need = 0;
+  for (int l = 0; l + 1 < L; ++l) {
+    ResidentLds o;
+    resident_lds_layout(dims[l], dims[l + 1], B, true, s3, o);
+    need = o.bytes > need ? o.bytes : need;
+  }
+  // top layer: one workgroup per NARROW_KCHUNK columns (the column kernel's
+  // partial-sum order)
+  const int dL = dims[L], kc = NARROW_KCHUNK, C = (dL + kc - 1) / kc;
+  if ((L - 1) + C > RES_MAX_WG) return -1;
+  ResidentLds o;
+  resident_lds_layout(dims[L - 1], dL < kc ? dL : kc, B, false, s3, o);
+  need = o.bytes > need ? o.bytes : need;
+  if (need > limit) return -1;
+  a.L = L;
+  a.B = B;
+  a.chunks = C;
+  a.kc = kc;
+  a.nwg = (L - 1) + C;
+  a.lds_bytes = res_round(need, 16);
+  for (int l = 0; l <= L; ++l) a.dims[l] = dims[l];
+  long long bytes = 256;  // flags
+  for (int l = 0; l + 1 < L; ++l) {
+    if (l >= 1) bytes += 2LL * resident_tiles(dims[l], B) * RES_TILE * 4;
+    bytes += 2LL * resident_tiles(dims[l + 1], B) * RES_TILE * 4;
+  }
+  bytes += 2LL * C * resident_tiles(dims[L - 1], B) * RES_TILE * 4;
+  return bytes;
+}
+
+void resident_bind(ResidentArgs& a, char* ws) {
+  const int L = a.L, B = a.B;
+  a.flags = reinterpret_cast<unsigned*>(ws);
+  char* at = ws + 256;
+  for (int l = 0; l < NARROW_MAX_L; ++l) { a.xe[l] = nullptr; a.xg[l] = nullptr; }
+  for (int l = 0; l + 1 < L; ++l) {
+    if (l >= 1) {
+      a.xe[l] = reinterpret_cast<float*>(at);
+      at += 2LL * resident_tiles(a.dims[l], B) * RES_TILE * 4;
+    }
+    a.xg[l] = reinterpret_cast<float*>(at);
+    at += 2LL * resident_tiles(a.dims[l + 1], B) * RES_TILE * 4;
+  }
+  a.xp = reinterpret_cast<float*>(at);
+}
+
+hipError_t resident_prepare(int operand, int split, int act, int lds_bytes) {
+  return dispatch(operand, split, act, true, lds_bytes, nullptr, nullptr);
+}
+
+hipError_t launch_resident(const ResidentArgs& a, int operand, int split, int act, hipStream_t s) {
+  return dispatch(operand, split, act, false, 0, &a, s);
+}
+
+}  // namespace ipc

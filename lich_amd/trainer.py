@@ -66,9 +66,10 @@ class IPCConfig:
     # latency-bound whole-step kernel, where the extra MFMAs are free) and 2
     # otherwise (the MFMA-bound wide path).
     pred_split: int | None = None
-    # Kernel path: "auto" (whole-step kernel for narrow nets, else the wide
-    # GEMM path when eligible, else phased), "narrow" / "on", "wide",
-    # "phased" / "off".
+    # Kernel path: "auto" (the layer-resident whole-step kernel when eligible,
+    # else the column-block whole-step kernel for narrow nets, else the wide
+    # GEMM path when eligible, else phased), "resident", "narrow" / "on",
+    # "wide", "phased" / "off".
     fused: str = "auto"
 
 
@@ -213,8 +214,9 @@ class HipIPC:
 
     @property
     def path(self) -> str | None:
-        """Kernel path of the bound plan: "narrow" (whole-step kernel), "wide"
-        (LDS-DMA MFMA phases over 16-bit operand copies) or "phased"."""
+        """Kernel path of the bound plan: "resident" (layer-resident whole-step
+        kernel), "narrow" (column-block whole-step kernel), "wide" (LDS-DMA
+        MFMA phases over 16-bit operand copies) or "phased"."""
         if self._plan is None:
             return None
         return nat.PATH_NAMES[int(nat.lib().ipc_plan_path(self._plan))]

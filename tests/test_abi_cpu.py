@@ -203,14 +203,81 @@ def test_plan_path_selection_and_wide_workspace():
         assert lib.ipc_plan_path(h) == nat.PATH_PHASED and lib.ipc_plan_workspace_bytes(h) == 0
     finally:
         lib.ipc_plan_destroy(h)
-    # a narrow net keeps the whole-step kernel under AUTO
+    # a narrow net keeps a whole-step kernel under AUTO: the layer-resident one
+    # for 16-bit operands, the column-block one when asked for or for fp32
     narrow = (ctypes.c_int * 4)(10, 64, 64, 784)
-    assert lib.ipc_plan_create(ctypes.byref(h), 3, narrow, 128, 0, 1, 3, 2, 1e-4, 0.5, 1, 0, -1) == nat.IPC_OK
+    for operand, path, want in ((1, -1, nat.PATH_RESIDENT), (1, 1, nat.PATH_NARROW), (0, -1, nat.PATH_NARROW)):
+        assert lib.ipc_plan_create(ctypes.byref(h), 3, narrow, 128, 0, operand, 3, 2, 1e-4, 0.5, 1, 0, path) == nat.IPC_OK
+        try:
+            assert lib.ipc_plan_path(h) == want and lib.ipc_plan_fused(h) == 1
+        finally:
+            lib.ipc_plan_destroy(h)
+    assert lib.ipc_plan_path(None) == -1
+
+
+def _resident_ws_bytes(dims, B, recompute):
+    """Restated workspace of a layer-resident plan: the column kernel's
+    barrier words and f(x) buffers, then 256 bytes of step flags and the
+    double-buffered exchange of 16x16 tiles (1 KiB each): eps[l] for
+    l = 1..L-2, W[l]^T eps[l] for l = 0..L-2, and one partial product per
+    128-column chunk of the top layer."""
+    L = len(dims) - 1
+    n = 256
+    if recompute:
+        n += sum((dims[l] * B * 4 + 255) // 256 * 256 for l in range(1, L + 1))
+    n = (n + 255) // 256 * 256 + 256
+
+    def tiles(d):
+        return -(-d // 16) * -(-B // 16)
+
+    for l in range(L - 1):
+        if l >= 1:
+            n += 2 * tiles(dims[l]) * 1024
+        n += 2 * tiles(dims[l + 1]) * 1024
+    return n + 2 * -(-dims[L] // 128) * tiles(dims[L - 1]) * 1024
+
+
+@pytest.mark.parametrize("dims,B,recompute", [
+    ((10, 64, 64, 64, 64, 64, 64, 784), 128, 1),
+    ((10, 64, 784), 128, 0),
+    ((7, 33, 48, 130), 40, 1),
+    ((3, 64, 100), 17, 1),
+])
+def test_resident_plan_workspace(dims, B, recompute):
+    lib = _lib()
+    h = ctypes.c_void_p()
+    L = len(dims) - 1
+    d = (ctypes.c_int * (L + 1))(*dims)
+    assert lib.ipc_plan_create(ctypes.byref(h), L, d, B, 0, 2, 3, 2, 1e-4, 0.5, recompute, 0, 3) == nat.IPC_OK
     try:
-        assert lib.ipc_plan_path(h) == nat.PATH_NARROW
+        assert lib.ipc_plan_path(h) == nat.PATH_RESIDENT
+        assert lib.ipc_plan_workspace_bytes(h) == _resident_ws_bytes(dims, B, recompute)
     finally:
         lib.ipc_plan_destroy(h)
-    assert lib.ipc_plan_path(None) == -1
+
+
+@pytest.mark.parametrize("dims,B,operand,split,wmode,why", [
+    ((10, 64, 64, 784), 128, 0, 1, 0, "fp32 operands"),
+    ((10, 64, 64, 784), 256, 1, 3, 0, "batch above 128"),
+    ((10, 128, 64, 784), 128, 1, 3, 0, "hidden width above 64"),
+    ((10, 784), 128, 1, 3, 0, "a single layer"),
+    ((10, 64, 64, 784), 8, 1, 3, 2, "rank-B outer-product weight update"),
+    ((10, 64, 64, 784), 128, 1, 2, 0, "split 2"),
+])
+def test_resident_path_refuses_ineligible_nets(dims, B, operand, split, wmode, why):
+    lib = _lib()
+    h = ctypes.c_void_p()
+    L = len(dims) - 1
+    d = (ctypes.c_int * (L + 1))(*dims)
+    rc = lib.ipc_plan_create(ctypes.byref(h), L, d, B, 0, operand, split, 2, 1e-4, 0.5, 1, wmode, 3)
+    assert rc == nat.ERR_CONFIG, why
+    assert "layer-resident" in nat.last_error()
+    # AUTO then picks another path
+    if lib.ipc_plan_create(ctypes.byref(h), L, d, B, 0, operand, split, 2, 1e-4, 0.5, 1, wmode, -1) == nat.IPC_OK:
+        try:
+            assert lib.ipc_plan_path(h) != nat.PATH_RESIDENT
+        finally:
+            lib.ipc_plan_destroy(h)
 
 
 def test_check_maps_codes_to_exceptions():

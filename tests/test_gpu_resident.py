@@ -1,0 +1,139 @@
+"""Layer-resident whole-step kernel (multi-step launches of narrow 16-bit-operand plans).
+
+* Against the fp32 oracle after T steps: states <= 2e-2, weight deltas <= 5e-3
+  (the 16-bit operand bars), on ragged shapes: widths and batches that are not
+  multiples of 16, a top layer whose last 128-column chunk is partial, L = 2
+  (one hidden-layer workgroup next to the top chunks).
+* Against the column-block whole-step kernel: the same operands, the same
+  MFMA chains and the same 128-column partial-sum order, so every state,
+  error and weight must agree bit for bit.
+* Launch boundaries do not change bits, and no wait ever hits its spin limit.
+"""
+import pytest
+import torch
+
+from lich_amd.trainer import HipIPC, IPCConfig
+from oracle import ipc_oracle as O
+from tests.helpers import DEV, report
+
+pytestmark = pytest.mark.gpu
+
+F16, BF16 = torch.float16, torch.bfloat16
+
+SHAPES = [
+    ((10, 64, 784), 128),
+    ((10, 64, 64, 64, 784), 128),
+    ((10,) + (64,) * 6 + (784,), 128),
+    ((7, 33, 48, 130), 40),
+    ((10, 48, 64, 40, 300), 100),
+    ((3, 64, 64, 100), 17),
+]
+
+
+def _model(dims, w0, act, op, path, split=None, recompute=True):
+    cfg = IPCConfig(dims=dims, activation=act, dtype=op, fused=path, pred_split=split,
+                    recompute_activation=recompute)
+    return HipIPC(cfg, device=DEV, weights=w0)
+
+
+def _run(dims, B, act, op, path, T, seed, split=None):
+    w0 = O.init_weights(dims, seed=seed, init="xavier_uniform")
+    x_in, _labels, y = O.make_batch(dims, B, seed=seed)
+    m = _model(dims, w0, act, op, path, split)
+    m.initialize_batch(x_in.to(DEV), y.to(DEV))
+    m.run_steps(T)
+    torch.cuda.synchronize()
+    return m, w0, x_in, y
+
+
+@pytest.mark.parametrize("op", [F16, BF16])
+@pytest.mark.parametrize("dims,B", SHAPES)
+def test_resident_matches_oracle(dims, B, op):
+    T, act = 4, "tanh"
+    report("resident-oracle", dims=dims, B=B, op=op)
+    m, w0, x_in, y = _run(dims, B, act, op, "resident", T, seed=3)
+    assert m.path == "resident" and m.barrier_timeouts() == 0
+    x = O.forward_init(x_in, y, w0, act)
+    x_t, w_t, e_t = O.run_steps(x, w0, T, act=act, alpha=1e-4, gamma=0.5)
+    L = len(w0)
+    s_err = O.global_rel_err([m.x[l] for l in range(1, L)], [x_t[l] for l in range(1, L)])
+    dw = [m.w[l].double().cpu() - w0[l].double() for l in range(L)]
+    dw_ref = [w_t[l].double() - w0[l].double() for l in range(L)]
+    dw_err = O.global_rel_err(dw, dw_ref)
+    print(f"resident {dims} B={B} {op}: state_err={s_err:.3e} dW_err={dw_err:.3e}")
+    assert s_err <= 2e-2 and dw_err <= 5e-3
+
+
+@pytest.mark.parametrize("act", ["tanh", "relu", "sigmoid", "gelu"])
+@pytest.mark.parametrize("op,split", [(F16, 3), (BF16, 3), (F16, 1)])
+@pytest.mark.parametrize("dims,B", [SHAPES[2], SHAPES[3], SHAPES[4]])
+def test_resident_equals_column_kernel_bitwise(dims, B, op, split, act):
+    T = 5
+    report("resident-vs-column", dims=dims, B=B, op=op, split=split, act=act)
+    ms = [_run(dims, B, act, op, path, T, seed=4, split=split)[0] for path in ("resident", "narrow")]
+    assert [m.path for m in ms] == ["resident", "narrow"]
+    res, col = ms
+    for name, a, b in (("x", res.x, col.x), ("e", res.e[:-1], col.e[:-1]), ("w", res.w, col.w)):
+        for l, (u, v) in enumerate(zip(a, b)):
+            assert torch.equal(u, v), (name, l, float((u - v).abs().max()))
+    assert res.barrier_timeouts() == 0
+
+
+def test_resident_launch_boundaries_do_not_change_bits():
+    dims, B = (10,) + (64,) * 6 + (784,), 128
+    report("resident-launches", dims=dims, B=B)
+    w0 = O.init_weights(dims, seed=5, init="xavier_uniform")
+    x_in, _labels, y = O.make_batch(dims, B, seed=5)
+    ms = []
+    for chunks in ((8,), (3, 1, 4), (1,) * 8):
+        m = _model(dims, w0, "tanh", F16, "resident")
+        m.initialize_batch(x_in.to(DEV), y.to(DEV))
+        for n in chunks:
+            m.run_steps(n)
+        ms.append(m)
+    torch.cuda.synchronize()
+    for m in ms[1:]:
+        for a, b in zip(ms[0].w + ms[0].x + ms[0].e[:-1], m.w + m.x + m.e[:-1]):
+            assert torch.equal(a, b)
+    assert all(m.barrier_timeouts() == 0 for m in ms)
+
+
+def test_resident_forward_init_leaves_errors_exactly_zero():
+    """The column kernel's forward initialisation sums the top layer in the
+    same 128-column partials as the resident top chunks, so the first step's
+    hidden errors are exactly zero and after T steps dW[l] == 0 for l >= T."""
+    dims, B, T = (10,) + (64,) * 6 + (784,), 128, 3
+    report("resident-wavefront", dims=dims, B=B)
+    w0 = O.init_weights(dims, seed=6, init="xavier_uniform")
+    x_in, _labels, y = O.make_batch(dims, B, seed=6)
+    m = _model(dims, w0, "tanh", F16, "resident")
+    m.initialize_batch(x_in.to(DEV), y.to(DEV))
+    m.run_steps(1)
+    torch.cuda.synchronize()
+    for l in range(1, len(w0)):
+        assert torch.count_nonzero(m.e[l]) == 0, l
+    m.run_steps(T - 1)
+    torch.cuda.synchronize()
+    for l in range(len(w0)):
+        nz = torch.count_nonzero(m.w[l].cpu() - w0[l])
+        assert (nz == 0) if l >= T else (nz > 0), l
+
+
+def test_resident_save_mode_writes_activations():
+    dims, B, T = (10, 64, 64, 784), 64, 4
+    report("resident-save", dims=dims, B=B)
+    w0 = O.init_weights(dims, seed=7, init="xavier_uniform")
+    x_in, _labels, y = O.make_batch(dims, B, seed=7)
+    ms = []
+    for recompute in (True, False):
+        m = _model(dims, w0, "silu", BF16, "resident", recompute=recompute)
+        m.initialize_batch(x_in.to(DEV), y.to(DEV))
+        m.run_steps(T)
+        ms.append(m)
+    torch.cuda.synchronize()
+    for a, b in zip(ms[0].w + ms[0].x, ms[1].w + ms[1].x):
+        assert torch.equal(a, b)
+    saved = ms[1].a
+    for l in range(1, len(dims)):
+        ref = O.act_forward("silu", ms[1].x[l].cpu())
+        assert torch.allclose(saved[l].cpu(), ref, rtol=1e-6, atol=1e-6), l
