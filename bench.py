@@ -83,7 +83,8 @@ def time_phases(model, reps=50, replays=5):
     from lich_amd import _native as nat
 
     out = {}
-    phases = ((0, "phaseA_pred+infer"), (2, "phaseB_weight")) if model.fused else \
+    # a whole-step plan's single-phase launches run on the column-block kernel
+    phases = ((0, "column_kernel_phaseA_pred+infer"), (2, "column_kernel_phaseB_weight")) if model.fused else \
         ((0, "pred"), (1, "infer"), (2, "weight"))
     for phase, name in phases:
         graph = torch.cuda.CUDAGraph()
@@ -338,7 +339,7 @@ def main() -> int:
     elapsed, done, replay_us = run_steady(model, x, y, T, warmup, steps)
     ms_per_step = elapsed * 1e3 / done
     value = B * done / elapsed
-    log(f"headline: {ms_per_step * 1e3:.2f} us/step, {value:,.0f} samples/s, fused={model.fused}, "
+    log(f"headline: {ms_per_step * 1e3:.2f} us/step, {value:,.0f} samples/s, path={model.path}, "
         f"{model.launches_per_step()} launch(es) per step call, {replay_us:.2f} us per {T}-step replay")
 
     bf = phase_bytes_flops(dims, B)
@@ -351,10 +352,11 @@ def main() -> int:
     phases = {k: {"us": round(v, 3)} for k, v in phase_us.items()}
     log(f"phases: {phases}")
     if model.fused:
-        # the dominant (only) kernel is the whole-step kernel: one launch per
+        # the dominant (only) kernel is a whole-step kernel: one launch per
         # T-step replay, so its launch duration is the replay's GPU time
         launch_us = replay_us
-        kernel = f"whole-step kernel, {T} steps per launch"
+        name = "layer-resident whole-step kernel" if model.path == "resident" else "whole-step kernel"
+        kernel = f"{name}, {T} steps per launch"
         launch_bytes, launch_flops = T * step_bytes, T * step_flops
     else:
         dom = max(phase_us, key=phase_us.get)
@@ -388,7 +390,7 @@ def main() -> int:
         "config": {"workload": "paper profile depth 6: dims (10,64x6,784), B=128, tanh, alpha=1e-4, gamma=0.5, "
                                "T=4 steps per hipGraph replay, fp32 master x/eps/W, fp16 operands, fp32 accumulate",
                    "global_batch": B, "seq_len": None, "parallelism": "single GPU",
-                   "fused_whole_step_kernel": model.fused, "phases": phases},
+                   "fused_whole_step_kernel": model.fused, "path": model.path, "phases": phases},
         "roofline": roofline, "cpu_baseline": cpu, "wide": wide,
     }
     print(json.dumps(line), flush=True)

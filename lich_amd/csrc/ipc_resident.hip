@@ -42,8 +42,9 @@ namespace ipc {
 
 namespace {
 
-constexpr int NT = 512;  // threads per workgroup (8 waves)
-constexpr int MAXT = 4;  // output tiles per wave and phase
+constexpr int NT = 1024;  // threads per workgroup (16 waves)
+constexpr int NWV = NT / 64;
+constexpr int MAXT = 2;  // output tiles per wave and phase (32 tiles at most)
 
 template <typename OT> struct Vec8;
 template <> struct Vec8<f16> { typedef f16x8 T; };
@@ -61,6 +62,30 @@ __device__ __forceinline__ f32x4 zero4() { return f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 __device__ __forceinline__ f32x4 ld4(const float* q) { return *reinterpret_cast<const f32x4*>(q); }
 __device__ __forceinline__ void st4(float* q, f32x4 v) { *reinterpret_cast<f32x4*>(q) = v; }
 
+constexpr int PBATCH = 8;  // top-layer partial products loaded per batch
+
+// P_0 + P_1 + ... + P_{C-1} of the exchange record at `off` (partials
+// `stride` floats apart), added in chunk order; every load of a batch is
+// issued before the first add, so a batch costs one memory latency.
+__device__ __forceinline__ f32x4 sum_partials(const float* base, long long stride, int C, int off) {
+  f32x4 sum = zero4();
+  for (int c0 = 0; c0 < C; c0 += PBATCH) {
+    f32x4 v[PBATCH];
+#pragma unroll
+    for (int u = 0; u < PBATCH; ++u) v[u] = c0 + u < C ? ld4(base + (c0 + u) * stride + off) : zero4();
+#pragma unroll
+    for (int u = 0; u < PBATCH; ++u) {
+      if (c0 + u == 0) {
+        sum = v[u];
+      } else if (c0 + u < C) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) sum[q] = sum[q] + v[u][q];
+      }
+    }
+  }
+  return sum;
+}
+
 // x + gamma(-e + f'(x) g), evaluated without contraction so that every
 // workgroup holding a copy of the state computes the same bits.
 template <int ACT>
@@ -77,7 +102,7 @@ struct Resident {
   const ResidentArgs& p;
   OT* lds;
   ResidentLds lay;
-  const int tid, lane, wave, lr, lg;
+  int tid, lane, wave, lr, lg;
   int wg, L, B, l, j, M, K, k0, ldw_g;  // ldw_g: row stride of W[l] in memory
   bool hidden;
   int nbt, n_pred, n_inf, n_upd, ktl, ks_k, ks_m, ks_b;
@@ -105,6 +130,18 @@ struct Resident {
     ks_k = (K + 31) / 32;
     ks_m = (M + 31) / 32;
     ks_b = (B + 31) / 32;
+  }
+
+  // Re-derives the lane indices from an opaque copy of the thread id: every
+  // per-lane address is then recomputed in each step instead of being held
+  // in registers across the whole step loop.
+  __device__ __forceinline__ void refresh() {
+    int t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    tid = t;
+    lane = t & 63;
+    lr = t & 15;
+    lg = (t & 63) >> 4;
   }
 
   __device__ __forceinline__ V8 ld8(int off) const { return *reinterpret_cast<const V8*>(lds + off); }
@@ -211,14 +248,14 @@ __device__ __forceinline__ void wait_peers(const ResidentArgs& p, const int* pee
 template <typename OT, int SPLIT, int ACT>
 __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const ResidentArgs& p, const int* peers,
                                            int npeers) {
-  constexpr int MU = 2;  // update tiles per wave: d_l x d_{l+1} <= 64 x 64 is at most 16 tiles
+  constexpr int MU = 1;  // update tiles per wave: d_l x d_{l+1} <= 64 x 64 is at most 16 tiles
   const int L = k.L, B = k.B, C = p.chunks, l = k.l, wave = k.wave, lg = k.lg, lr = k.lr;
   const int npr = k.n_pred, ninf = k.n_inf;
   const float gamma = p.gamma, alpha = p.alpha;
   f32x4 xa[MAXT], ea[MAXT], xb[MAXT], gb[MAXT], wr[MU];
 #pragma unroll
   for (int i = 0; i < MAXT; ++i) {
-    const int t = wave + 8 * i;
+    const int t = wave + NWV * i;
     xa[i] = zero4(); xb[i] = zero4(); ea[i] = zero4(); gb[i] = zero4();
     const int b = k.tcol(t);
     if (t < npr)
@@ -236,7 +273,7 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
   }
 #pragma unroll
   for (int i = 0; i < MU; ++i) {
-    const int t = wave + 8 * i;
+    const int t = wave + NWV * i;
     wr[i] = zero4();
     if (t < k.n_upd) {
       const int c = (t % k.ktl) * 16 + lr;
@@ -249,14 +286,14 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
   }
 #pragma unroll
   for (int i = 0; i < MAXT; ++i) {
-    const int t = wave + 8 * i;
+    const int t = wave + NWV * i;
     if (t < ninf)
 #pragma unroll
       for (int q = 0; q < 4; ++q) k.stage_f(k.trow(t, q), k.tcol(t), xb[i][q]);
   }
 #pragma unroll
   for (int i = 0; i < MU; ++i) {
-    const int t = wave + 8 * i;
+    const int t = wave + NWV * i;
     if (t < k.n_upd) {
       const int c = (t % k.ktl) * 16 + lr;
 #pragma unroll
@@ -270,12 +307,14 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
 
   const bool from_top = l + 1 == L - 1;
   for (int s = 0; s < p.steps; ++s) {
+    k.refresh();
+    const int lg = k.lg, lr = k.lr;
     const int buf = s & 1;
     // ---- 1. eps[l] = x[l] - W f(x[l+1]); g = W^T eps[l]
     float* xe = l >= 1 ? p.xe[l] + (long long)buf * npr * RES_TILE : nullptr;
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) {
-      const int t = wave + 8 * i;
+      const int t = wave + NWV * i;
       if (t < npr) {
         const f32x4 c = k.pred_tile(t);
         const int b = k.tcol(t);
@@ -298,7 +337,7 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
     float* xg = p.xg[l] + (long long)buf * ninf * RES_TILE;
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) {
-      const int t = wave + 8 * i;
+      const int t = wave + NWV * i;
       if (t < ninf) {
         gb[i] = k.infer_tile(t);
         st4(xg + k.rec(t), gb[i]);
@@ -308,39 +347,56 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
     publish(&p.flags[k.wg], (unsigned)(s + 1));
     wait_peers(p, peers, npeers, (unsigned)(s + 1));
     // ---- 3. x[l] with g[l] from workgroup l-1; x[l+1] with eps[l+1] from above
-    if (l >= 1) {
-      const float* xgl = p.xg[l - 1] + (long long)buf * npr * RES_TILE;
+    // (every exchange load of the phase is issued before the first use)
+    f32x4 gl[MAXT], eu[MAXT];
+    const float* xgl = l >= 1 ? p.xg[l - 1] + (long long)buf * npr * RES_TILE : nullptr;
+    if (xgl) {
 #pragma unroll
       for (int i = 0; i < MAXT; ++i) {
-        const int t = wave + 8 * i;
-        if (t < npr) {
-          const f32x4 g = ld4(xgl + k.rec(t));
-#pragma unroll
-          for (int q = 0; q < 4; ++q) xa[i][q] = state_update<ACT>(xa[i][q], ea[i][q], g[q], gamma);
-        }
+        const int t = wave + NWV * i;
+        gl[i] = t < npr ? ld4(xgl + k.rec(t)) : zero4();
       }
     }
-    const float* xeu = from_top ? p.xp + (long long)buf * C * ninf * RES_TILE
-                                : p.xe[l + 1] + (long long)buf * ninf * RES_TILE;
+    if (!from_top) {
+      const float* xeu = p.xe[l + 1] + (long long)buf * ninf * RES_TILE;
+#pragma unroll
+      for (int i = 0; i < MAXT; ++i) {
+        const int t = wave + NWV * i;
+        eu[i] = t < ninf ? ld4(xeu + k.rec(t)) : zero4();
+      }
+    } else {
+      // eps[L-1] = x[L-1] - (P_0 + P_1 + ...), the top chunks' partials in chunk order
+      const float* xp = p.xp + (long long)buf * C * ninf * RES_TILE;
+#pragma unroll
+      for (int i = 0; i < MAXT; ++i) {
+        const int t = wave + NWV * i;
+        eu[i] = zero4();
+        if (t < ninf) {
+          const f32x4 sum = sum_partials(xp, (long long)ninf * RES_TILE, C, k.rec(t));
+#pragma unroll
+          for (int q = 0; q < 4; ++q) eu[i][q] = xb[i][q] - sum[q];
+        }
+        // one tile's batch of partials in registers at a time
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    if (xgl) {
+#pragma unroll
+      for (int i = 0; i < MAXT; ++i) {
+        const int t = wave + NWV * i;
+        if (t < npr)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) xa[i][q] = state_update<ACT>(xa[i][q], ea[i][q], gl[i][q], gamma);
+      }
+    }
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) {
-      const int t = wave + 8 * i;
+      const int t = wave + NWV * i;
       if (t < ninf) {
-        f32x4 eu = ld4(xeu + k.rec(t));
-        if (from_top) {
-          // eps[L-1] = x[L-1] - (P_0 + P_1 + ...), the top chunks' partials in chunk order
-          for (int c = 1; c < C; ++c) {
-            const f32x4 v = ld4(xeu + (long long)c * ninf * RES_TILE + k.rec(t));
-#pragma unroll
-            for (int q = 0; q < 4; ++q) eu[q] = eu[q] + v[q];
-          }
-#pragma unroll
-          for (int q = 0; q < 4; ++q) eu[q] = xb[i][q] - eu[q];
-        }
         const int b = k.tcol(t);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          xb[i][q] = state_update<ACT>(xb[i][q], eu[q], gb[i][q], gamma);
+          xb[i][q] = state_update<ACT>(xb[i][q], eu[i][q], gb[i][q], gamma);
           k.stage_f(k.trow(t, q), b, xb[i][q]);
         }
       }
@@ -349,7 +405,7 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
     // ---- 4. W[l] += alpha eps[l] f(x_new[l+1])^T
 #pragma unroll
     for (int i = 0; i < MU; ++i) {
-      const int t = wave + 8 * i;
+      const int t = wave + NWV * i;
       if (t < k.n_upd) {
         const f32x4 c = k.update_tile(t);
         const int col = (t % k.ktl) * 16 + lr;
@@ -373,7 +429,7 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
   float* FX = l >= 1 ? p.fx[l] : nullptr;
 #pragma unroll
   for (int i = 0; i < MAXT; ++i) {
-    const int t = wave + 8 * i;
+    const int t = wave + NWV * i;
     if (t < npr) {
       const int b = k.tcol(t);
 #pragma unroll
@@ -390,7 +446,7 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
   }
 #pragma unroll
   for (int i = 0; i < MU; ++i) {
-    const int t = wave + 8 * i;
+    const int t = wave + NWV * i;
     if (t < k.n_upd) {
       const int c = (t % k.ktl) * 16 + lr;
 #pragma unroll
@@ -410,11 +466,11 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
   const int L = k.L, B = k.B, C = p.chunks, l = k.l, j = k.j, wave = k.wave, lg = k.lg, lr = k.lr;
   const int npr = k.n_pred;
   const float gamma = p.gamma, alpha = p.alpha;
-  f32x4 xa[MAXT], pc[MAXT], wr[MAXT];
+  f32x4 xa[MAXT], wr[MAXT];
 #pragma unroll
   for (int i = 0; i < MAXT; ++i) {
-    const int t = wave + 8 * i;
-    xa[i] = zero4(); wr[i] = zero4(); pc[i] = zero4();
+    const int t = wave + NWV * i;
+    xa[i] = zero4(); wr[i] = zero4();
     if (t < npr) {
       const int b = k.tcol(t);
 #pragma unroll
@@ -436,17 +492,29 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
     // f(x[L]) of the chunk (x[L] is clamped: staged once); also written to fx[L]
     const float* XL = p.x[L];
     float* FL = p.fx[L];
-    for (int idx = threadIdx.x; idx < k.K * B; idx += NT) {
-      const int kk = idx / B, b = idx - kk * B;
-      const long long o = (long long)(k.k0 + kk) * B + b;
-      const float v = XL[o];
-      k.stage_f(kk, b, v);
-      if (FL) FL[o] = act_t<ACT>(v);
+    constexpr int SB = 8;  // loads in flight per thread
+    const int n = k.K * B;
+    for (int base = threadIdx.x; base < n; base += SB * NT) {
+      float v[SB];
+#pragma unroll
+      for (int u = 0; u < SB; ++u) {
+        const int idx = base + u * NT;
+        v[u] = idx < n ? XL[(long long)k.k0 * B + idx] : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < SB; ++u) {
+        const int idx = base + u * NT;
+        if (idx < n) {
+          const int kk = idx / B, b = idx - kk * B;
+          k.stage_f(kk, b, v[u]);
+          if (FL) FL[(long long)k.k0 * B + idx] = act_t<ACT>(v[u]);
+        }
+      }
     }
   }
 #pragma unroll
   for (int i = 0; i < MAXT; ++i) {
-    const int t = wave + 8 * i;
+    const int t = wave + NWV * i;
     if (t < k.n_upd) {
       const int c = (t % k.ktl) * 16 + lr;
 #pragma unroll
@@ -460,34 +528,34 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
 
   const bool writes_rows = j == 0;  // chunk 0 writes e, x and f(x) of layer L-1
   for (int s = 0; s < p.steps; ++s) {
+    k.refresh();
+    const int lg = k.lg, lr = k.lr;
     const int buf = s & 1;
     const bool last = s + 1 == p.steps;
     // ---- 1. partial product of the chunk
     float* xp = p.xp + (long long)buf * C * npr * RES_TILE;
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) {
-      const int t = wave + 8 * i;
-      if (t < npr) {
-        pc[i] = k.pred_tile(t);
-        st4(xp + (long long)j * npr * RES_TILE + k.rec(t), pc[i]);
-      }
+      const int t = wave + NWV * i;
+      if (t < npr) st4(xp + (long long)j * npr * RES_TILE + k.rec(t), k.pred_tile(t));
     }
     // ---- 2. exchange
     publish(&p.flags[k.wg], (unsigned)(s + 1));
     wait_peers(p, peers, npeers, (unsigned)(s + 1));
-    // ---- 3. eps[L-1] = x[L-1] - (P_0 + P_1 + ...) in chunk order, x[L-1] with g from workgroup L-2
+    // ---- 3. eps[L-1] = x[L-1] - (P_0 + P_1 + ...) in chunk order (this chunk's
+    // own partial read back like the others), x[L-1] with g from workgroup L-2
     const float* xg = p.xg[L - 2] + (long long)buf * npr * RES_TILE;
+    f32x4 g[MAXT];
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) {
-      const int t = wave + 8 * i;
-      if (t < npr) {
-        f32x4 sum = j == 0 ? pc[i] : ld4(xp + k.rec(t));
-        for (int c = 1; c < C; ++c) {
-          const f32x4 v = c == j ? pc[i] : ld4(xp + (long long)c * npr * RES_TILE + k.rec(t));
+      const int t = wave + NWV * i;
+      g[i] = t < npr ? ld4(xg + k.rec(t)) : zero4();
+    }
 #pragma unroll
-          for (int q = 0; q < 4; ++q) sum[q] = sum[q] + v[q];
-        }
-        const f32x4 g = ld4(xg + k.rec(t));
+    for (int i = 0; i < MAXT; ++i) {
+      const int t = wave + NWV * i;
+      if (t < npr) {
+        const f32x4 sum = sum_partials(xp, (long long)npr * RES_TILE, C, k.rec(t));
         const int b = k.tcol(t);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -495,7 +563,7 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
           const bool in = r < k.M && b < B;
           const float ev = in ? xa[i][q] - sum[q] : 0.0f;
           if (in) k.lds[k.lay.ea + r * k.lay.lda + b] = cvt<OT>(ev);
-          xa[i][q] = state_update<ACT>(xa[i][q], ev, g[q], gamma);
+          xa[i][q] = state_update<ACT>(xa[i][q], ev, g[i][q], gamma);
           if (last && writes_rows && in) {
             const long long o = (long long)r * B + b;
             p.e[l][o] = ev;
@@ -504,12 +572,13 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
           }
         }
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
     __syncthreads();
     // ---- 4. W[L-1][:, chunk] += alpha eps[L-1] f(x[L])[chunk]^T
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) {
-      const int t = wave + 8 * i;
+      const int t = wave + NWV * i;
       if (t < k.n_upd) {
         const f32x4 c = k.update_tile(t);
         const int col = (t % k.ktl) * 16 + lr;
@@ -528,7 +597,7 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
   }
 #pragma unroll
   for (int i = 0; i < MAXT; ++i) {
-    const int t = wave + 8 * i;
+    const int t = wave + NWV * i;
     if (t < k.n_upd) {
       const int c = (t % k.ktl) * 16 + lr;
 #pragma unroll
