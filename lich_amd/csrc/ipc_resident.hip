@@ -86,12 +86,20 @@ __device__ __forceinline__ f32x4 sum_partials(const float* base, long long strid
   return sum;
 }
 
-// x + gamma(-e + f'(x) g), evaluated without contraction so that every
-// workgroup holding a copy of the state computes the same bits.
-template <int ACT>
-__device__ __forceinline__ float state_update(float x, float e, float g, float gamma) {
+// x + gamma(-e + d g) with d = f'(x), evaluated without contraction so that
+// every workgroup holding a copy of the state computes the same bits.  d
+// depends on the old state only and is evaluated before the exchange.
+__device__ __forceinline__ float state_update(float x, float e, float g, float d, float gamma) {
 #pragma clang fp contract(off)
-  return x + gamma * (-e + dact_t<ACT>(x) * g);
+  return x + gamma * (-e + d * g);
+}
+
+template <int ACT>
+__device__ __forceinline__ f32x4 dact4(f32x4 x) {
+  f32x4 d;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) d[q] = dact_t<ACT>(x[q]);
+  return d;
 }
 
 template <typename OT, int SPLIT, int ACT>
@@ -343,8 +351,14 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
         st4(xg + k.rec(t), gb[i]);
       }
     }
-    // ---- 2. exchange
+    // ---- 2. exchange; f'(x[l]) and f'(x[l+1]) of the old states meanwhile
     publish(&p.flags[k.wg], (unsigned)(s + 1));
+    f32x4 da[MAXT], db[MAXT];
+#pragma unroll
+    for (int i = 0; i < MAXT; ++i) {
+      da[i] = l >= 1 ? dact4<ACT>(xa[i]) : zero4();
+      db[i] = dact4<ACT>(xb[i]);
+    }
     wait_peers(p, peers, npeers, (unsigned)(s + 1));
     // ---- 3. x[l] with g[l] from workgroup l-1; x[l+1] with eps[l+1] from above
     // (every exchange load of the phase is issued before the first use)
@@ -386,7 +400,7 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
         const int t = wave + NWV * i;
         if (t < npr)
 #pragma unroll
-          for (int q = 0; q < 4; ++q) xa[i][q] = state_update<ACT>(xa[i][q], ea[i][q], gl[i][q], gamma);
+          for (int q = 0; q < 4; ++q) xa[i][q] = state_update(xa[i][q], ea[i][q], gl[i][q], da[i][q], gamma);
       }
     }
 #pragma unroll
@@ -396,7 +410,7 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
         const int b = k.tcol(t);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          xb[i][q] = state_update<ACT>(xb[i][q], eu[i][q], gb[i][q], gamma);
+          xb[i][q] = state_update(xb[i][q], eu[i][q], gb[i][q], db[i][q], gamma);
           k.stage_f(k.trow(t, q), b, xb[i][q]);
         }
       }
@@ -539,8 +553,11 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
       const int t = wave + NWV * i;
       if (t < npr) st4(xp + (long long)j * npr * RES_TILE + k.rec(t), k.pred_tile(t));
     }
-    // ---- 2. exchange
+    // ---- 2. exchange; f'(x[L-1]) of the old state meanwhile
     publish(&p.flags[k.wg], (unsigned)(s + 1));
+    f32x4 da[MAXT];
+#pragma unroll
+    for (int i = 0; i < MAXT; ++i) da[i] = dact4<ACT>(xa[i]);
     wait_peers(p, peers, npeers, (unsigned)(s + 1));
     // ---- 3. eps[L-1] = x[L-1] - (P_0 + P_1 + ...) in chunk order (this chunk's
     // own partial read back like the others), x[L-1] with g from workgroup L-2
@@ -563,7 +580,7 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
           const bool in = r < k.M && b < B;
           const float ev = in ? xa[i][q] - sum[q] : 0.0f;
           if (in) k.lds[k.lay.ea + r * k.lay.lda + b] = cvt<OT>(ev);
-          xa[i][q] = state_update<ACT>(xa[i][q], ev, g[i][q], gamma);
+          xa[i][q] = state_update(xa[i][q], ev, g[i][q], da[i][q], gamma);
           if (last && writes_rows && in) {
             const long long o = (long long)r * B + b;
             p.e[l][o] = ev;
