@@ -16,10 +16,10 @@
 //   1. P = W f(x[l+1]) with split-3 16-bit MFMA (hi*hi + lo*hi + hi*lo);
 //      eps[l] = x[l] - P; g = W[l]^T eps[l] (the inference term of layer l+1).
 //      Top chunks publish their partial P instead.
-//   2. publish eps[l] and g (16x16 tiles stored as each lane's four result
-//      registers, so every access is one 16-byte record) and raise the
-//      workgroup's flag; wait for the flags of the workgroups it exchanges
-//      with (the same set both ways, so a double-buffered exchange is safe).
+//   2. publish eps[l] and g (16x16 result tiles, one 16-byte record per
+//      lane) and raise the workgroup's flag; wait for the flags of the
+//      workgroups it exchanges with (the same set both ways, so a
+//      double-buffered exchange is safe).
 //   3. x[l] += gamma(-eps[l] + f'(x[l]) g[l]) with g[l] from workgroup l-1 and
 //      x[l+1] += gamma(-eps[l+1] + f'(x[l+1]) g) with eps[l+1] from workgroup
 //      l+1 (or x[L-1] minus the top chunks' partials, summed in chunk order).
@@ -59,8 +59,17 @@ __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
 
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.0f, 0.0f, 0.0f, 0.0f}; }
 
-__device__ __forceinline__ f32x4 ld4(const float* q) { return *reinterpret_cast<const f32x4*>(q); }
-__device__ __forceinline__ void st4(float* q, f32x4 v) { *reinterpret_cast<f32x4*>(q) = v; }
+// floor(n / d) for 0 <= n < 2^22 and inv = 1.0f / d: (n + 0.5) / d is never
+// an integer and lies at least 0.5 / d from one, more than the product's
+// rounding error, so the float quotient truncates to the exact result (a few
+// instructions instead of an integer-division sequence).
+__device__ __forceinline__ int qdiv(int n, float inv) { return (int)(((float)n + 0.5f) * inv); }
+
+// An exchange record is one 16x16 result tile stored as every lane's four
+// result registers (16 bytes per lane), so each access is one 16-byte load or
+// store per lane.
+__device__ __forceinline__ f32x4 ld_rec(const float* r) { return *reinterpret_cast<const f32x4*>(r); }
+__device__ __forceinline__ void st_rec(float* r, f32x4 v) { *reinterpret_cast<f32x4*>(r) = v; }
 
 constexpr int PBATCH = 8;  // top-layer partial products loaded per batch
 
@@ -72,7 +81,7 @@ __device__ __forceinline__ f32x4 sum_partials(const float* base, long long strid
   for (int c0 = 0; c0 < C; c0 += PBATCH) {
     f32x4 v[PBATCH];
 #pragma unroll
-    for (int u = 0; u < PBATCH; ++u) v[u] = c0 + u < C ? ld4(base + (c0 + u) * stride + off) : zero4();
+    for (int u = 0; u < PBATCH; ++u) v[u] = c0 + u < C ? ld_rec(base + (c0 + u) * stride + off) : zero4();
 #pragma unroll
     for (int u = 0; u < PBATCH; ++u) {
       if (c0 + u == 0) {
@@ -114,6 +123,7 @@ struct Resident {
   int wg, L, B, l, j, M, K, k0, ldw_g;  // ldw_g: row stride of W[l] in memory
   bool hidden;
   int nbt, n_pred, n_inf, n_upd, ktl, ks_k, ks_m, ks_b;
+  float inv_nbt, inv_ktl, inv_B;
 
   __device__ __forceinline__ Resident(const ResidentArgs& a, char* base)
       : p(a), lds(reinterpret_cast<OT*>(base)), tid(threadIdx.x), lane(threadIdx.x & 63), wave(threadIdx.x >> 6),
@@ -138,6 +148,9 @@ struct Resident {
     ks_k = (K + 31) / 32;
     ks_m = (M + 31) / 32;
     ks_b = (B + 31) / 32;
+    inv_nbt = 1.0f / (float)nbt;
+    inv_ktl = 1.0f / (float)ktl;
+    inv_B = 1.0f / (float)B;
   }
 
   // Re-derives the lane indices from an opaque copy of the thread id: every
@@ -175,13 +188,16 @@ struct Resident {
   }
 
   // Tile t of a [rows][B] matrix: row of result element i of this lane, and its column.
-  __device__ __forceinline__ int trow(int t, int i) const { return (t / nbt) * 16 + 4 * lg + i; }
-  __device__ __forceinline__ int tcol(int t) const { return (t % nbt) * 16 + lr; }
+  __device__ __forceinline__ int trow(int t, int i) const { return qdiv(t, inv_nbt) * 16 + 4 * lg + i; }
+  __device__ __forceinline__ int tcol(int t) const { return (t - qdiv(t, inv_nbt) * nbt) * 16 + lr; }
+  // update tile t: row tile over M, column tile over K
+  __device__ __forceinline__ int urt(int t) const { return qdiv(t, inv_ktl); }
+  __device__ __forceinline__ int uct(int t) const { return t - qdiv(t, inv_ktl) * ktl; }
   __device__ __forceinline__ int rec(int t) const { return t * RES_TILE + lane * 4; }
 
   // acc = W_block f(x upper) for prediction tile t
   __device__ __forceinline__ f32x4 pred_tile(int t) const {
-    const int rt = t / nbt, ct = t % nbt;
+    const int rt = qdiv(t, inv_nbt), ct = t - rt * nbt;
     const int a0 = (rt * 16 + lr) * lay.ldw + lg * 8;
     const int b0 = (ct * 16 + lr) * lay.ldf + lg * 8;
     f32x4 c = zero4();
@@ -201,7 +217,7 @@ struct Resident {
 
   // acc = W^T eps for inference tile t (rows over K)
   __device__ __forceinline__ f32x4 infer_tile(int t) const {
-    const int rt = t / nbt, ct = t % nbt;
+    const int rt = qdiv(t, inv_nbt), ct = t - rt * nbt;
     const int a0 = lay.wt + (rt * 16 + lr) * lay.ldwt + lg * 8;
     const int b0 = lay.eb + (ct * 16 + lr) * lay.lde + lg * 8;
     f32x4 c = zero4();
@@ -211,7 +227,7 @@ struct Resident {
 
   // acc = eps f(x upper)^T over the batch for update tile t (rows over M, columns over K)
   __device__ __forceinline__ f32x4 update_tile(int t) const {
-    const int rt = t / ktl, ct = t % ktl;
+    const int rt = urt(t), ct = uct(t);
     const int a0 = lay.ea + (rt * 16 + lr) * lay.lda + lg * 8;
     const int b0 = lay.ft + (ct * 16 + lr) * lay.ldft + lg * 8;
     f32x4 c = zero4();
@@ -221,16 +237,19 @@ struct Resident {
 };
 
 // Publishes step `value` for this workgroup: every store of the workgroup
-// before it becomes visible at agent scope before the flag does.
+// before it becomes visible at agent scope before the flag does (the barrier
+// orders the other waves' stores before thread 0's fence, the fence before
+// the relaxed flag store).
 __device__ __forceinline__ void publish(unsigned* flag, unsigned value) {
   __syncthreads();
   if (threadIdx.x == 0) {
     __threadfence();
-    __hip_atomic_store(flag, value, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(flag, value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
-// Waits until every peer's flag reaches `value` (one lane of wave 0 per peer).
+// Waits until every peer's flag reaches `value` (one lane of wave 0 per peer,
+// relaxed polls, then one fence that pairs with the publishers' fences).
 __device__ __forceinline__ void wait_peers(const ResidentArgs& p, const int* peers, int npeers, unsigned value) {
   if (threadIdx.x < 64) {
     const int lane = threadIdx.x;
@@ -238,7 +257,7 @@ __device__ __forceinline__ void wait_peers(const ResidentArgs& p, const int* pee
     int spins = 0;
     while (true) {
       bool ok = true;
-      if (f) ok = __hip_atomic_load(f, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) >= value;
+      if (f) ok = __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= value;
       if (__all(ok)) break;
       __builtin_amdgcn_s_sleep(1);
       if (++spins > p.spin_limit) {
@@ -284,10 +303,10 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
     const int t = wave + NWV * i;
     wr[i] = zero4();
     if (t < k.n_upd) {
-      const int c = (t % k.ktl) * 16 + lr;
+      const int c = k.uct(t) * 16 + lr;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int r = (t / k.ktl) * 16 + 4 * lg + q;
+        const int r = k.urt(t) * 16 + 4 * lg + q;
         if (r < k.M && c < k.K) wr[i][q] = p.w[l][(long long)r * k.ldw_g + c];
       }
     }
@@ -303,10 +322,10 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
   for (int i = 0; i < MU; ++i) {
     const int t = wave + NWV * i;
     if (t < k.n_upd) {
-      const int c = (t % k.ktl) * 16 + lr;
+      const int c = k.uct(t) * 16 + lr;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int r = (t / k.ktl) * 16 + 4 * lg + q;
+        const int r = k.urt(t) * 16 + 4 * lg + q;
         if (r < k.M && c < k.K) k.stage_w(r, c, wr[i][q]);
       }
     }
@@ -338,7 +357,7 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
             k.lds[k.lay.ea + r * k.lay.lda + b] = eo;
           }
         }
-        if (xe) st4(xe + k.rec(t), ea[i]);
+        if (xe) st_rec(xe + k.rec(t), ea[i]);
       }
     }
     __syncthreads();
@@ -348,7 +367,7 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
       const int t = wave + NWV * i;
       if (t < ninf) {
         gb[i] = k.infer_tile(t);
-        st4(xg + k.rec(t), gb[i]);
+        st_rec(xg + k.rec(t), gb[i]);
       }
     }
     // ---- 2. exchange; f'(x[l]) and f'(x[l+1]) of the old states meanwhile
@@ -368,7 +387,7 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
 #pragma unroll
       for (int i = 0; i < MAXT; ++i) {
         const int t = wave + NWV * i;
-        gl[i] = t < npr ? ld4(xgl + k.rec(t)) : zero4();
+        gl[i] = t < npr ? ld_rec(xgl + k.rec(t)) : zero4();
       }
     }
     if (!from_top) {
@@ -376,7 +395,7 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
 #pragma unroll
       for (int i = 0; i < MAXT; ++i) {
         const int t = wave + NWV * i;
-        eu[i] = t < ninf ? ld4(xeu + k.rec(t)) : zero4();
+        eu[i] = t < ninf ? ld_rec(xeu + k.rec(t)) : zero4();
       }
     } else {
       // eps[L-1] = x[L-1] - (P_0 + P_1 + ...), the top chunks' partials in chunk order
@@ -422,10 +441,10 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
       const int t = wave + NWV * i;
       if (t < k.n_upd) {
         const f32x4 c = k.update_tile(t);
-        const int col = (t % k.ktl) * 16 + lr;
+        const int col = k.uct(t) * 16 + lr;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const int r = (t / k.ktl) * 16 + 4 * lg + q;
+          const int r = k.urt(t) * 16 + 4 * lg + q;
           if (r < k.M && col < k.K) {
 #pragma clang fp contract(off)
             wr[i][q] = wr[i][q] + alpha * c[q];
@@ -462,10 +481,10 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
   for (int i = 0; i < MU; ++i) {
     const int t = wave + NWV * i;
     if (t < k.n_upd) {
-      const int c = (t % k.ktl) * 16 + lr;
+      const int c = k.uct(t) * 16 + lr;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int r = (t / k.ktl) * 16 + 4 * lg + q;
+        const int r = k.urt(t) * 16 + 4 * lg + q;
         if (r < k.M && c < k.K) p.w[l][(long long)r * k.ldw_g + c] = wr[i][q];
       }
     }
@@ -494,10 +513,10 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
       }
     }
     if (t < k.n_upd) {
-      const int c = (t % k.ktl) * 16 + lr;
+      const int c = k.uct(t) * 16 + lr;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int r = (t / k.ktl) * 16 + 4 * lg + q;
+        const int r = k.urt(t) * 16 + 4 * lg + q;
         if (r < k.M && c < k.K) wr[i][q] = p.w[l][(long long)r * k.ldw_g + k.k0 + c];
       }
     }
@@ -519,7 +538,7 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
       for (int u = 0; u < SB; ++u) {
         const int idx = base + u * NT;
         if (idx < n) {
-          const int kk = idx / B, b = idx - kk * B;
+          const int kk = qdiv(idx, k.inv_B), b = idx - kk * B;
           k.stage_f(kk, b, v[u]);
           if (FL) FL[(long long)k.k0 * B + idx] = act_t<ACT>(v[u]);
         }
@@ -530,10 +549,10 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
   for (int i = 0; i < MAXT; ++i) {
     const int t = wave + NWV * i;
     if (t < k.n_upd) {
-      const int c = (t % k.ktl) * 16 + lr;
+      const int c = k.uct(t) * 16 + lr;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int r = (t / k.ktl) * 16 + 4 * lg + q;
+        const int r = k.urt(t) * 16 + 4 * lg + q;
         if (r < k.M && c < k.K) k.stage_w(r, c, wr[i][q]);
       }
     }
@@ -551,7 +570,7 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) {
       const int t = wave + NWV * i;
-      if (t < npr) st4(xp + (long long)j * npr * RES_TILE + k.rec(t), k.pred_tile(t));
+      if (t < npr) st_rec(xp + (long long)j * npr * RES_TILE + k.rec(t), k.pred_tile(t));
     }
     // ---- 2. exchange; f'(x[L-1]) of the old state meanwhile
     publish(&p.flags[k.wg], (unsigned)(s + 1));
@@ -566,7 +585,7 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) {
       const int t = wave + NWV * i;
-      g[i] = t < npr ? ld4(xg + k.rec(t)) : zero4();
+      g[i] = t < npr ? ld_rec(xg + k.rec(t)) : zero4();
     }
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) {
@@ -598,10 +617,10 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
       const int t = wave + NWV * i;
       if (t < k.n_upd) {
         const f32x4 c = k.update_tile(t);
-        const int col = (t % k.ktl) * 16 + lr;
+        const int col = k.uct(t) * 16 + lr;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const int r = (t / k.ktl) * 16 + 4 * lg + q;
+          const int r = k.urt(t) * 16 + 4 * lg + q;
           if (r < k.M && col < k.K) {
 #pragma clang fp contract(off)
             wr[i][q] = wr[i][q] + alpha * c[q];
@@ -616,10 +635,10 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
   for (int i = 0; i < MAXT; ++i) {
     const int t = wave + NWV * i;
     if (t < k.n_upd) {
-      const int c = (t % k.ktl) * 16 + lr;
+      const int c = k.uct(t) * 16 + lr;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int r = (t / k.ktl) * 16 + 4 * lg + q;
+        const int r = k.urt(t) * 16 + 4 * lg + q;
         if (r < k.M && c < k.K) p.w[l][(long long)r * k.ldw_g + k.k0 + c] = wr[i][q];
       }
     }
