@@ -247,6 +247,14 @@ int ipc_plan_sync(ipc_plan* plan, void* stream);
 #define IPC_PHASE_WEIGHT 2
 int ipc_plan_phase(ipc_plan* plan, int phase, int reps, void* stream);
 
+/* Tile ids of the phased path's three launches (IPC_TILE_AUTO = -1 keeps the
+ * automatic choice; the generic tiles 0-2 otherwise).  This is how a tuning
+ * table's per-shape kernel configuration reaches a plan, as
+ * TileLangIPC._tuned_or_default does for the reference's per-layer kernels
+ * (trainer.py:183-216); the whole-step and wide paths run fixed kernels and
+ * ignore it.  Valid before or after ipc_plan_bind. */
+int ipc_plan_set_tiles(ipc_plan* plan, int tile_pred, int tile_infer, int tile_weight);
+
 /* Kernel launches one ipc_plan_step(steps=1) enqueues. */
 int ipc_plan_launch_count(const ipc_plan* plan);
 

@@ -79,6 +79,7 @@ def _declare(lib):
         "ipc_plan_create": ([POINTER(vp), i, POINTER(c_int), i, i, i, i, i, f, f, i, i, i], i),
         "ipc_plan_fused": ([vp], i),
         "ipc_plan_path": ([vp], i),
+        "ipc_plan_set_tiles": ([vp, i, i, i], i),
         "ipc_plan_workspace_bytes": ([vp], c_longlong),
         "ipc_plan_bind": ([vp, POINTER(vp), POINTER(vp), POINTER(vp), POINTER(vp), vp], i),
         "ipc_plan_step": ([vp, i, vp], i),

@@ -398,6 +398,7 @@ struct ipc_plan {
   std::vector<GemmProblem> pred, infer, weight;
   std::vector<OuterProblem> outer;
   int tile_pred = 0, tile_infer = 0, tile_weight = 0;
+  int tile_override[3] = {IPC_TILE_AUTO, IPC_TILE_AUTO, IPC_TILE_AUTO};  // ipc_plan_set_tiles
   // forward initialisation launches (l = L-1 .. 1, sequential)
   std::vector<GemmProblem> fwd;
   const void* act_src = nullptr;  // x[L]
@@ -618,6 +619,9 @@ int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w
   plan->tile_pred = pick_tile(rows_p, B, 1);
   plan->tile_infer = rows_i ? pick_tile(rows_i, B, 1) : 0;
   plan->tile_weight = rows_w ? pick_tile(rows_w, cols_w, 1) : 0;
+  if (plan->tile_override[0] != IPC_TILE_AUTO) plan->tile_pred = plan->tile_override[0];
+  if (plan->tile_override[1] != IPC_TILE_AUTO) plan->tile_infer = plan->tile_override[1];
+  if (plan->tile_override[2] != IPC_TILE_AUTO) plan->tile_weight = plan->tile_override[2];
   plan->launches = 1 + (plan->infer.empty() ? 0 : 1) + (plan->weight.empty() ? 0 : 1) + (int)plan->outer.size();
   if (plan->narrow) {
     NarrowArgs& na = plan->nargs;
@@ -859,6 +863,21 @@ int ipc_plan_sync(ipc_plan* plan, void* stream) {
   if (!plan->wide) return ok();
   return launch_rc(launch_wide_copy(plan->wsync.data(), (int)plan->wsync.size(), plan->operand, (hipStream_t)stream),
                    "wide operand copies");
+}
+
+int ipc_plan_set_tiles(ipc_plan* plan, int tile_pred, int tile_infer, int tile_weight) {
+  if (!plan) return fail(IPC_ERR_NULL, "plan is NULL");
+  const int t[3] = {tile_pred, tile_infer, tile_weight};
+  for (int i = 0; i < 3; ++i)
+    if (t[i] != IPC_TILE_AUTO && (t[i] < IPC_TILE_32x32 || t[i] > IPC_TILE_128x128))
+      return fail(IPC_ERR_CONFIG, "plan tile %d must be IPC_TILE_AUTO or a generic tile 0-2", t[i]);
+  for (int i = 0; i < 3; ++i) plan->tile_override[i] = t[i];
+  if (plan->bound) {
+    if (t[0] != IPC_TILE_AUTO) plan->tile_pred = t[0];
+    if (t[1] != IPC_TILE_AUTO) plan->tile_infer = t[1];
+    if (t[2] != IPC_TILE_AUTO) plan->tile_weight = t[2];
+  }
+  return ok();
 }
 
 int ipc_plan_launch_count(const ipc_plan* plan) { return plan ? plan->launches : 0; }

@@ -31,7 +31,9 @@ from typing import Sequence
 import torch
 
 from . import _native as nat
+from .hierarchical_policy import kernel_signature, load_hierarchical_policy
 from .kernels import KernelConfig, build_forward
+from .tuning import config_to_dict
 
 
 @dataclass(frozen=True)
@@ -43,9 +45,13 @@ class IPCConfig:
     dtype: torch.dtype = torch.float16
     kernel: KernelConfig = field(default_factory=KernelConfig)
     recompute_activation: bool = True
+    # A lich_amd.tuning.TuningTable, consulted after the hierarchical policy
+    # (precedence of trainer.py:183-216); its configs pick the phased path's tiles.
     tuning_table: object | None = None
     # The reference's grid.z layer batching knobs (trainer.py:38-41) are
-    # accepted; every phase is already one multi-layer launch here.
+    # accepted; every phase is already one multi-layer launch here.  The
+    # hierarchical policy file, when present, selects recompute and graph use
+    # per net (its grid.z choice is recorded in ``grid_z_cap``).
     use_grid_z: bool = True
     grid_z_max_layers: int = 2
     grid_z_auto: bool = True
@@ -159,6 +165,91 @@ class HipIPC:
         self._steady_state_runner = None
         self._steady_state_graph_steps: int | None = None
         self._steady_state_graph_key = None
+        self._hierarchical_policy = None
+        if cfg.hierarchical_policy_auto:
+            try:
+                self._hierarchical_policy = load_hierarchical_policy(cfg.hierarchical_policy_path)
+            except (OSError, ValueError):
+                self._hierarchical_policy = None
+        self._runtime_recompute: bool = bool(cfg.recompute_activation)
+        self.grid_z_cap: int = int(cfg.grid_z_max_layers)
+        self._signature_cache: dict[int, str] = {}
+
+    # ------------------------------------------------------------------ tuning artefacts
+    def _tuned_or_default(self, kind: str, M: int, K: int, B: int) -> KernelConfig:
+        """Kernel configuration for one (kind, shape): the policy's per-net
+        profile, then its global entries, then the tuning table, then
+        ``cfg.kernel`` (reference ``trainer.py:183-216``)."""
+        dt = str(self.cfg.dtype).split(".")[-1]
+        pol = self._hierarchical_policy
+        if pol is not None:
+            tuned = pol.lookup_profile_kernel(dims=tuple(int(d) for d in self.cfg.dims), batch=int(B), kind=kind,
+                                              M=M, K=K, activation=self.cfg.activation, dtype=dt)
+            if tuned is None:
+                tuned = pol.lookup_kernel(kind=kind, M=M, K=K, B=B, activation=self.cfg.activation, dtype=dt)
+            if tuned is not None:
+                return tuned
+        table = self.cfg.tuning_table
+        if table is not None:
+            tuned = table.lookup(kind=kind, M=M, K=K, B=B, activation=self.cfg.activation, dtype=dt)
+            if tuned is not None:
+                return tuned
+        return self.cfg.kernel
+
+    def _kernel_rows(self, B: int) -> list[dict]:
+        rows, seen = [], set()
+        dt = str(self.cfg.dtype).split(".")[-1]
+        for l in range(self.L):
+            shapes = [("prediction", self.cfg.dims[l], self.cfg.dims[l + 1]),
+                      ("weight", self.cfg.dims[l], self.cfg.dims[l + 1])]
+            if l > 0:
+                shapes.append(("inference", self.cfg.dims[l], self.cfg.dims[l - 1]))
+            for kind, M, K in shapes:
+                if (kind, M, K) in seen:
+                    continue
+                seen.add((kind, M, K))
+                rows.append({"kind": kind, "shape": {"M": int(M), "K": int(K), "B": int(B)},
+                             "activation": self.cfg.activation, "dtype": dt,
+                             "config": config_to_dict(self._tuned_or_default(kind, int(M), int(K), int(B)))})
+        return rows
+
+    def _active_kernel_signature(self, B: int) -> str:
+        """Fingerprint of the kernel table in use (reference ``trainer.py:218-246``)."""
+        B = int(B)
+        if B not in self._signature_cache:
+            self._signature_cache[B] = kernel_signature(self._kernel_rows(B))
+        return self._signature_cache[B]
+
+    def _policy_kw(self, B: int) -> dict:
+        return dict(dims=tuple(int(d) for d in self.cfg.dims), batch=int(B), activation=self.cfg.activation,
+                    dtype=str(self.cfg.dtype).split(".")[-1], kernel_sig=self._active_kernel_signature(B))
+
+    def _apply_execution_policy(self, B: int) -> None:
+        """Recompute and grid.z choices of the policy for this net and batch
+        (reference ``trainer.py:158-177``)."""
+        self._runtime_recompute = bool(self.cfg.recompute_activation)
+        self.grid_z_cap = int(self.cfg.grid_z_max_layers)
+        pol = self._hierarchical_policy
+        if pol is not None:
+            kw = self._policy_kw(B)
+            self._runtime_recompute = pol.selected_recompute_activation(default=self._runtime_recompute, **kw)
+            self.grid_z_cap = pol.selected_grid_z(default=self.grid_z_cap, **kw)
+
+    def phase_tiles(self, B: int) -> tuple[int, int, int]:
+        """Tile ids of the phased path's launches: the tuned configuration of
+        each phase's largest layer (-1: automatic)."""
+        dims = [int(d) for d in self.cfg.dims]
+        out = []
+        for kind, layers in (("prediction", range(self.L)), ("inference", range(1, self.L)),
+                             ("weight", range(self.L))):
+            best = None
+            for l in layers:
+                M, K = (dims[l], dims[l - 1]) if kind == "inference" else (dims[l], dims[l + 1])
+                if best is None or M * K > best[0] * best[1]:
+                    best = (M, K)
+            t = nat.TILE_AUTO if best is None else self._tuned_or_default(kind, best[0], best[1], B).tile_id()
+            out.append(t if t in (0, 1, 2) else nat.TILE_AUTO)
+        return tuple(out)
 
     # ------------------------------------------------------------------ plan
     @property
@@ -167,7 +258,7 @@ class HipIPC:
 
     @property
     def recompute_activation(self) -> bool:
-        return bool(self.cfg.recompute_activation)
+        return bool(self._runtime_recompute)
 
     def __del__(self):
         self._destroy_plan()
@@ -191,6 +282,7 @@ class HipIPC:
             float(self.cfg.alpha), float(self.cfg.gamma), int(self.recompute_activation), self._wmode,
             self._fused))
         self._plan = handle
+        nat.check(nat.lib().ipc_plan_set_tiles(handle, *self.phase_tiles(B)))
         nbytes = int(nat.lib().ipc_plan_workspace_bytes(handle))
         # zero-initialised (the wide path relies on zero padding); torch's
         # allocations are 256-byte aligned as the plan requires
@@ -248,6 +340,7 @@ class HipIPC:
         if self.x is None or self.x[0].shape[1] != B:
             self._invalidate_steady_state_graph()
             self._destroy_plan()
+            self._apply_execution_policy(B)
             kw = dict(device=self.device, dtype=self.storage_dtype)
             self.x = [torch.empty((int(d), B), **kw) for d in self.cfg.dims]
             self.e = [torch.empty((int(d), B), **kw) for d in self.cfg.dims]
@@ -286,7 +379,16 @@ class HipIPC:
 
     # ------------------------------------------------------------------ steady state / graph
     def recommended_use_cuda_graph(self, batch: int | None = None, *, default: bool = True) -> bool:
-        return bool(default)
+        """The policy's graph choice for this net and batch, else ``default``
+        (reference ``trainer.py:248-262``)."""
+        pol = self._hierarchical_policy
+        if pol is None:
+            return bool(default)
+        if batch is None:
+            if self.x is None:
+                return bool(default)
+            batch = int(self.x[0].shape[1])
+        return pol.selected_use_graph(default=bool(default), **self._policy_kw(int(batch)))
 
     def _invalidate_steady_state_graph(self) -> None:
         self._steady_state_runner = None
