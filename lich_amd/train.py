@@ -50,10 +50,17 @@ def parse_args(argv=None) -> argparse.Namespace:
     return p.parse_args(argv)
 
 
-def batch_accuracy(model, x: torch.Tensor, labels: torch.Tensor) -> int:
-    """Correct predictions of ``predict(x)`` (argmax over the class rows)."""
+def batch_correct(model, x: torch.Tensor, labels: torch.Tensor) -> torch.Tensor:
+    """Correct predictions of ``predict(x)`` (argmax over the class rows), as a
+    device scalar: the loop adds them up on the device and synchronises once
+    per epoch instead of once per batch."""
     logits = model.predict(x)                     # [classes, B]
-    return int((logits.float().argmax(dim=0) == labels).sum().item())
+    return (logits.float().argmax(dim=0) == labels).sum()
+
+
+def batch_accuracy(model, x: torch.Tensor, labels: torch.Tensor) -> int:
+    """Correct predictions of ``predict(x)`` as a host integer."""
+    return int(batch_correct(model, x, labels).item())
 
 
 def train(a: argparse.Namespace):
@@ -74,7 +81,8 @@ def train(a: argparse.Namespace):
     history = []
     for epoch in range(a.epochs):
         t0 = time.perf_counter()
-        total = correct = 0
+        total = 0
+        correct = torch.zeros((), dtype=torch.int64, device=device)
         it = ds.batches(a.batch, shuffle=True, seed=a.seed, epoch=epoch, drop_last=True)
         pending = next(it, None)
         if pending is not None:
@@ -93,11 +101,11 @@ def train(a: argparse.Namespace):
                 runner.replay()
             else:
                 model.run_steps(a.steps)
-            correct += batch_accuracy(model, x, labels)
+            correct += batch_correct(model, x, labels)
             total += int(labels.numel())
-        torch.cuda.synchronize(device)
+        n_correct = int(correct.item())
         dt = time.perf_counter() - t0
-        rec = {"epoch": epoch + 1, "time_s": round(dt, 3), "train_acc": correct / max(total, 1),
+        rec = {"epoch": epoch + 1, "time_s": round(dt, 3), "train_acc": n_correct / max(total, 1),
                "samples_per_s": round(total / dt, 1), "samples": total, "path": model.path, "dataset": ds.name}
         history.append(rec)
         if a.json:
