@@ -210,8 +210,9 @@ int ipc_plan_path(const ipc_plan* plan);
  * becomes non-zero if a barrier wait ever ran past its spin limit); in
  * recompute mode the whole-step kernel keeps the f(x[l]) values phase A
  * evaluates for the weight update after them, and a layer-resident plan its
- * per-workgroup step flags (also left zero after every launch) and the
- * double-buffered eps / W^T eps exchange after those.  The wide path keeps its
+ * per-workgroup step flags (also left zero after every launch), the
+ * double-buffered eps / W^T eps exchange and the top chunks' cached 16-bit
+ * copies of f(x[L]) after those.  The wide path keeps its
  * 16-bit operand copies there (W as hi and lo terms, W^T, f(x) and eps in
  * both layouts, zero padded); their padding must stay zero. */
 long long ipc_plan_workspace_bytes(const ipc_plan* plan);
@@ -234,7 +235,9 @@ int ipc_plan_forward_init(ipc_plan* plan, void* stream);
 
 /* Wide path: re-derives the 16-bit operand copies from the fp32 masters x
  * and W.  Needed only after the caller wrote x[1..L] or W outside
- * ipc_plan_step / ipc_plan_forward_init; a no-op for the other paths. */
+ * ipc_plan_step / ipc_plan_forward_init.  Layer-resident plan: marks the
+ * cached 16-bit copies of f(x[L]) stale (needed only after the caller wrote
+ * x[L] without ipc_plan_forward_init).  A no-op for the other paths. */
 int ipc_plan_sync(ipc_plan* plan, void* stream);
 
 /* Enqueues only one phase of the step `reps` times (0 = prediction+error,

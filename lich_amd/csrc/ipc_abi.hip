@@ -679,6 +679,7 @@ int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w
       }
       ra.bar = na.bar;
       resident_bind(ra, static_cast<char*>(workspace) + plan->res_ws_off);
+      na.res_image_flag = ra.flags + RES_MAX_WG;
       TRY(launch_rc(resident_prepare(plan->operand, plan->split, plan->act, ra.lds_bytes),
                     "layer-resident kernel LDS limit"));
     }
@@ -860,6 +861,8 @@ int ipc_plan_forward_init(ipc_plan* plan, void* stream) {
 int ipc_plan_sync(ipc_plan* plan, void* stream) {
   if (!plan) return fail(IPC_ERR_NULL, "plan is NULL");
   if (!plan->bound) return fail(IPC_ERR_STATE, "plan has no bound buffers");
+  if (plan->resident)
+    return launch_rc(resident_invalidate(plan->rargs, (hipStream_t)stream), "layer-resident input images");
   if (!plan->wide) return ok();
   return launch_rc(launch_wide_copy(plan->wsync.data(), (int)plan->wsync.size(), plan->operand, (hipStream_t)stream),
                    "wide operand copies");

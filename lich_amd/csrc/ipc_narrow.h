@@ -33,6 +33,7 @@ struct NarrowArgs {
   float* a[NARROW_MAX_L + 1];  // saved activations (save mode) or nullptr
   float* fx[NARROW_MAX_L + 1]; // f(x[l]) as read by phase B: a[l] in save mode, else workspace
   unsigned* bar;               // workspace: [0] arrivals, [1] exits, [2] barrier timeout flag
+  unsigned* res_image_flag;    // layer-resident plans: cleared by FORWARD (x[L] changed), else nullptr
 };
 
 // Workspace bytes of a plan: 256 bytes of barrier counters, then (recompute
@@ -93,7 +94,7 @@ __host__ __device__ inline void narrow_lds_layout(const int* dims, int L, int KS
 // workgroup each) and exchanges only eps and W^T eps with its neighbours.
 constexpr int RES_MAX_WIDTH = 64;   // d_0 .. d_{L-1}
 constexpr int RES_MAX_B = 128;
-constexpr int RES_MAX_WG = 64;
+constexpr int RES_MAX_WG = 63;      // word 63 of the flag area is the input-image flag
 constexpr int RES_TILE = 256;       // floats per exchanged 16x16 tile (64 lanes x 4)
 
 struct ResidentArgs {
@@ -107,7 +108,9 @@ struct ResidentArgs {
   float* xe[NARROW_MAX_L];      // eps[l], l = 1..L-2:        [2][tiles(d_l)][RES_TILE]
   float* xg[NARROW_MAX_L];      // W[l]^T eps[l], l = 0..L-2: [2][tiles(d_{l+1})][RES_TILE]
   float* xp;                    // top-layer partial products: [2][chunks][tiles(d_{L-1})][RES_TILE]
-  unsigned* flags;              // [nwg] last step each workgroup has published
+  char* image;                  // per top chunk: its f(x[L]) operand LDS image, image_stride bytes apart
+  long long image_stride;
+  unsigned* flags;              // [nwg] last step each workgroup has published; [RES_MAX_WG] image valid
   unsigned* bar;                // [1] exit counter, [2] wait timeout flag (shared with the column kernel)
 };
 
@@ -153,8 +156,11 @@ inline int resident_tiles(int d, int B) { return ((d + 15) / 16) * ((B + 15) / 1
 // exchange buffers need, or -1 when the net is not eligible.
 long long resident_plan(const int* dims, int L, int B, int split, ResidentArgs& a);
 
-// Lays the flags and exchange buffers out in `ws` (resident_plan's bytes).
+// Lays the flags, exchange buffers and input images out in `ws` (resident_plan's bytes).
 void resident_bind(ResidentArgs& a, char* ws);
+
+// Marks the top chunks' cached f(x[L]) images stale (x[L] was rewritten).
+hipError_t resident_invalidate(const ResidentArgs& a, hipStream_t s);
 
 hipError_t resident_prepare(int operand, int split, int act, int lds_bytes);
 hipError_t launch_resident(const ResidentArgs& a, int operand, int split, int act, hipStream_t s);

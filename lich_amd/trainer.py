@@ -314,8 +314,9 @@ class HipIPC:
         return nat.PATH_NAMES[int(nat.lib().ipc_plan_path(self._plan))]
 
     def sync_operand_copies(self) -> None:
-        """Re-derive the wide path's 16-bit operand copies after ``x`` or ``w``
-        were written outside a step (no-op for the other paths)."""
+        """Declare writes of ``x`` or ``w`` made outside a step: re-derives the
+        wide path's 16-bit operand copies, marks the layer-resident path's
+        cached copies of f(x[L]) stale (no-op for the other paths)."""
         if self._plan is not None:
             nat.check(nat.lib().ipc_plan_sync(self._plan, nat.current_stream_handle(self.device)))
 

@@ -220,7 +220,7 @@ def _resident_ws_bytes(dims, B, recompute):
     barrier words and f(x) buffers, then 256 bytes of step flags and the
     double-buffered exchange of 16x16 tiles (1 KiB each): eps[l] for
     l = 1..L-2, W[l]^T eps[l] for l = 0..L-2, and one partial product per
-    128-column chunk of the top layer."""
+    128-column chunk of the top layer; then the chunks' input images."""
     L = len(dims) - 1
     n = 256
     if recompute:
@@ -234,7 +234,14 @@ def _resident_ws_bytes(dims, B, recompute):
         if l >= 1:
             n += 2 * tiles(dims[l]) * 1024
         n += 2 * tiles(dims[l + 1]) * 1024
-    return n + 2 * -(-dims[L] // 128) * tiles(dims[L - 1]) * 1024
+    C = -(-dims[L] // 128)
+    n += 2 * C * tiles(dims[L - 1]) * 1024
+    # then, per top chunk, its cached 16-bit f(x[L]) operands as laid out in
+    # LDS (split 3: hi and lo [B16][K32+8], hi [K16][B32+8]), 256-byte aligned
+    r = lambda v, m: -(-v // m) * m  # noqa: E731
+    K = min(dims[L], 128)
+    image = r((2 * r(B, 16) * (r(K, 32) + 8) + r(K, 16) * (r(B, 32) + 8)) * 2, 256)
+    return r(n, 256) + C * image
 
 
 @pytest.mark.parametrize("dims,B,recompute", [

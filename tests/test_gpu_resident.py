@@ -137,3 +137,32 @@ def test_resident_save_mode_writes_activations():
     for l in range(1, len(dims)):
         ref = O.act_forward("silu", ms[1].x[l].cpu())
         assert torch.allclose(saved[l].cpu(), ref, rtol=1e-6, atol=1e-6), l
+
+
+def test_cached_input_images_follow_new_batches_and_direct_writes():
+    """The top chunks cache their f(x[L]) operands between launches; a new
+    batch (forward initialisation) or a direct write of x[L] followed by
+    sync_operand_copies must refresh them: the resident plan keeps matching
+    the column kernel, which restages x[L] in every launch."""
+    dims, B = (10,) + (64,) * 4 + (784,), 96
+    report("resident-image-cache", dims=dims, B=B)
+    w0 = O.init_weights(dims, seed=10, init="xavier_uniform")
+    batches = [O.make_batch(dims, B, seed=s) for s in (11, 12, 13)]
+    ms = [_model(dims, w0, "tanh", F16, path) for path in ("resident", "narrow")]
+    for m in ms:
+        x1, _l, y1 = batches[0]
+        m.initialize_batch(x1.to(DEV), y1.to(DEV))
+        m.run_steps(4)
+        m.run_steps(4)                          # warm launch: cached images
+        x2, _l, y2 = batches[1]
+        m.initialize_batch(x2.to(DEV), y2.to(DEV))
+        m.run_steps(4)
+        x3, _l, _y = batches[2]
+        m.x[-1].copy_(x3.to(DEV))               # direct write of the input ...
+        m.sync_operand_copies()                 # ... declared to the plan
+        m.run_steps(4)
+    torch.cuda.synchronize()
+    res, col = ms
+    for a, b in zip(res.w + res.x + res.e[:-1], col.w + col.x + col.e[:-1]):
+        assert torch.equal(a, b)
+    assert res.barrier_timeouts() == 0
