@@ -238,18 +238,19 @@ struct Resident {
 
 // Publishes step `value` for this workgroup: every store of the workgroup
 // before it becomes visible at agent scope before the flag does (the barrier
-// orders the other waves' stores before thread 0's fence, the fence before
-// the relaxed flag store).
+// orders the other waves' stores before thread 0's release fence, which
+// writes back L2, and the fence orders them before the relaxed flag store).
 __device__ __forceinline__ void publish(unsigned* flag, unsigned value) {
   __syncthreads();
   if (threadIdx.x == 0) {
-    __threadfence();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     __hip_atomic_store(flag, value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
 // Waits until every peer's flag reaches `value` (one lane of wave 0 per peer,
-// relaxed polls, then one fence that pairs with the publishers' fences).
+// relaxed polls, then one acquire fence, which invalidates L2, pairing with
+// the publishers' release fences).
 __device__ __forceinline__ void wait_peers(const ResidentArgs& p, const int* peers, int npeers, unsigned value) {
   if (threadIdx.x < 64) {
     const int lane = threadIdx.x;
@@ -265,7 +266,7 @@ __device__ __forceinline__ void wait_peers(const ResidentArgs& p, const int* pee
         break;
       }
     }
-    __threadfence();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
   __syncthreads();
 }
