@@ -107,6 +107,34 @@ def time_phases(model, reps=50, replays=5):
     return out
 
 
+def time_step_launch(model, T, reps=50, replays=5):
+    """Average duration of one T-step launch of a whole-step plan, from HIP
+    events on the launch stream around graph replays of `reps` back-to-back
+    launches (the graph launch itself amortised, as rocprof's kernel trace
+    measures it)."""
+    import torch
+
+    from lich_amd import _native as nat
+
+    graph = torch.cuda.CUDAGraph()
+    nat.check(nat.lib().ipc_plan_step(model._plan, T, nat.current_stream_handle()))  # warm
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        for _ in range(reps):
+            nat.check(nat.lib().ipc_plan_step(model._plan, T, nat.current_stream_handle()))
+    graph.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(replays):
+        graph.replay()
+    end.record(stream)
+    end.synchronize()
+    del graph
+    return start.elapsed_time(end) * 1e3 / (reps * replays)
+
+
 def run_steady(model, x, y, T, warmup_steps, steps):
     """Replays a hipGraph of T steps; returns (wall seconds, steps done, GPU
     microseconds per replay from HIP events on the replay stream)."""
@@ -353,9 +381,9 @@ def main() -> int:
     phases = {k: {"us": round(v, 3)} for k, v in phase_us.items()}
     log(f"phases: {phases}")
     if model.fused:
-        # the dominant (only) kernel is a whole-step kernel: one launch per
-        # T-step replay, so its launch duration is the replay's GPU time
-        launch_us = replay_us
+        # the dominant (only) kernel is a whole-step kernel, one launch per
+        # T-step replay; its duration is timed over back-to-back launches
+        launch_us = time_step_launch(pmodel, T)
         name = "layer-resident whole-step kernel" if model.path == "resident" else "whole-step kernel"
         kernel = f"{name}, {T} steps per launch"
         launch_bytes, launch_flops = T * step_bytes, T * step_flops
