@@ -108,9 +108,11 @@ struct ResidentArgs {
   float* xe[NARROW_MAX_L];      // eps[l], l = 1..L-2:        [2][tiles(d_l)][RES_TILE]
   float* xg[NARROW_MAX_L];      // W[l]^T eps[l], l = 0..L-2: [2][tiles(d_{l+1})][RES_TILE]
   float* xp;                    // top-layer partial products: [2][chunks][tiles(d_{L-1})][RES_TILE]
+  float* xs;                    // eps[L-1] summed by top chunk 0: [2][tiles(d_{L-1})][RES_TILE]
   char* image;                  // per top chunk: its f(x[L]) operand LDS image, image_stride bytes apart
   long long image_stride;
-  unsigned* flags;              // [nwg] last step each workgroup has published; [RES_MAX_WG] image valid
+  unsigned* flags;              // [nwg] last step each workgroup has published, [nwg] the last step
+                                // whose eps[L-1] top chunk 0 has published; [RES_MAX_WG] image valid
   unsigned* bar;                // [1] exit counter, [2] wait timeout flag (shared with the column kernel)
 };
 

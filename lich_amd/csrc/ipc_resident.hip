@@ -22,7 +22,9 @@
 //      double-buffered exchange is safe).
 //   3. x[l] += gamma(-eps[l] + f'(x[l]) g[l]) with g[l] from workgroup l-1 and
 //      x[l+1] += gamma(-eps[l+1] + f'(x[l+1]) g) with eps[l+1] from workgroup
-//      l+1 (or x[L-1] minus the top chunks' partials, summed in chunk order).
+//      l+1.  eps[L-1] = x[L-1] minus the top chunks' partials summed in chunk
+//      order: top chunk 0 forms it as soon as its siblings have published and
+//      hands it to workgroup L-2 as one record under a second flag.
 //      Both neighbours evaluate every shared state with the same operands in
 //      the same order, so their copies stay bit-identical without a second
 //      exchange.
@@ -391,27 +393,13 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
         gl[i] = t < npr ? ld_rec(xgl + k.rec(t)) : zero4();
       }
     }
-    if (!from_top) {
-      const float* xeu = p.xe[l + 1] + (long long)buf * ninf * RES_TILE;
+    {
+      // eps[l+1] from workgroup l+1, or eps[L-1] as summed by top chunk 0
+      const float* xeu = (from_top ? p.xs : p.xe[l + 1]) + (long long)buf * ninf * RES_TILE;
 #pragma unroll
       for (int i = 0; i < MAXT; ++i) {
         const int t = wave + NWV * i;
         eu[i] = t < ninf ? ld_rec(xeu + k.rec(t)) : zero4();
-      }
-    } else {
-      // eps[L-1] = x[L-1] - (P_0 + P_1 + ...), the top chunks' partials in chunk order
-      const float* xp = p.xp + (long long)buf * C * ninf * RES_TILE;
-#pragma unroll
-      for (int i = 0; i < MAXT; ++i) {
-        const int t = wave + NWV * i;
-        eu[i] = zero4();
-        if (t < ninf) {
-          const f32x4 sum = sum_partials(xp, (long long)ninf * RES_TILE, C, k.rec(t));
-#pragma unroll
-          for (int q = 0; q < 4; ++q) eu[i][q] = xb[i][q] - sum[q];
-        }
-        // one tile's batch of partials in registers at a time
-        __builtin_amdgcn_sched_barrier(0);
       }
     }
     if (xgl) {
@@ -600,9 +588,38 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
     f32x4 da[MAXT];
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) da[i] = dact4<ACT>(xa[i]);
-    wait_peers(p, peers, npeers, (unsigned)(s + 1));
     // ---- 3. eps[L-1] = x[L-1] - (P_0 + P_1 + ...) in chunk order (this chunk's
-    // own partial read back like the others), x[L-1] with g from workgroup L-2
+    // own partial read back like the others), x[L-1] with g from workgroup L-2.
+    // Chunk 0 sums as soon as its siblings have published (before workgroup
+    // L-2's g arrives) and publishes the result for workgroup L-2.
+    const int nsib = C - 1;
+    wait_peers(p, peers, j == 0 ? nsib : npeers, (unsigned)(s + 1));
+    f32x4 ev4[MAXT];
+#pragma unroll
+    for (int i = 0; i < MAXT; ++i) {
+      const int t = wave + NWV * i;
+      ev4[i] = zero4();
+      if (t < npr) {
+        const f32x4 sum = sum_partials(xp, (long long)npr * RES_TILE, C, k.rec(t));
+        const int b = k.tcol(t);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int r = k.trow(t, q);
+          ev4[i][q] = (r < k.M && b < B) ? xa[i][q] - sum[q] : 0.0f;
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (j == 0) {
+      float* xs = p.xs + (long long)buf * npr * RES_TILE;
+#pragma unroll
+      for (int i = 0; i < MAXT; ++i) {
+        const int t = wave + NWV * i;
+        if (t < npr) st_rec(xs + k.rec(t), ev4[i]);
+      }
+      publish(&p.flags[p.nwg], (unsigned)(s + 1));
+      wait_peers(p, peers + nsib, npeers - nsib, (unsigned)(s + 1));
+    }
     const float* xg = p.xg[L - 2] + (long long)buf * npr * RES_TILE;
     f32x4 g[MAXT];
 #pragma unroll
@@ -614,13 +631,12 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
     for (int i = 0; i < MAXT; ++i) {
       const int t = wave + NWV * i;
       if (t < npr) {
-        const f32x4 sum = sum_partials(xp, (long long)npr * RES_TILE, C, k.rec(t));
         const int b = k.tcol(t);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const int r = k.trow(t, q);
           const bool in = r < k.M && b < B;
-          const float ev = in ? xa[i][q] - sum[q] : 0.0f;
+          const float ev = ev4[i][q];
           if (in) k.lds[k.lay.ea + r * k.lay.lda + b] = cvt<OT>(ev);
           xa[i][q] = state_update(xa[i][q], ev, g[i][q], da[i][q], gamma);
           if (last && writes_rows && in) {
@@ -631,7 +647,6 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
           }
         }
       }
-      __builtin_amdgcn_sched_barrier(0);
     }
     __syncthreads();
     // ---- 4. W[L-1][:, chunk] += alpha eps[L-1] f(x[L])[chunk]^T
@@ -690,13 +705,14 @@ __global__ void __launch_bounds__(NT) resident_kernel(const ResidentArgs args) {
     int n = 0;
     if (k.hidden) {
       if (k.l >= 1) peers[n++] = k.l - 1;
-      if (k.l + 1 <= L - 2) peers[n++] = k.l + 1;
-      else
-        for (int c = 0; c < C; ++c) peers[n++] = top0 + c;
+      // next to the top layer: top chunk 0's eps[L-1] flag (it is published only
+      // after every chunk has published, so it also covers their progress)
+      peers[n++] = k.l + 1 <= L - 2 ? k.l + 1 : p.nwg;
     } else {
-      peers[n++] = L - 2;
+      // siblings first: chunk 0 waits for them alone before it sums the partials
       for (int c = 0; c < C; ++c)
         if (c != k.j) peers[n++] = top0 + c;
+      peers[n++] = L - 2;
     }
     npeers = n;
   }
@@ -709,7 +725,7 @@ __global__ void __launch_bounds__(NT) resident_kernel(const ResidentArgs args) {
   if (threadIdx.x == 0) {
     const unsigned prev = __hip_atomic_fetch_add(&p.bar[1], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     if (prev == (unsigned)p.nwg - 1) {
-      for (int w = 0; w < p.nwg; ++w) __hip_atomic_store(&p.flags[w], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int w = 0; w <= p.nwg; ++w) __hip_atomic_store(&p.flags[w], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       // the top chunks' input images are now written (read by the next launch,
       // after this kernel has completed)
       __hip_atomic_store(&p.flags[RES_MAX_WG], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -772,7 +788,7 @@ long long resident_plan(const int* dims, int L, int B, int split, ResidentArgs& 
   // top layer: one workgroup per NARROW_KCHUNK columns (the column kernel's
   // partial-sum order)
   const int dL = dims[L], kc = NARROW_KCHUNK, C = (dL + kc - 1) / kc;
-  if ((L - 1) + C > RES_MAX_WG) return -1;
+  if ((L - 1) + C + 1 > RES_MAX_WG) return -1;  // flags[nwg] is chunk 0's eps flag
   ResidentLds o;
   resident_lds_layout(dims[L - 1], dL < kc ? dL : kc, B, false, s3, o);
   need = o.bytes > need ? o.bytes : need;
@@ -789,7 +805,7 @@ long long resident_plan(const int* dims, int L, int B, int split, ResidentArgs& 
     if (l >= 1) bytes += 2LL * resident_tiles(dims[l], B) * RES_TILE * 4;
     bytes += 2LL * resident_tiles(dims[l + 1], B) * RES_TILE * 4;
   }
-  bytes += 2LL * C * resident_tiles(dims[L - 1], B) * RES_TILE * 4;
+  bytes += 2LL * (C + 1) * resident_tiles(dims[L - 1], B) * RES_TILE * 4;
   a.image_stride = res_round((o.ea - o.fh) * 2, 256);  // the fh .. ea region of the widest chunk
   bytes = res_round(bytes, 256) + C * a.image_stride;
   return bytes;
@@ -810,6 +826,8 @@ void resident_bind(ResidentArgs& a, char* ws) {
   }
   a.xp = reinterpret_cast<float*>(at);
   at += 2LL * a.chunks * resident_tiles(a.dims[L - 1], B) * RES_TILE * 4;
+  a.xs = reinterpret_cast<float*>(at);
+  at += 2LL * resident_tiles(a.dims[L - 1], B) * RES_TILE * 4;
   a.image = ws + res_round((long long)(at - ws), 256);
 }
 

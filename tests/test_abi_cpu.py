@@ -235,7 +235,7 @@ def _resident_ws_bytes(dims, B, recompute):
             n += 2 * tiles(dims[l]) * 1024
         n += 2 * tiles(dims[l + 1]) * 1024
     C = -(-dims[L] // 128)
-    n += 2 * C * tiles(dims[L - 1]) * 1024
+    n += 2 * (C + 1) * tiles(dims[L - 1]) * 1024   # the partials and chunk 0's summed eps[L-1]
     # then, per top chunk, its cached 16-bit f(x[L]) operands as laid out in
     # LDS (split 3: hi and lo [B16][K32+8], hi [K16][B32+8]), 256-byte aligned
     r = lambda v, m: -(-v // m) * m  # noqa: E731
