@@ -236,6 +236,82 @@ struct Resident {
     for (int ks = 0; ks < ks_b; ++ks) c = mfma16(ld8(a0 + ks * 32), ld8(b0 + ks * 32), c);
     return c;
   }
+
+  // The wave's tiles t = wave and wave + NWV of a [rows][cols] tiling with
+  // `nct` column tiles lie in the same column tile when nct divides NWV.  The
+  // paired forms below then read every B fragment from LDS once for both
+  // tiles and run the two accumulation chains interleaved; each accumulator
+  // still sees exactly the MFMA sequence of the single-tile form.
+  static_assert(MAXT == 2, "the paired tile forms cover two tiles per wave");
+
+  __device__ __forceinline__ void pred_tiles(int n, f32x4 (&c)[MAXT]) const {
+    const int t0 = wave, t1 = wave + NWV;
+    if (t1 < n && NWV % nbt == 0) {
+      const int rt0 = qdiv(t0, inv_nbt), ct = t0 - rt0 * nbt, rt1 = rt0 + NWV / nbt;
+      const int a0 = (rt0 * 16 + lr) * lay.ldw + lg * 8, a1 = (rt1 * 16 + lr) * lay.ldw + lg * 8;
+      const int b0 = (ct * 16 + lr) * lay.ldf + lg * 8;
+      f32x4 c0 = zero4(), c1 = zero4();
+      for (int ks = 0; ks < ks_k; ++ks) {
+        const V8 bh = ld8(lay.fh + b0 + ks * 32);
+        const V8 ah0 = ld8(lay.wh + a0 + ks * 32), ah1 = ld8(lay.wh + a1 + ks * 32);
+        c0 = mfma16(ah0, bh, c0);
+        c1 = mfma16(ah1, bh, c1);
+        if (S3) {
+          const V8 bl = ld8(lay.fl + b0 + ks * 32);
+          const V8 al0 = ld8(lay.wl + a0 + ks * 32), al1 = ld8(lay.wl + a1 + ks * 32);
+          c0 = mfma16(al0, bh, c0);
+          c1 = mfma16(al1, bh, c1);
+          c0 = mfma16(ah0, bl, c0);
+          c1 = mfma16(ah1, bl, c1);
+        }
+      }
+      c[0] = c0;
+      c[1] = c1;
+    } else {
+      c[0] = t0 < n ? pred_tile(t0) : zero4();
+      c[1] = t1 < n ? pred_tile(t1) : zero4();
+    }
+  }
+
+  __device__ __forceinline__ void infer_tiles(int n, f32x4 (&c)[MAXT]) const {
+    const int t0 = wave, t1 = wave + NWV;
+    if (t1 < n && NWV % nbt == 0) {
+      const int rt0 = qdiv(t0, inv_nbt), ct = t0 - rt0 * nbt, rt1 = rt0 + NWV / nbt;
+      const int a0 = lay.wt + (rt0 * 16 + lr) * lay.ldwt + lg * 8, a1 = lay.wt + (rt1 * 16 + lr) * lay.ldwt + lg * 8;
+      const int b0 = lay.eb + (ct * 16 + lr) * lay.lde + lg * 8;
+      f32x4 c0 = zero4(), c1 = zero4();
+      for (int ks = 0; ks < ks_m; ++ks) {
+        const V8 b = ld8(b0 + ks * 32);
+        c0 = mfma16(ld8(a0 + ks * 32), b, c0);
+        c1 = mfma16(ld8(a1 + ks * 32), b, c1);
+      }
+      c[0] = c0;
+      c[1] = c1;
+    } else {
+      c[0] = t0 < n ? infer_tile(t0) : zero4();
+      c[1] = t1 < n ? infer_tile(t1) : zero4();
+    }
+  }
+
+  __device__ __forceinline__ void update_tiles(int n, f32x4 (&c)[MAXT]) const {
+    const int t0 = wave, t1 = wave + NWV;
+    if (t1 < n && NWV % ktl == 0) {
+      const int rt0 = urt(t0), ct = t0 - rt0 * ktl, rt1 = rt0 + NWV / ktl;
+      const int a0 = lay.ea + (rt0 * 16 + lr) * lay.lda + lg * 8, a1 = lay.ea + (rt1 * 16 + lr) * lay.lda + lg * 8;
+      const int b0 = lay.ft + (ct * 16 + lr) * lay.ldft + lg * 8;
+      f32x4 c0 = zero4(), c1 = zero4();
+      for (int ks = 0; ks < ks_b; ++ks) {
+        const V8 b = ld8(b0 + ks * 32);
+        c0 = mfma16(ld8(a0 + ks * 32), b, c0);
+        c1 = mfma16(ld8(a1 + ks * 32), b, c1);
+      }
+      c[0] = c0;
+      c[1] = c1;
+    } else {
+      c[0] = t0 < n ? update_tile(t0) : zero4();
+      c[1] = t1 < n ? update_tile(t1) : zero4();
+    }
+  }
 };
 
 // Publishes step `value` for this workgroup: every store of the workgroup
@@ -273,11 +349,43 @@ __device__ __forceinline__ void wait_peers(const ResidentArgs& p, const int* pee
   __syncthreads();
 }
 
+// Launch set-up, run while the workgroup's first state and weight loads are
+// in flight: the peer list, and zeros in the operand regions when the block
+// does not fill them (a dimension off the 32-element MFMA k-step or the
+// 16-row tile leaves padding that the MFMAs read); ends with a barrier, so
+// the staging writes that follow land after the zeros.
+template <typename OT, int SPLIT, int ACT>
+__device__ __forceinline__ void setup(const Resident<OT, SPLIT, ACT>& k, const ResidentArgs& p, int* peers,
+                                      int& npeers) {
+  if ((k.M | k.K | k.B) & 31) {
+    uint4* z = reinterpret_cast<uint4*>(k.lds);
+    for (int i = threadIdx.x; i < k.lay.bytes / 16; i += NT) z[i] = uint4{0u, 0u, 0u, 0u};
+  }
+  if (threadIdx.x == 0) {
+    // the workgroups this one exchanges with, in both directions
+    const int L = k.L, C = p.chunks, top0 = L - 1;
+    int n = 0;
+    if (k.hidden) {
+      if (k.l >= 1) peers[n++] = k.l - 1;
+      // next to the top layer: top chunk 0's eps[L-1] flag (it is published only
+      // after every chunk has published, so it also covers their progress)
+      peers[n++] = k.l + 1 <= L - 2 ? k.l + 1 : p.nwg;
+    } else {
+      // siblings first: chunk 0 waits for them alone before it sums the partials
+      for (int c = 0; c < C; ++c)
+        if (c != k.j) peers[n++] = top0 + c;
+      peers[n++] = L - 2;
+    }
+    npeers = n;
+  }
+  __syncthreads();
+}
+
 // Hidden layer l (0 <= l <= L-2): W[l] at the update tiles, x[l] at the
 // prediction tiles, x[l+1] at the inference tiles, all resident for the launch.
 template <typename OT, int SPLIT, int ACT>
-__device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const ResidentArgs& p, const int* peers,
-                                           int npeers) {
+__device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const ResidentArgs& p, int* peers,
+                                           int& npeers_lds) {
   constexpr int MU = 1;  // update tiles per wave: d_l x d_{l+1} <= 64 x 64 is at most 16 tiles
   const int L = k.L, B = k.B, C = p.chunks, l = k.l, wave = k.wave, lg = k.lg, lr = k.lr;
   const int npr = k.n_pred, ninf = k.n_inf;
@@ -314,6 +422,8 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
       }
     }
   }
+  setup(k, p, peers, npeers_lds);
+  const int npeers = npeers_lds;
 #pragma unroll
   for (int i = 0; i < MAXT; ++i) {
     const int t = wave + NWV * i;
@@ -342,11 +452,13 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
     const int buf = s & 1;
     // ---- 1. eps[l] = x[l] - W f(x[l+1]); g = W^T eps[l]
     float* xe = l >= 1 ? p.xe[l] + (long long)buf * npr * RES_TILE : nullptr;
+    f32x4 cp[MAXT];
+    k.pred_tiles(npr, cp);
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) {
       const int t = wave + NWV * i;
       if (t < npr) {
-        const f32x4 c = k.pred_tile(t);
+        const f32x4 c = cp[i];
         const int b = k.tcol(t);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -365,13 +477,11 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
     }
     __syncthreads();
     float* xg = p.xg[l] + (long long)buf * ninf * RES_TILE;
+    k.infer_tiles(ninf, gb);
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) {
       const int t = wave + NWV * i;
-      if (t < ninf) {
-        gb[i] = k.infer_tile(t);
-        st_rec(xg + k.rec(t), gb[i]);
-      }
+      if (t < ninf) st_rec(xg + k.rec(t), gb[i]);
     }
     // ---- 2. exchange; f'(x[l]) and f'(x[l+1]) of the old states meanwhile
     publish(&p.flags[k.wg], (unsigned)(s + 1));
@@ -483,8 +593,8 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
 // Top-layer chunk j: columns [k0, k0 + K) of W[L-1] at the update tiles,
 // x[L-1] at the prediction tiles, f(x[L]) of the chunk in LDS.
 template <typename OT, int SPLIT, int ACT>
-__device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const ResidentArgs& p, const int* peers,
-                                        int npeers) {
+__device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const ResidentArgs& p, int* peers,
+                                        int& npeers_lds) {
   const int L = k.L, B = k.B, C = p.chunks, l = k.l, j = k.j, wave = k.wave, lg = k.lg, lr = k.lr;
   const int npr = k.n_pred;
   const float gamma = p.gamma, alpha = p.alpha;
@@ -510,6 +620,8 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
       }
     }
   }
+  setup(k, p, peers, npeers_lds);
+  const int npeers = npeers_lds;
   // f(x[L]) of the chunk: x[L] is clamped, so its 16-bit operand copies (the
   // LDS region fh .. ea) are cached in the workspace by the first launch after
   // the forward initialisation (which marks the cache stale) and copied back
@@ -578,10 +690,14 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
     const bool last = s + 1 == p.steps;
     // ---- 1. partial product of the chunk
     float* xp = p.xp + (long long)buf * C * npr * RES_TILE;
+    {
+      f32x4 cp[MAXT];
+      k.pred_tiles(npr, cp);
 #pragma unroll
-    for (int i = 0; i < MAXT; ++i) {
-      const int t = wave + NWV * i;
-      if (t < npr) st_rec(xp + (long long)j * npr * RES_TILE + k.rec(t), k.pred_tile(t));
+      for (int i = 0; i < MAXT; ++i) {
+        const int t = wave + NWV * i;
+        if (t < npr) st_rec(xp + (long long)j * npr * RES_TILE + k.rec(t), cp[i]);
+      }
     }
     // ---- 2. exchange; f'(x[L-1]) of the old state meanwhile
     publish(&p.flags[k.wg], (unsigned)(s + 1));
@@ -594,6 +710,17 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
     // L-2's g arrives) and publishes the result for workgroup L-2.
     const int nsib = C - 1;
     wait_peers(p, peers, j == 0 ? nsib : npeers, (unsigned)(s + 1));
+    // the other chunks have waited for workgroup L-2 as well: its g records
+    // are loaded together with the partials
+    const float* xg = p.xg[L - 2] + (long long)buf * npr * RES_TILE;
+    f32x4 g[MAXT];
+    if (j != 0) {
+#pragma unroll
+      for (int i = 0; i < MAXT; ++i) {
+        const int t = wave + NWV * i;
+        g[i] = t < npr ? ld_rec(xg + k.rec(t)) : zero4();
+      }
+    }
     f32x4 ev4[MAXT];
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) {
@@ -618,14 +745,27 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
         if (t < npr) st_rec(xs + k.rec(t), ev4[i]);
       }
       publish(&p.flags[p.nwg], (unsigned)(s + 1));
-      wait_peers(p, peers + nsib, npeers - nsib, (unsigned)(s + 1));
     }
-    const float* xg = p.xg[L - 2] + (long long)buf * npr * RES_TILE;
-    f32x4 g[MAXT];
+    // eps[L-1] into the weight-update A operand
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) {
       const int t = wave + NWV * i;
-      g[i] = t < npr ? ld_rec(xg + k.rec(t)) : zero4();
+      if (t < npr) {
+        const int b = k.tcol(t);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int r = k.trow(t, q);
+          if (r < k.M && b < B) k.lds[k.lay.ea + r * k.lay.lda + b] = cvt<OT>(ev4[i][q]);
+        }
+      }
+    }
+    if (j == 0) {
+      wait_peers(p, peers + nsib, npeers - nsib, (unsigned)(s + 1));
+#pragma unroll
+      for (int i = 0; i < MAXT; ++i) {
+        const int t = wave + NWV * i;
+        g[i] = t < npr ? ld_rec(xg + k.rec(t)) : zero4();
+      }
     }
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) {
@@ -637,7 +777,6 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
           const int r = k.trow(t, q);
           const bool in = r < k.M && b < B;
           const float ev = ev4[i][q];
-          if (in) k.lds[k.lay.ea + r * k.lay.lda + b] = cvt<OT>(ev);
           xa[i][q] = state_update(xa[i][q], ev, g[i][q], da[i][q], gamma);
           if (last && writes_rows && in) {
             const long long o = (long long)r * B + b;
@@ -650,11 +789,13 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
     }
     __syncthreads();
     // ---- 4. W[L-1][:, chunk] += alpha eps[L-1] f(x[L])[chunk]^T
+    f32x4 cu[MAXT];
+    k.update_tiles(k.n_upd, cu);
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) {
       const int t = wave + NWV * i;
       if (t < k.n_upd) {
-        const f32x4 c = k.update_tile(t);
+        const f32x4 c = cu[i];
         const int col = k.uct(t) * 16 + lr;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -695,28 +836,8 @@ __global__ void __launch_bounds__(NT) resident_kernel(const ResidentArgs args) {
   static_assert(sizeof(ResidentArgs) % 4 == 0, "argument block copy");
   for (int i = threadIdx.x; i < (int)(sizeof(ResidentArgs) / 4); i += NT)
     reinterpret_cast<int*>(&p)[i] = reinterpret_cast<const int*>(&args)[i];
-  for (int i = threadIdx.x; i < args.lds_bytes / 16; i += NT)
-    reinterpret_cast<uint4*>(lds_raw)[i] = uint4{0u, 0u, 0u, 0u};
   __syncthreads();
   R k(p, lds_raw);
-  if (threadIdx.x == 0) {
-    // the workgroups this one exchanges with, in both directions
-    const int L = k.L, C = p.chunks, top0 = L - 1;
-    int n = 0;
-    if (k.hidden) {
-      if (k.l >= 1) peers[n++] = k.l - 1;
-      // next to the top layer: top chunk 0's eps[L-1] flag (it is published only
-      // after every chunk has published, so it also covers their progress)
-      peers[n++] = k.l + 1 <= L - 2 ? k.l + 1 : p.nwg;
-    } else {
-      // siblings first: chunk 0 waits for them alone before it sums the partials
-      for (int c = 0; c < C; ++c)
-        if (c != k.j) peers[n++] = top0 + c;
-      peers[n++] = L - 2;
-    }
-    npeers = n;
-  }
-  __syncthreads();
   if (k.hidden) run_hidden(k, p, peers, npeers);
   else run_top(k, p, peers, npeers);
 
