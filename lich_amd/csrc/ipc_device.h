@@ -137,6 +137,15 @@ template <int ACT> __device__ __forceinline__ float dact_t(float x) {
   return 1.0f;
 }
 
+// f'(x) given y = act_t<ACT>(x) already evaluated: the same bits as
+// dact_t<ACT>(x) (tanh and sigmoid reuse y, the others evaluate f'(x) anew).
+template <int ACT> __device__ __forceinline__ float dact_from_t(float x, float y) {
+#pragma clang fp contract(off)
+  if (ACT == ACT_TANH) return 1.0f - y * y;
+  if (ACT == ACT_SIGMOID) return y * (1.0f - y);
+  return dact_t<ACT>(x);
+}
+
 // ---------------------------------------------------------------- MFMA
 // 32x32 output block per wave.  Operand lane layout (both operands): lane l
 // supplies row/column (l % 32) and the k-slice (l / 32) of the instruction's

@@ -23,11 +23,12 @@
 //   3. x[l] += gamma(-eps[l] + f'(x[l]) g[l]) with g[l] from workgroup l-1 and
 //      x[l+1] += gamma(-eps[l+1] + f'(x[l+1]) g) with eps[l+1] from workgroup
 //      l+1.  eps[L-1] = x[L-1] minus the top chunks' partials summed in chunk
-//      order: top chunk 0 forms it as soon as its siblings have published and
-//      hands it to workgroup L-2 as one record under a second flag.
-//      Both neighbours evaluate every shared state with the same operands in
-//      the same order, so their copies stay bit-identical without a second
-//      exchange.
+//      order; top chunk 0 hands it to workgroup L-2 as one record under a
+//      second flag.  The chunks apply x[L-1]'s update one step late (with
+//      workgroup L-2's g of the previous step), so they never wait for
+//      workgroup L-2's current step.  Both neighbours evaluate every shared
+//      state with the same operands in the same order, so their copies stay
+//      bit-identical without a second exchange.
 //   4. W[l] += alpha eps[l] f(x_new[l+1])^T over the batch with MFMA, operand
 //      copies restaged in LDS.
 // One flag exchange per step replaces the two grid barriers; W, the states
@@ -51,6 +52,9 @@ constexpr int MAXT = 2;  // output tiles per wave and phase (32 tiles at most)
 template <typename OT> struct Vec8;
 template <> struct Vec8<f16> { typedef f16x8 T; };
 template <> struct Vec8<bf16> { typedef bf16x8 T; };
+template <typename OT> struct Vec4;
+template <> struct Vec4<f16> { typedef _Float16 T __attribute__((ext_vector_type(4))); };
+template <> struct Vec4<bf16> { typedef __bf16 T __attribute__((ext_vector_type(4))); };
 
 __device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
@@ -113,9 +117,19 @@ __device__ __forceinline__ f32x4 dact4(f32x4 x) {
   return d;
 }
 
+// dact4 given f(x) as well (the value staged for the MFMAs)
+template <int ACT>
+__device__ __forceinline__ f32x4 dact4_from(f32x4 x, f32x4 f) {
+  f32x4 d;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) d[q] = dact_from_t<ACT>(x[q], f[q]);
+  return d;
+}
+
 template <typename OT, int SPLIT, int ACT>
 struct Resident {
   typedef typename Vec8<OT>::T V8;
+  typedef typename Vec4<OT>::T V4;
   static constexpr bool S3 = SPLIT >= 3;
 
   const ResidentArgs& p;
@@ -170,14 +184,93 @@ struct Resident {
   __device__ __forceinline__ V8 ld8(int off) const { return *reinterpret_cast<const V8*>(lds + off); }
 
   // f(v) as 16-bit hi (and lo) terms into the prediction B operand [b][k] and
-  // hi into the weight-update B operand [k][b]; (k, b) outside K x B is left zero.
-  __device__ __forceinline__ void stage_f(int k, int b, float v) {
+  // hi into the weight-update B operand [k][b]; (k, b) outside K x B is left
+  // zero.  Returns f(v).
+  __device__ __forceinline__ float stage_f(int k, int b, float v) {
+    const float f = act_t<ACT>(v);
     if (k < K && b < B) {
-      const float f = act_t<ACT>(v);
       const OT hi = cvt<OT>(f);
       lds[lay.fh + b * lay.ldf + k] = hi;
       if (S3) lds[lay.fl + b * lay.ldf + k] = cvt<OT>(f - to_f32(hi));
       lds[lay.ft + k * lay.ldft + b] = hi;
+    }
+    return f;
+  }
+
+  // The same for the four rows r0 .. r0 + 3 (r0 a multiple of 4) of column b
+  // that one lane holds of a result tile: they are contiguous in the [b][k]
+  // block, written with one 8-byte store each when all four exist.
+  __device__ __forceinline__ f32x4 stage_f4(int r0, int b, f32x4 v) {
+    f32x4 f;
+    OT hi[4], lo[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      f[q] = act_t<ACT>(v[q]);
+      hi[q] = cvt<OT>(f[q]);
+      if (S3) lo[q] = cvt<OT>(f[q] - to_f32(hi[q]));
+    }
+    if (b < B) {
+      if (r0 + 4 <= K) {
+        *reinterpret_cast<V4*>(lds + lay.fh + b * lay.ldf + r0) = V4{hi[0], hi[1], hi[2], hi[3]};
+        if (S3) *reinterpret_cast<V4*>(lds + lay.fl + b * lay.ldf + r0) = V4{lo[0], lo[1], lo[2], lo[3]};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) lds[lay.ft + (r0 + q) * lay.ldft + b] = hi[q];
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (r0 + q < K) {
+            lds[lay.fh + b * lay.ldf + r0 + q] = hi[q];
+            if (S3) lds[lay.fl + b * lay.ldf + r0 + q] = lo[q];
+            lds[lay.ft + (r0 + q) * lay.ldft + b] = hi[q];
+          }
+      }
+    }
+    return f;
+  }
+
+  // eps rows r0 .. r0 + 3 of column b (zero outside M x B) into the inference
+  // B operand [b][m] (contiguous) and the weight-update A operand [m][b].
+  __device__ __forceinline__ void stage_e4(int r0, int b, f32x4 e) {
+    if (b >= B) return;
+    OT eo[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) eo[q] = cvt<OT>(e[q]);
+    if (r0 + 4 <= M) {
+      *reinterpret_cast<V4*>(lds + lay.eb + b * lay.lde + r0) = V4{eo[0], eo[1], eo[2], eo[3]};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) lds[lay.ea + (r0 + q) * lay.lda + b] = eo[q];
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (r0 + q < M) {
+          lds[lay.eb + b * lay.lde + r0 + q] = eo[q];
+          lds[lay.ea + (r0 + q) * lay.lda + b] = eo[q];
+        }
+    }
+  }
+
+  // W rows m0 .. m0 + 3 of column k (the four values of one update-tile lane)
+  // into the operand copies; the transposed copy [k][m] takes them with one
+  // 8-byte store when all four rows exist.
+  __device__ __forceinline__ void stage_w4(int m0, int k, f32x4 w) {
+    if (k >= K) return;
+    OT hi[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      hi[q] = cvt<OT>(w[q]);
+      if (m0 + q < M) {
+        lds[lay.wh + (m0 + q) * lay.ldw + k] = hi[q];
+        if (S3) lds[lay.wl + (m0 + q) * lay.ldw + k] = cvt<OT>(w[q] - to_f32(hi[q]));
+      }
+    }
+    if (hidden) {
+      if (m0 + 4 <= M) {
+        *reinterpret_cast<V4*>(lds + lay.wt + k * lay.ldwt + m0) = V4{hi[0], hi[1], hi[2], hi[3]};
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (m0 + q < M) lds[lay.wt + k * lay.ldwt + m0 + q] = hi[q];
+      }
     }
   }
 
@@ -326,17 +419,20 @@ __device__ __forceinline__ void publish(unsigned* flag, unsigned value) {
   }
 }
 
-// Waits until every peer's flag reaches `value` (one lane of wave 0 per peer,
-// relaxed polls, then one acquire fence, which invalidates L2, pairing with
-// the publishers' release fences).
-__device__ __forceinline__ void wait_peers(const ResidentArgs& p, const int* peers, int npeers, unsigned value) {
+// Waits until every peer's flag reaches `value`, the last `n_prev` peers'
+// flags `value - 1` (one lane of wave 0 per peer, relaxed polls, then one
+// acquire fence, which invalidates L2, pairing with the publishers' release
+// fences).
+__device__ __forceinline__ void wait_peers(const ResidentArgs& p, const int* peers, int npeers, unsigned value,
+                                           int n_prev = 0) {
   if (threadIdx.x < 64) {
     const int lane = threadIdx.x;
     const unsigned* f = lane < npeers ? &p.flags[peers[lane]] : nullptr;
+    const unsigned want = lane < npeers - n_prev ? value : value - 1u;
     int spins = 0;
     while (true) {
       bool ok = true;
-      if (f) ok = __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= value;
+      if (f) ok = __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= want;
       if (__all(ok)) break;
       __builtin_amdgcn_s_sleep(1);
       if (++spins > p.spin_limit) {
@@ -371,7 +467,7 @@ __device__ __forceinline__ void setup(const Resident<OT, SPLIT, ACT>& k, const R
       // after every chunk has published, so it also covers their progress)
       peers[n++] = k.l + 1 <= L - 2 ? k.l + 1 : p.nwg;
     } else {
-      // siblings first: chunk 0 waits for them alone before it sums the partials
+      // the siblings, then workgroup L-2 (waited for one step behind)
       for (int c = 0; c < C; ++c)
         if (c != k.j) peers[n++] = top0 + c;
       peers[n++] = L - 2;
@@ -390,11 +486,12 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
   const int L = k.L, B = k.B, C = p.chunks, l = k.l, wave = k.wave, lg = k.lg, lr = k.lr;
   const int npr = k.n_pred, ninf = k.n_inf;
   const float gamma = p.gamma, alpha = p.alpha;
-  f32x4 xa[MAXT], ea[MAXT], xb[MAXT], gb[MAXT], wr[MU];
+  // fb: f(x[l+1]) as staged for the MFMAs, reused for the next step's f'(x[l+1])
+  f32x4 xa[MAXT], ea[MAXT], xb[MAXT], gb[MAXT], fb[MAXT], wr[MU];
 #pragma unroll
   for (int i = 0; i < MAXT; ++i) {
     const int t = wave + NWV * i;
-    xa[i] = zero4(); xb[i] = zero4(); ea[i] = zero4(); gb[i] = zero4();
+    xa[i] = zero4(); xb[i] = zero4(); ea[i] = zero4(); gb[i] = zero4(); fb[i] = zero4();
     const int b = k.tcol(t);
     if (t < npr)
 #pragma unroll
@@ -427,21 +524,12 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
 #pragma unroll
   for (int i = 0; i < MAXT; ++i) {
     const int t = wave + NWV * i;
-    if (t < ninf)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) k.stage_f(k.trow(t, q), k.tcol(t), xb[i][q]);
+    if (t < ninf) fb[i] = k.stage_f4(k.trow(t, 0), k.tcol(t), xb[i]);
   }
 #pragma unroll
   for (int i = 0; i < MU; ++i) {
     const int t = wave + NWV * i;
-    if (t < k.n_upd) {
-      const int c = k.uct(t) * 16 + lr;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int r = k.urt(t) * 16 + 4 * lg + q;
-        if (r < k.M && c < k.K) k.stage_w(r, c, wr[i][q]);
-      }
-    }
+    if (t < k.n_upd) k.stage_w4(k.urt(t) * 16 + 4 * lg, k.uct(t) * 16 + lr, wr[i]);
   }
   __syncthreads();
 
@@ -463,20 +551,15 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const int r = k.trow(t, q);
-          const bool in = r < k.M && b < B;
-          const float ev = in ? xa[i][q] - c[q] : 0.0f;
-          ea[i][q] = ev;
-          if (in) {
-            const OT eo = cvt<OT>(ev);
-            k.lds[k.lay.eb + b * k.lay.lde + r] = eo;
-            k.lds[k.lay.ea + r * k.lay.lda + b] = eo;
-          }
+          ea[i][q] = r < k.M && b < B ? xa[i][q] - c[q] : 0.0f;
         }
+        k.stage_e4(k.trow(t, 0), b, ea[i]);
         if (xe) st_rec(xe + k.rec(t), ea[i]);
       }
     }
     __syncthreads();
-    float* xg = p.xg[l] + (long long)buf * ninf * RES_TILE;
+    // next to the top layer the chunks read g one step later: three buffers
+    float* xg = p.xg[l] + (long long)(from_top ? s % 3 : buf) * ninf * RES_TILE;
     k.infer_tiles(ninf, gb);
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) {
@@ -489,7 +572,7 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) {
       da[i] = l >= 1 ? dact4<ACT>(xa[i]) : zero4();
-      db[i] = dact4<ACT>(xb[i]);
+      db[i] = dact4_from<ACT>(xb[i], fb[i]);
     }
     wait_peers(p, peers, npeers, (unsigned)(s + 1));
     // ---- 3. x[l] with g[l] from workgroup l-1; x[l+1] with eps[l+1] from above
@@ -525,12 +608,9 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
     for (int i = 0; i < MAXT; ++i) {
       const int t = wave + NWV * i;
       if (t < ninf) {
-        const int b = k.tcol(t);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          xb[i][q] = state_update(xb[i][q], eu[i][q], gb[i][q], db[i][q], gamma);
-          k.stage_f(k.trow(t, q), b, xb[i][q]);
-        }
+        for (int q = 0; q < 4; ++q) xb[i][q] = state_update(xb[i][q], eu[i][q], gb[i][q], db[i][q], gamma);
+        fb[i] = k.stage_f4(k.trow(t, 0), k.tcol(t), xb[i]);
       }
     }
     __syncthreads();
@@ -540,16 +620,15 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
       const int t = wave + NWV * i;
       if (t < k.n_upd) {
         const f32x4 c = k.update_tile(t);
-        const int col = k.uct(t) * 16 + lr;
+        const int col = k.uct(t) * 16 + lr, r0 = k.urt(t) * 16 + 4 * lg;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const int r = k.urt(t) * 16 + 4 * lg + q;
-          if (r < k.M && col < k.K) {
+          if (r0 + q < k.M && col < k.K) {
 #pragma clang fp contract(off)
             wr[i][q] = wr[i][q] + alpha * c[q];
-            k.stage_w(r, col, wr[i][q]);
           }
         }
+        k.stage_w4(r0, col, wr[i]);
       }
     }
     __syncthreads();
@@ -585,6 +664,28 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
       for (int q = 0; q < 4; ++q) {
         const int r = k.urt(t) * 16 + 4 * lg + q;
         if (r < k.M && c < k.K) p.w[l][(long long)r * k.ldw_g + c] = wr[i][q];
+      }
+    }
+  }
+  if (from_top) {
+    // x[L-1] after the last step: the top chunks apply each step's update one
+    // step late, so the final one is written here, from this workgroup's copy
+    float* XU = p.x[l + 1];
+    float* FXU = p.fx[l + 1];
+#pragma unroll
+    for (int i = 0; i < MAXT; ++i) {
+      const int t = wave + NWV * i;
+      if (t < ninf) {
+        const int b = k.tcol(t);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int r = k.trow(t, q);
+          if (r < k.K && b < B) {
+            const long long o = (long long)r * B + b;
+            XU[o] = xb[i][q];
+            if (FXU) FXU[o] = act_t<ACT>(xb[i][q]);
+          }
+        }
       }
     }
   }
@@ -682,7 +783,13 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
   }
   __syncthreads();
 
-  const bool writes_rows = j == 0;  // chunk 0 writes e, x and f(x) of layer L-1
+  // The chunks apply each step's x[L-1] update one step late, just before the
+  // next step's eps[L-1]: their own chain (partial product, partial sums,
+  // weight update) then waits for workgroup L-2's previous step only, and
+  // workgroup L-2 writes x[L-1] after the last step.
+  f32x4 ev_prev[MAXT];
+#pragma unroll
+  for (int i = 0; i < MAXT; ++i) ev_prev[i] = zero4();
   for (int s = 0; s < p.steps; ++s) {
     k.refresh();
     const int lg = k.lg, lr = k.lr;
@@ -699,28 +806,28 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
         if (t < npr) st_rec(xp + (long long)j * npr * RES_TILE + k.rec(t), cp[i]);
       }
     }
-    // ---- 2. exchange; f'(x[L-1]) of the old state meanwhile
+    // ---- 2. exchange: the siblings' partials of this step, workgroup L-2's g
+    // of the previous one; f'(x[L-1]) of the state the late update starts from
+    // meanwhile
     publish(&p.flags[k.wg], (unsigned)(s + 1));
     f32x4 da[MAXT];
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) da[i] = dact4<ACT>(xa[i]);
-    // ---- 3. eps[L-1] = x[L-1] - (P_0 + P_1 + ...) in chunk order (this chunk's
-    // own partial read back like the others), x[L-1] with g from workgroup L-2.
-    // Chunk 0 sums as soon as its siblings have published (before workgroup
-    // L-2's g arrives) and publishes the result for workgroup L-2.
-    const int nsib = C - 1;
-    wait_peers(p, peers, j == 0 ? nsib : npeers, (unsigned)(s + 1));
-    // the other chunks have waited for workgroup L-2 as well: its g records
-    // are loaded together with the partials
-    const float* xg = p.xg[L - 2] + (long long)buf * npr * RES_TILE;
+    wait_peers(p, peers, npeers, (unsigned)(s + 1), 1);
     f32x4 g[MAXT];
-    if (j != 0) {
+#pragma unroll
+    for (int i = 0; i < MAXT; ++i) g[i] = zero4();
+    if (s >= 1) {
+      const float* xg = p.xg[L - 2] + (long long)((s - 1) % 3) * npr * RES_TILE;
 #pragma unroll
       for (int i = 0; i < MAXT; ++i) {
         const int t = wave + NWV * i;
-        g[i] = t < npr ? ld_rec(xg + k.rec(t)) : zero4();
+        if (t < npr) g[i] = ld_rec(xg + k.rec(t));
       }
     }
+    // ---- 3. x[L-1] of this step (the previous step's update), then eps[L-1] =
+    // x[L-1] - (P_0 + P_1 + ...) in chunk order (this chunk's own partial read
+    // back like the others); chunk 0 publishes it for workgroup L-2
     f32x4 ev4[MAXT];
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) {
@@ -732,6 +839,7 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const int r = k.trow(t, q);
+          if (s >= 1) xa[i][q] = state_update(xa[i][q], ev_prev[i][q], g[i][q], da[i][q], gamma);
           ev4[i][q] = (r < k.M && b < B) ? xa[i][q] - sum[q] : 0.0f;
         }
       }
@@ -746,43 +854,19 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
       }
       publish(&p.flags[p.nwg], (unsigned)(s + 1));
     }
-    // eps[L-1] into the weight-update A operand
+    // eps[L-1] into the weight-update A operand (and e[L-1] after the last step)
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) {
       const int t = wave + NWV * i;
+      ev_prev[i] = ev4[i];
       if (t < npr) {
         const int b = k.tcol(t);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const int r = k.trow(t, q);
-          if (r < k.M && b < B) k.lds[k.lay.ea + r * k.lay.lda + b] = cvt<OT>(ev4[i][q]);
-        }
-      }
-    }
-    if (j == 0) {
-      wait_peers(p, peers + nsib, npeers - nsib, (unsigned)(s + 1));
-#pragma unroll
-      for (int i = 0; i < MAXT; ++i) {
-        const int t = wave + NWV * i;
-        g[i] = t < npr ? ld_rec(xg + k.rec(t)) : zero4();
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < MAXT; ++i) {
-      const int t = wave + NWV * i;
-      if (t < npr) {
-        const int b = k.tcol(t);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int r = k.trow(t, q);
-          const bool in = r < k.M && b < B;
-          const float ev = ev4[i][q];
-          xa[i][q] = state_update(xa[i][q], ev, g[i][q], da[i][q], gamma);
-          if (last && writes_rows && in) {
-            const long long o = (long long)r * B + b;
-            p.e[l][o] = ev;
-            p.x[l][o] = xa[i][q];
-            if (p.fx[l]) p.fx[l][o] = act_t<ACT>(xa[i][q]);
+          if (r < k.M && b < B) {
+            k.lds[k.lay.ea + r * k.lay.lda + b] = cvt<OT>(ev4[i][q]);
+            if (last && j == 0) p.e[l][(long long)r * B + b] = ev4[i][q];
           }
         }
       }
@@ -924,7 +1008,7 @@ long long resident_plan(const int* dims, int L, int B, int split, ResidentArgs& 
   long long bytes = 256;  // flags
   for (int l = 0; l + 1 < L; ++l) {
     if (l >= 1) bytes += 2LL * resident_tiles(dims[l], B) * RES_TILE * 4;
-    bytes += 2LL * resident_tiles(dims[l + 1], B) * RES_TILE * 4;
+    bytes += (l + 2 == L ? 3LL : 2LL) * resident_tiles(dims[l + 1], B) * RES_TILE * 4;
   }
   bytes += 2LL * (C + 1) * resident_tiles(dims[L - 1], B) * RES_TILE * 4;
   a.image_stride = res_round((o.ea - o.fh) * 2, 256);  // the fh .. ea region of the widest chunk
@@ -943,7 +1027,7 @@ void resident_bind(ResidentArgs& a, char* ws) {
       at += 2LL * resident_tiles(a.dims[l], B) * RES_TILE * 4;
     }
     a.xg[l] = reinterpret_cast<float*>(at);
-    at += 2LL * resident_tiles(a.dims[l + 1], B) * RES_TILE * 4;
+    at += (l + 2 == L ? 3LL : 2LL) * resident_tiles(a.dims[l + 1], B) * RES_TILE * 4;
   }
   a.xp = reinterpret_cast<float*>(at);
   at += 2LL * a.chunks * resident_tiles(a.dims[L - 1], B) * RES_TILE * 4;

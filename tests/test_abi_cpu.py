@@ -219,7 +219,8 @@ def _resident_ws_bytes(dims, B, recompute):
     """Restated workspace of a layer-resident plan: the column kernel's
     barrier words and f(x) buffers, then 256 bytes of step flags and the
     double-buffered exchange of 16x16 tiles (1 KiB each): eps[l] for
-    l = 1..L-2, W[l]^T eps[l] for l = 0..L-2, and one partial product per
+    l = 1..L-2, W[l]^T eps[l] for l = 0..L-2 (three buffers for l = L-2, which
+    the top chunks read one step late), and one partial product per
     128-column chunk of the top layer; then the chunks' input images."""
     L = len(dims) - 1
     n = 256
@@ -233,7 +234,7 @@ def _resident_ws_bytes(dims, B, recompute):
     for l in range(L - 1):
         if l >= 1:
             n += 2 * tiles(dims[l]) * 1024
-        n += 2 * tiles(dims[l + 1]) * 1024
+        n += (3 if l + 2 == L else 2) * tiles(dims[l + 1]) * 1024
     C = -(-dims[L] // 128)
     n += 2 * (C + 1) * tiles(dims[L - 1]) * 1024   # the partials and chunk 0's summed eps[L-1]
     # then, per top chunk, its cached 16-bit f(x[L]) operands as laid out in
