@@ -71,11 +71,41 @@ __device__ __forceinline__ f32x4 zero4() { return f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 // instructions instead of an integer-division sequence).
 __device__ __forceinline__ int qdiv(int n, float inv) { return (int)(((float)n + 0.5f) * inv); }
 
+// Global-memory (address space 1) views.  The state and workspace pointers
+// arrive through the LDS copy of the argument block, which hides their address
+// space; flat accesses would count against the LDS wait counter as well, so
+// every LDS wait after one would also wait for memory.
+typedef __attribute__((address_space(1))) float gf32;
+typedef __attribute__((address_space(1))) f32x4 gf32x4;
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) u32x4 gu32x4;
+__device__ __forceinline__ gf32* gbl(float* p) { return (gf32*)p; }
+__device__ __forceinline__ const gf32* gbl(const float* p) { return (const gf32*)p; }
+
+// A pointer every lane holds the same value of, moved to scalar registers
+// (loads through it then take a 32-bit per-lane offset instead of a 64-bit
+// per-lane address).
+__device__ __forceinline__ const float* uniform(const float* p) {
+  const unsigned long long v = reinterpret_cast<unsigned long long>(p);
+  const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)v);
+  const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(v >> 32));
+  return reinterpret_cast<const float*>(((unsigned long long)hi << 32) | lo);
+}
+
+// Element idx of a state or weight matrix (a uniform pointer) when `in`,
+// else 0.  The load is issued for every lane (at index 0 when out of range),
+// so a wave's loads leave together instead of one branch, and one memory
+// latency, each.
+__device__ __forceinline__ float ld_or0(const float* m, int idx, bool in) {
+  const float v = gbl(m)[in ? idx : 0];
+  return in ? v : 0.0f;
+}
+
 // An exchange record is one 16x16 result tile stored as every lane's four
 // result registers (16 bytes per lane), so each access is one 16-byte load or
 // store per lane.
-__device__ __forceinline__ f32x4 ld_rec(const float* r) { return *reinterpret_cast<const f32x4*>(r); }
-__device__ __forceinline__ void st_rec(float* r, f32x4 v) { *reinterpret_cast<f32x4*>(r) = v; }
+__device__ __forceinline__ f32x4 ld_rec(const float* r) { return *(const gf32x4*)r; }
+__device__ __forceinline__ void st_rec(float* r, f32x4 v) { *(gf32x4*)r = v; }
 
 constexpr int PBATCH = 8;  // top-layer partial products loaded per batch
 
@@ -488,35 +518,32 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
   const float gamma = p.gamma, alpha = p.alpha;
   // fb: f(x[l+1]) as staged for the MFMAs, reused for the next step's f'(x[l+1])
   f32x4 xa[MAXT], ea[MAXT], xb[MAXT], gb[MAXT], fb[MAXT], wr[MU];
+  // (a tile index past the tile count maps to rows past the matrix, so the
+  // range checks alone zero it; every load is issued without a branch)
 #pragma unroll
   for (int i = 0; i < MAXT; ++i) {
     const int t = wave + NWV * i;
-    xa[i] = zero4(); xb[i] = zero4(); ea[i] = zero4(); gb[i] = zero4(); fb[i] = zero4();
+    ea[i] = zero4(); gb[i] = zero4(); fb[i] = zero4();
     const int b = k.tcol(t);
-    if (t < npr)
+    const float* x0 = uniform(p.x[l]);
+    const float* x1 = uniform(p.x[l + 1]);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int r = k.trow(t, q);
-        if (r < k.M && b < B) xa[i][q] = p.x[l][(long long)r * B + b];
-      }
-    if (t < ninf)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int r = k.trow(t, q);
-        if (r < k.K && b < B) xb[i][q] = p.x[l + 1][(long long)r * B + b];
-      }
+    for (int q = 0; q < 4; ++q) {
+      const int r = k.trow(t, q);
+      xa[i][q] = ld_or0(x0, r * B + b, r < k.M && b < B);
+      xb[i][q] = ld_or0(x1, r * B + b, r < k.K && b < B);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // one batch of loads per tile (register pressure)
   }
 #pragma unroll
   for (int i = 0; i < MU; ++i) {
     const int t = wave + NWV * i;
-    wr[i] = zero4();
-    if (t < k.n_upd) {
-      const int c = k.uct(t) * 16 + lr;
+    const int c = k.uct(t) * 16 + lr;
+    const float* w = uniform(p.w[l]);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int r = k.urt(t) * 16 + 4 * lg + q;
-        if (r < k.M && c < k.K) wr[i][q] = p.w[l][(long long)r * k.ldw_g + c];
-      }
+    for (int q = 0; q < 4; ++q) {
+      const int r = k.urt(t) * 16 + 4 * lg + q;
+      wr[i][q] = ld_or0(w, r * k.ldw_g + c, r < k.M && c < k.K);
     }
   }
   setup(k, p, peers, npeers_lds);
@@ -648,9 +675,9 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
         const int r = k.trow(t, q);
         if (r < k.M && b < B) {
           const long long o = (long long)r * B + b;
-          E[o] = ea[i][q];
-          if (X) X[o] = xa[i][q];
-          if (FX) FX[o] = act_t<ACT>(xa[i][q]);
+          gbl(E)[o] = ea[i][q];
+          if (X) gbl(X)[o] = xa[i][q];
+          if (FX) gbl(FX)[o] = act_t<ACT>(xa[i][q]);
         }
       }
     }
@@ -663,7 +690,7 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int r = k.urt(t) * 16 + 4 * lg + q;
-        if (r < k.M && c < k.K) p.w[l][(long long)r * k.ldw_g + c] = wr[i][q];
+        if (r < k.M && c < k.K) gbl(p.w[l])[(long long)r * k.ldw_g + c] = wr[i][q];
       }
     }
   }
@@ -682,8 +709,8 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
           const int r = k.trow(t, q);
           if (r < k.K && b < B) {
             const long long o = (long long)r * B + b;
-            XU[o] = xb[i][q];
-            if (FXU) FXU[o] = act_t<ACT>(xb[i][q]);
+            gbl(XU)[o] = xb[i][q];
+            if (FXU) gbl(FXU)[o] = act_t<ACT>(xb[i][q]);
           }
         }
       }
@@ -703,23 +730,18 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
 #pragma unroll
   for (int i = 0; i < MAXT; ++i) {
     const int t = wave + NWV * i;
-    xa[i] = zero4(); wr[i] = zero4();
-    if (t < npr) {
-      const int b = k.tcol(t);
+    // (tile indices past the counts map to rows past the matrix: the range
+    // checks alone zero them, and every load is issued without a branch)
+    const int b = k.tcol(t), c = k.uct(t) * 16 + lr;
+    const float* x0 = uniform(p.x[l]);
+    const float* w = uniform(p.w[l]);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int r = k.trow(t, q);
-        if (r < k.M && b < B) xa[i][q] = p.x[l][(long long)r * B + b];
-      }
+    for (int q = 0; q < 4; ++q) {
+      const int r = k.trow(t, q), ru = k.urt(t) * 16 + 4 * lg + q;
+      xa[i][q] = ld_or0(x0, r * B + b, r < k.M && b < B);
+      wr[i][q] = ld_or0(w, ru * k.ldw_g + k.k0 + c, ru < k.M && c < k.K);
     }
-    if (t < k.n_upd) {
-      const int c = k.uct(t) * 16 + lr;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int r = k.urt(t) * 16 + 4 * lg + q;
-        if (r < k.M && c < k.K) wr[i][q] = p.w[l][(long long)r * k.ldw_g + k.k0 + c];
-      }
-    }
+    __builtin_amdgcn_sched_barrier(0);  // one batch of loads per tile (register pressure)
   }
   setup(k, p, peers, npeers_lds);
   const int npeers = npeers_lds;
@@ -733,14 +755,15 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
   const bool warm = *reinterpret_cast<const volatile unsigned*>(&p.flags[RES_MAX_WG]) == 1u;
   if (warm) {
     constexpr int CB = 8;  // 16-byte loads in flight per thread
-    const uint4* src = reinterpret_cast<const uint4*>(image);
+    const gu32x4* src = (const gu32x4*)image;
+    u32x4* dst = reinterpret_cast<u32x4*>(lds_image);
     for (int base = threadIdx.x; base < n16; base += CB * NT) {
-      uint4 v[CB];
+      u32x4 v[CB];
 #pragma unroll
-      for (int u = 0; u < CB; ++u) v[u] = base + u * NT < n16 ? src[base + u * NT] : uint4{0u, 0u, 0u, 0u};
+      for (int u = 0; u < CB; ++u) v[u] = src[min(base + u * NT, n16 - 1)];
 #pragma unroll
       for (int u = 0; u < CB; ++u)
-        if (base + u * NT < n16) lds_image[base + u * NT] = v[u];
+        if (base + u * NT < n16) dst[base + u * NT] = v[u];
     }
   } else {
     // evaluate f(x[L]) of the chunk; also written to fx[L]
@@ -753,7 +776,7 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
 #pragma unroll
       for (int u = 0; u < SB; ++u) {
         const int idx = base + u * NT;
-        v[u] = idx < n ? XL[(long long)k.k0 * B + idx] : 0.0f;
+        v[u] = ld_or0(XL, k.k0 * B + idx, idx < n);
       }
 #pragma unroll
       for (int u = 0; u < SB; ++u) {
@@ -761,13 +784,14 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
         if (idx < n) {
           const int kk = qdiv(idx, k.inv_B), b = idx - kk * B;
           k.stage_f(kk, b, v[u]);
-          if (FL) FL[(long long)k.k0 * B + idx] = act_t<ACT>(v[u]);
+          if (FL) gbl(FL)[(long long)k.k0 * B + idx] = act_t<ACT>(v[u]);
         }
       }
     }
     __syncthreads();
-    uint4* dst = reinterpret_cast<uint4*>(image);
-    for (int i = threadIdx.x; i < n16; i += NT) dst[i] = lds_image[i];
+    gu32x4* dst = (gu32x4*)image;
+    const u32x4* src = reinterpret_cast<const u32x4*>(lds_image);
+    for (int i = threadIdx.x; i < n16; i += NT) dst[i] = src[i];
   }
 #pragma unroll
   for (int i = 0; i < MAXT; ++i) {
@@ -866,7 +890,7 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
           const int r = k.trow(t, q);
           if (r < k.M && b < B) {
             k.lds[k.lay.ea + r * k.lay.lda + b] = cvt<OT>(ev4[i][q]);
-            if (last && j == 0) p.e[l][(long long)r * B + b] = ev4[i][q];
+            if (last && j == 0) gbl(p.e[l])[(long long)r * B + b] = ev4[i][q];
           }
         }
       }
@@ -902,7 +926,7 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int r = k.urt(t) * 16 + 4 * lg + q;
-        if (r < k.M && c < k.K) p.w[l][(long long)r * k.ldw_g + k.k0 + c] = wr[i][q];
+        if (r < k.M && c < k.K) gbl(p.w[l])[(long long)r * k.ldw_g + k.k0 + c] = wr[i][q];
       }
     }
   }
