@@ -171,10 +171,10 @@ struct Resident {
   int nbt, n_pred, n_inf, n_upd, ktl, ks_k, ks_m, ks_b;
   float inv_nbt, inv_ktl, inv_B;
 
-  __device__ __forceinline__ Resident(const ResidentArgs& a, char* base)
+  __device__ __forceinline__ Resident(const ResidentArgs& a, char* base, int role)
       : p(a), lds(reinterpret_cast<OT*>(base)), tid(threadIdx.x), lane(threadIdx.x & 63), wave(threadIdx.x >> 6),
         lr(threadIdx.x & 15), lg((threadIdx.x & 63) >> 4) {
-    wg = blockIdx.x;
+    wg = role;
     L = p.L;
     B = p.B;
     hidden = wg < L - 1;
@@ -932,6 +932,22 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
   }
 }
 
+// XCD-aware placement.  Blocks are dealt to the eight XCDs round-robin by
+// block index, so the top chunks take blocks 0, 8, 16, ... (one XCD: each of
+// them reads all the others' partial products every step, and those reads
+// then share one L2) and the hidden workgroups the blocks between; the spare
+// blocks of the grid exit at once.  Placement only affects speed: every
+// exchange is ordered at agent scope wherever the workgroups run.
+__host__ __device__ inline int resident_role(int bid, int hidden, int chunks) {
+  if ((bid & 7) == 0) return (bid >> 3) < chunks ? hidden + (bid >> 3) : -1;
+  const int l = bid - 1 - (bid >> 3);
+  return l < hidden ? l : -1;
+}
+inline int resident_grid(int hidden, int chunks) {
+  const int top = 8 * (chunks - 1) + 1, low = hidden > 0 ? hidden + (hidden - 1) / 7 + 1 : 0;
+  return top > low ? top : low;
+}
+
 template <typename OT, int SPLIT, int ACT>
 __global__ void __launch_bounds__(NT) resident_kernel(const ResidentArgs args) {
   using R = Resident<OT, SPLIT, ACT>;
@@ -942,10 +958,12 @@ __global__ void __launch_bounds__(NT) resident_kernel(const ResidentArgs args) {
   __shared__ int peers[RES_MAX_WG];
   __shared__ int npeers;
   static_assert(sizeof(ResidentArgs) % 4 == 0, "argument block copy");
+  const int role = resident_role(blockIdx.x, args.L - 1, args.chunks);
+  if (role < 0) return;  // a spare block of the XCD-aware grid
   for (int i = threadIdx.x; i < (int)(sizeof(ResidentArgs) / 4); i += NT)
     reinterpret_cast<int*>(&p)[i] = reinterpret_cast<const int*>(&args)[i];
   __syncthreads();
-  R k(p, lds_raw);
+  R k(p, lds_raw, role);
   if (k.hidden) run_hidden(k, p, peers, npeers);
   else run_top(k, p, peers, npeers);
 
@@ -971,7 +989,8 @@ struct ResLaunch {
                                hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
   }
   static hipError_t launch(const ResidentArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL((resident_kernel<OT, SPLIT, ACT>), dim3(a.nwg), dim3(NT), (size_t)a.lds_bytes, s, a);
+    hipLaunchKernelGGL((resident_kernel<OT, SPLIT, ACT>), dim3(resident_grid(a.L - 1, a.chunks)), dim3(NT),
+                       (size_t)a.lds_bytes, s, a);
     return hipGetLastError();
   }
 };
