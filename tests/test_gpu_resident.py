@@ -3,7 +3,8 @@
 * Against the fp32 oracle after T steps: states <= 2e-2, weight deltas <= 5e-3
   (the 16-bit operand bars), on ragged shapes: widths and batches that are not
   multiples of 16, a top layer whose last 128-column chunk is partial, L = 2
-  (one hidden-layer workgroup next to the top chunks).
+  (one hidden-layer workgroup next to the top chunks), and nine hidden layers
+  with nine top chunks (the XCD-aware grid's later blocks).
 * Against the column-block whole-step kernel: the same operands, the same
   MFMA chains and the same 128-column partial-sum order, so every state,
   error and weight must agree bit for bit.
@@ -27,6 +28,9 @@ SHAPES = [
     ((7, 33, 48, 130), 40),
     ((10, 48, 64, 40, 300), 100),
     ((3, 64, 64, 100), 17),
+    # nine hidden workgroups and nine top chunks: roles past the first block of
+    # each XCD in the XCD-aware grid (65 blocks)
+    ((10,) + (32,) * 9 + (1100,), 64),
 ]
 
 
@@ -66,7 +70,7 @@ def test_resident_matches_oracle(dims, B, op):
 
 @pytest.mark.parametrize("act", ["tanh", "relu", "sigmoid", "gelu"])
 @pytest.mark.parametrize("op,split", [(F16, 3), (BF16, 3), (F16, 1)])
-@pytest.mark.parametrize("dims,B", [SHAPES[2], SHAPES[3], SHAPES[4]])
+@pytest.mark.parametrize("dims,B", [SHAPES[2], SHAPES[3], SHAPES[4], SHAPES[6]])
 def test_resident_equals_column_kernel_bitwise(dims, B, op, split, act):
     T = 5
     report("resident-vs-column", dims=dims, B=B, op=op, split=split, act=act)
