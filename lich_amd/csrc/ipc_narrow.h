@@ -96,9 +96,11 @@ constexpr int RES_MAX_WIDTH = 64;   // d_0 .. d_{L-1}
 constexpr int RES_MAX_B = 128;
 constexpr int RES_MAX_WG = 63;      // word 63 of the flag area is the input-image flag
 constexpr int RES_TILE = 256;       // floats per exchanged 16x16 tile (64 lanes x 4)
+constexpr int RES_TOP_ROWS = 32;    // rows of W[L-1] per top workgroup (a 64-row layer takes two)
 
 struct ResidentArgs {
   int L, B, steps, nwg, chunks, kc, spin_limit, lds_bytes;
+  int halves;                   // top-layer row blocks of RES_TOP_ROWS (one workgroup per chunk and block)
   float alpha, gamma;
   int dims[NARROW_MAX_L + 1];
   float* x[NARROW_MAX_L + 1];
@@ -108,11 +110,12 @@ struct ResidentArgs {
   float* xe[NARROW_MAX_L];      // eps[l], l = 1..L-2:        [2][tiles(d_l)][RES_TILE]
   float* xg[NARROW_MAX_L];      // W[l]^T eps[l], l = 0..L-2: [2][tiles(d_{l+1})][RES_TILE]
   float* xp;                    // top-layer partial products: [2][chunks][tiles(d_{L-1})][RES_TILE]
-  float* xs;                    // eps[L-1] summed by top chunk 0: [2][tiles(d_{L-1})][RES_TILE]
+  float* xs;                    // eps[L-1] as summed by each row block's chunk 0: [2][tiles(d_{L-1})][RES_TILE]
   char* image;                  // per top chunk: its f(x[L]) operand LDS image, image_stride bytes apart
   long long image_stride;
-  unsigned* flags;              // [nwg] last step each workgroup has published, [nwg] the last step
-                                // whose eps[L-1] top chunk 0 has published; [RES_MAX_WG] image valid
+  unsigned* flags;              // [nwg] last step each workgroup has published, [nwg + h] the last step
+                                // whose eps[L-1] rows top chunk 0 of row block h has published;
+                                // [RES_MAX_WG] image valid
   unsigned* bar;                // [1] exit counter, [2] wait timeout flag (shared with the column kernel)
 };
 

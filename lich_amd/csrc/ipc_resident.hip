@@ -167,6 +167,9 @@ struct Resident {
   ResidentLds lay;
   int tid, lane, wave, lr, lg;
   int wg, L, B, l, j, M, K, k0, ldw_g;  // ldw_g: row stride of W[l] in memory
+  // top workgroups: row block h (rows row0 .. row0 + M - 1 of W[L-1]); toff: the
+  // block's first tile in the layer's exchange records of npr_full tiles
+  int h, row0, toff, npr_full;
   bool hidden;
   int nbt, n_pred, n_inf, n_upd, ktl, ks_k, ks_m, ks_b;
   float inv_nbt, inv_ktl, inv_B;
@@ -179,8 +182,11 @@ struct Resident {
     B = p.B;
     hidden = wg < L - 1;
     l = hidden ? wg : L - 1;
-    j = hidden ? 0 : wg - (L - 1);
-    M = p.dims[l];
+    const int top = hidden ? 0 : wg - (L - 1);
+    j = hidden ? 0 : top % p.chunks;
+    h = hidden ? 0 : top / p.chunks;
+    row0 = h * RES_TOP_ROWS;
+    M = hidden ? p.dims[l] : min(RES_TOP_ROWS, p.dims[l] - row0);
     k0 = hidden ? 0 : j * p.kc;
     K = hidden ? p.dims[l + 1] : min(p.kc, p.dims[L] - k0);
     ldw_g = p.dims[l + 1];
@@ -189,6 +195,8 @@ struct Resident {
     const int mtl = (M + 15) / 16;
     ktl = (K + 15) / 16;
     n_pred = mtl * nbt;
+    toff = (row0 / 16) * nbt;
+    npr_full = ((p.dims[l] + 15) / 16) * nbt;
     n_inf = hidden ? ktl * nbt : 0;
     n_upd = mtl * ktl;
     ks_k = (K + 31) / 32;
@@ -493,13 +501,18 @@ __device__ __forceinline__ void setup(const Resident<OT, SPLIT, ACT>& k, const R
     int n = 0;
     if (k.hidden) {
       if (k.l >= 1) peers[n++] = k.l - 1;
-      // next to the top layer: top chunk 0's eps[L-1] flag (it is published only
-      // after every chunk has published, so it also covers their progress)
-      peers[n++] = k.l + 1 <= L - 2 ? k.l + 1 : p.nwg;
+      if (k.l + 1 <= L - 2) {
+        peers[n++] = k.l + 1;
+      } else {
+        // next to the top layer: each row block's chunk-0 eps[L-1] flag (published
+        // only after the block's other chunks have published, so it also covers
+        // their progress)
+        for (int hh = 0; hh < p.halves; ++hh) peers[n++] = p.nwg + hh;
+      }
     } else {
-      // the siblings, then workgroup L-2 (waited for one step behind)
+      // the siblings in the row block, then workgroup L-2 (waited for one step behind)
       for (int c = 0; c < C; ++c)
-        if (c != k.j) peers[n++] = top0 + c;
+        if (c != k.j) peers[n++] = top0 + k.h * C + c;
       peers[n++] = L - 2;
     }
     npeers = n;
@@ -724,7 +737,9 @@ template <typename OT, int SPLIT, int ACT>
 __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const ResidentArgs& p, int* peers,
                                         int& npeers_lds) {
   const int L = k.L, B = k.B, C = p.chunks, l = k.l, j = k.j, wave = k.wave, lg = k.lg, lr = k.lr;
-  const int npr = k.n_pred;
+  // npr: this row block's prediction tiles; nrec: the layer's, the size of every
+  // exchange record of the top layer (the block's tiles start at tile k.toff)
+  const int npr = k.n_pred, nrec = k.npr_full, r0 = k.row0;
   const float gamma = p.gamma, alpha = p.alpha;
   f32x4 xa[MAXT], wr[MAXT];
 #pragma unroll
@@ -738,8 +753,8 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int r = k.trow(t, q), ru = k.urt(t) * 16 + 4 * lg + q;
-      xa[i][q] = ld_or0(x0, r * B + b, r < k.M && b < B);
-      wr[i][q] = ld_or0(w, ru * k.ldw_g + k.k0 + c, ru < k.M && c < k.K);
+      xa[i][q] = ld_or0(x0, (r0 + r) * B + b, r < k.M && b < B);
+      wr[i][q] = ld_or0(w, (r0 + ru) * k.ldw_g + k.k0 + c, ru < k.M && c < k.K);
     }
     __builtin_amdgcn_sched_barrier(0);  // one batch of loads per tile (register pressure)
   }
@@ -766,9 +781,10 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
         if (base + u * NT < n16) dst[base + u * NT] = v[u];
     }
   } else {
-    // evaluate f(x[L]) of the chunk; also written to fx[L]
+    // evaluate f(x[L]) of the chunk; row block 0 also writes it to fx[L] and to
+    // the image (the chunk's row blocks share one)
     const float* XL = p.x[L];
-    float* FL = p.fx[L];
+    float* FL = k.h == 0 ? p.fx[L] : nullptr;
     constexpr int SB = 8;  // loads in flight per thread
     const int n = k.K * B;
     for (int base = threadIdx.x; base < n; base += SB * NT) {
@@ -789,9 +805,11 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
       }
     }
     __syncthreads();
-    gu32x4* dst = (gu32x4*)image;
-    const u32x4* src = reinterpret_cast<const u32x4*>(lds_image);
-    for (int i = threadIdx.x; i < n16; i += NT) dst[i] = src[i];
+    if (k.h == 0) {
+      gu32x4* dst = (gu32x4*)image;
+      const u32x4* src = reinterpret_cast<const u32x4*>(lds_image);
+      for (int i = threadIdx.x; i < n16; i += NT) dst[i] = src[i];
+    }
   }
 #pragma unroll
   for (int i = 0; i < MAXT; ++i) {
@@ -820,14 +838,14 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
     const int buf = s & 1;
     const bool last = s + 1 == p.steps;
     // ---- 1. partial product of the chunk
-    float* xp = p.xp + (long long)buf * C * npr * RES_TILE;
+    float* xp = p.xp + (long long)buf * C * nrec * RES_TILE;
     {
       f32x4 cp[MAXT];
       k.pred_tiles(npr, cp);
 #pragma unroll
       for (int i = 0; i < MAXT; ++i) {
         const int t = wave + NWV * i;
-        if (t < npr) st_rec(xp + (long long)j * npr * RES_TILE + k.rec(t), cp[i]);
+        if (t < npr) st_rec(xp + (long long)j * nrec * RES_TILE + k.rec(k.toff + t), cp[i]);
       }
     }
     // ---- 2. exchange: the siblings' partials of this step, workgroup L-2's g
@@ -842,11 +860,11 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) g[i] = zero4();
     if (s >= 1) {
-      const float* xg = p.xg[L - 2] + (long long)((s - 1) % 3) * npr * RES_TILE;
+      const float* xg = p.xg[L - 2] + (long long)((s - 1) % 3) * nrec * RES_TILE;
 #pragma unroll
       for (int i = 0; i < MAXT; ++i) {
         const int t = wave + NWV * i;
-        if (t < npr) g[i] = ld_rec(xg + k.rec(t));
+        if (t < npr) g[i] = ld_rec(xg + k.rec(k.toff + t));
       }
     }
     // ---- 3. x[L-1] of this step (the previous step's update), then eps[L-1] =
@@ -858,7 +876,7 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
       const int t = wave + NWV * i;
       ev4[i] = zero4();
       if (t < npr) {
-        const f32x4 sum = sum_partials(xp, (long long)npr * RES_TILE, C, k.rec(t));
+        const f32x4 sum = sum_partials(xp, (long long)nrec * RES_TILE, C, k.rec(k.toff + t));
         const int b = k.tcol(t);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -870,13 +888,13 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
       __builtin_amdgcn_sched_barrier(0);
     }
     if (j == 0) {
-      float* xs = p.xs + (long long)buf * npr * RES_TILE;
+      float* xs = p.xs + (long long)buf * nrec * RES_TILE;
 #pragma unroll
       for (int i = 0; i < MAXT; ++i) {
         const int t = wave + NWV * i;
-        if (t < npr) st_rec(xs + k.rec(t), ev4[i]);
+        if (t < npr) st_rec(xs + k.rec(k.toff + t), ev4[i]);
       }
-      publish(&p.flags[p.nwg], (unsigned)(s + 1));
+      publish(&p.flags[p.nwg + k.h], (unsigned)(s + 1));
     }
     // eps[L-1] into the weight-update A operand (and e[L-1] after the last step)
 #pragma unroll
@@ -890,7 +908,7 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
           const int r = k.trow(t, q);
           if (r < k.M && b < B) {
             k.lds[k.lay.ea + r * k.lay.lda + b] = cvt<OT>(ev4[i][q]);
-            if (last && j == 0) gbl(p.e[l])[(long long)r * B + b] = ev4[i][q];
+            if (last && j == 0) gbl(p.e[l])[(long long)(r0 + r) * B + b] = ev4[i][q];
           }
         }
       }
@@ -926,25 +944,28 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int r = k.urt(t) * 16 + 4 * lg + q;
-        if (r < k.M && c < k.K) gbl(p.w[l])[(long long)r * k.ldw_g + k.k0 + c] = wr[i][q];
+        if (r < k.M && c < k.K) gbl(p.w[l])[(long long)(r0 + r) * k.ldw_g + k.k0 + c] = wr[i][q];
       }
     }
   }
 }
 
 // XCD-aware placement.  Blocks are dealt to the eight XCDs round-robin by
-// block index, so the top chunks take blocks 0, 8, 16, ... (one XCD: each of
-// them reads all the others' partial products every step, and those reads
-// then share one L2) and the hidden workgroups the blocks between; the spare
-// blocks of the grid exit at once.  Placement only affects speed: every
-// exchange is ordered at agent scope wherever the workgroups run.
-__host__ __device__ inline int resident_role(int bid, int hidden, int chunks) {
-  if ((bid & 7) == 0) return (bid >> 3) < chunks ? hidden + (bid >> 3) : -1;
-  const int l = bid - 1 - (bid >> 3);
+// block index, so the top workgroups of row block h take blocks h, h + 8,
+// h + 16, ... (one XCD per row block: each of them reads all its siblings'
+// partial products every step, and those reads then share one L2) and the
+// hidden workgroups the other XCDs' blocks; the spare blocks of the grid exit
+// at once.  Placement only affects speed: every exchange is ordered at agent
+// scope wherever the workgroups run.
+__host__ __device__ inline int resident_role(int bid, int hidden, int chunks, int halves) {
+  const int x = bid & 7, i = bid >> 3;
+  if (x < halves) return i < chunks ? hidden + x * chunks + i : -1;
+  const int l = i * (8 - halves) + (x - halves);
   return l < hidden ? l : -1;
 }
-inline int resident_grid(int hidden, int chunks) {
-  const int top = 8 * (chunks - 1) + 1, low = hidden > 0 ? hidden + (hidden - 1) / 7 + 1 : 0;
+inline int resident_grid(int hidden, int chunks, int halves) {
+  const int top = 8 * (chunks - 1) + halves;
+  const int low = hidden > 0 ? 8 * ((hidden - 1) / (8 - halves)) + halves + (hidden - 1) % (8 - halves) + 1 : 0;
   return top > low ? top : low;
 }
 
@@ -958,7 +979,7 @@ __global__ void __launch_bounds__(NT) resident_kernel(const ResidentArgs args) {
   __shared__ int peers[RES_MAX_WG];
   __shared__ int npeers;
   static_assert(sizeof(ResidentArgs) % 4 == 0, "argument block copy");
-  const int role = resident_role(blockIdx.x, args.L - 1, args.chunks);
+  const int role = resident_role(blockIdx.x, args.L - 1, args.chunks, args.halves);
   if (role < 0) return;  // a spare block of the XCD-aware grid
   for (int i = threadIdx.x; i < (int)(sizeof(ResidentArgs) / 4); i += NT)
     reinterpret_cast<int*>(&p)[i] = reinterpret_cast<const int*>(&args)[i];
@@ -972,7 +993,8 @@ __global__ void __launch_bounds__(NT) resident_kernel(const ResidentArgs args) {
   if (threadIdx.x == 0) {
     const unsigned prev = __hip_atomic_fetch_add(&p.bar[1], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     if (prev == (unsigned)p.nwg - 1) {
-      for (int w = 0; w <= p.nwg; ++w) __hip_atomic_store(&p.flags[w], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int w = 0; w < p.nwg + p.halves; ++w)
+        __hip_atomic_store(&p.flags[w], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       // the top chunks' input images are now written (read by the next launch,
       // after this kernel has completed)
       __hip_atomic_store(&p.flags[RES_MAX_WG], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -989,7 +1011,7 @@ struct ResLaunch {
                                hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
   }
   static hipError_t launch(const ResidentArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL((resident_kernel<OT, SPLIT, ACT>), dim3(resident_grid(a.L - 1, a.chunks)), dim3(NT),
+    hipLaunchKernelGGL((resident_kernel<OT, SPLIT, ACT>), dim3(resident_grid(a.L - 1, a.chunks, a.halves)), dim3(NT),
                        (size_t)a.lds_bytes, s, a);
     return hipGetLastError();
   }
@@ -1035,17 +1057,20 @@ long long resident_plan(const int* dims, int L, int B, int split, ResidentArgs& 
   }
   // top layer: one workgroup per NARROW_KCHUNK columns (the column kernel's
   // partial-sum order)
+  // and row blocks of RES_TOP_ROWS rows (a workgroup per chunk and block)
   const int dL = dims[L], kc = NARROW_KCHUNK, C = (dL + kc - 1) / kc;
-  if ((L - 1) + C + 1 > RES_MAX_WG) return -1;  // flags[nwg] is chunk 0's eps flag
+  const int halves = (dims[L - 1] + RES_TOP_ROWS - 1) / RES_TOP_ROWS;
+  if ((L - 1) + halves * C + halves > RES_MAX_WG) return -1;  // flags[nwg + h]: block h's eps flags
   ResidentLds o;
-  resident_lds_layout(dims[L - 1], dL < kc ? dL : kc, B, false, s3, o);
+  resident_lds_layout(dims[L - 1] < RES_TOP_ROWS ? dims[L - 1] : RES_TOP_ROWS, dL < kc ? dL : kc, B, false, s3, o);
   need = o.bytes > need ? o.bytes : need;
   if (need > limit) return -1;
   a.L = L;
   a.B = B;
   a.chunks = C;
   a.kc = kc;
-  a.nwg = (L - 1) + C;
+  a.halves = halves;
+  a.nwg = (L - 1) + halves * C;
   a.lds_bytes = res_round(need, 16);
   for (int l = 0; l <= L; ++l) a.dims[l] = dims[l];
   long long bytes = 256;  // flags
