@@ -10,6 +10,7 @@
   error and weight must agree bit for bit.
 * Launch boundaries do not change bits, and no wait ever hits its spin limit.
 """
+import numpy as np
 import pytest
 import torch
 
@@ -141,6 +142,28 @@ def test_resident_save_mode_writes_activations():
     for l in range(1, len(dims)):
         ref = O.act_forward("silu", ms[1].x[l].cpu())
         assert torch.allclose(saved[l].cpu(), ref, rtol=1e-6, atol=1e-6), l
+
+
+def test_tanh_within_two_ulp():
+    """The kernels' fp32 tanh (a fitted odd polynomial below 0.55, the
+    exponential form above) against float64 tanh, on the resident kernel's
+    saved activations f(x[l]) = tanh(x[l]) of the final states."""
+    dims, B, T = (10, 64, 64, 784), 128, 4
+    report("tanh-ulp", dims=dims, B=B)
+    w0 = O.init_weights(dims, seed=8, init="xavier_uniform")
+    x_in, _labels, y = O.make_batch(dims, B, seed=8)
+    m = _model(dims, w0, "tanh", F16, "resident", recompute=False)
+    m.initialize_batch(x_in.to(DEV), y.to(DEV))
+    m.run_steps(T)
+    torch.cuda.synchronize()
+    worst = 0.0
+    for l in range(1, len(dims)):
+        x = m.x[l].double().cpu()
+        ref = torch.tanh(x)
+        ulp = torch.from_numpy(np.spacing(ref.abs().float().numpy())).double()
+        worst = max(worst, float(((m.a[l].double().cpu() - ref).abs() / ulp).max()))
+    print(f"tanh: worst {worst:.2f} ulp over the saved activations")
+    assert worst <= 2.0
 
 
 def test_cached_input_images_follow_new_batches_and_direct_writes():
