@@ -93,13 +93,12 @@ __device__ __forceinline__ const float* uniform(const float* p) {
 }
 
 // Element idx of a state or weight matrix (a uniform pointer) when `in`,
-// else 0.  The load is issued for every lane (at index 0 when out of range),
-// so a wave's loads leave together instead of one branch, and one memory
-// latency, each.
-__device__ __forceinline__ float ld_or0(const float* m, int idx, bool in) {
-  const float v = gbl(m)[in ? idx : 0];
-  return in ? v : 0.0f;
-}
+// else element 0 of it.  The load is issued for every lane, so a wave's loads
+// leave together instead of one branch, and one memory latency, each; and
+// the value is not masked here, so nothing waits for it before its first use.
+// Out-of-range values never reach an output: every use of one (staging,
+// errors, stores) checks the range again.
+__device__ __forceinline__ float ld_at(const float* m, int idx, bool in) { return gbl(m)[in ? idx : 0]; }
 
 // An exchange record is one 16x16 result tile stored as every lane's four
 // result registers (16 bytes per lane), so each access is one 16-byte load or
@@ -532,7 +531,7 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
   // fb: f(x[l+1]) as staged for the MFMAs, reused for the next step's f'(x[l+1])
   f32x4 xa[MAXT], ea[MAXT], xb[MAXT], gb[MAXT], fb[MAXT], wr[MU];
   // (a tile index past the tile count maps to rows past the matrix, so the
-  // range checks alone zero it; every load is issued without a branch)
+  // range checks alone cover it; every load is issued without a branch)
 #pragma unroll
   for (int i = 0; i < MAXT; ++i) {
     const int t = wave + NWV * i;
@@ -543,8 +542,8 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int r = k.trow(t, q);
-      xa[i][q] = ld_or0(x0, r * B + b, r < k.M && b < B);
-      xb[i][q] = ld_or0(x1, r * B + b, r < k.K && b < B);
+      xa[i][q] = ld_at(x0, r * B + b, r < k.M && b < B);
+      xb[i][q] = ld_at(x1, r * B + b, r < k.K && b < B);
     }
     __builtin_amdgcn_sched_barrier(0);  // one batch of loads per tile (register pressure)
   }
@@ -556,7 +555,7 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int r = k.urt(t) * 16 + 4 * lg + q;
-      wr[i][q] = ld_or0(w, r * k.ldw_g + c, r < k.M && c < k.K);
+      wr[i][q] = ld_at(w, r * k.ldw_g + c, r < k.M && c < k.K);
     }
   }
   setup(k, p, peers, npeers_lds);
@@ -746,15 +745,15 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
   for (int i = 0; i < MAXT; ++i) {
     const int t = wave + NWV * i;
     // (tile indices past the counts map to rows past the matrix: the range
-    // checks alone zero them, and every load is issued without a branch)
+    // checks alone cover them, and every load is issued without a branch)
     const int b = k.tcol(t), c = k.uct(t) * 16 + lr;
     const float* x0 = uniform(p.x[l]);
     const float* w = uniform(p.w[l]);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int r = k.trow(t, q), ru = k.urt(t) * 16 + 4 * lg + q;
-      xa[i][q] = ld_or0(x0, (r0 + r) * B + b, r < k.M && b < B);
-      wr[i][q] = ld_or0(w, (r0 + ru) * k.ldw_g + k.k0 + c, ru < k.M && c < k.K);
+      xa[i][q] = ld_at(x0, (r0 + r) * B + b, r < k.M && b < B);
+      wr[i][q] = ld_at(w, (r0 + ru) * k.ldw_g + k.k0 + c, ru < k.M && c < k.K);
     }
     __builtin_amdgcn_sched_barrier(0);  // one batch of loads per tile (register pressure)
   }
@@ -792,7 +791,7 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
 #pragma unroll
       for (int u = 0; u < SB; ++u) {
         const int idx = base + u * NT;
-        v[u] = ld_or0(XL, k.k0 * B + idx, idx < n);
+        v[u] = ld_at(XL, k.k0 * B + idx, idx < n);
       }
 #pragma unroll
       for (int u = 0; u < SB; ++u) {
