@@ -37,7 +37,7 @@ METRIC = "iPC train samples/sec (L=6,h=64,B=128); fused-GEMM TFLOP/s vs MFMA pea
 # `bench.py --no-cpu --no-wide`, each scaled by the same counter's reading for
 # a plain device copy of known size (`bench.py --copy-calibration`: FETCH_SIZE
 # x 2.0, WRITE_SIZE x 1.0).  Keyed by kernel; re-measure after a kernel change.
-MEASURED_TRAFFIC = {"layer-resident whole-step kernel, 4 steps per launch": 3_703_808 + 3_401_888,
+MEASURED_TRAFFIC = {"layer-resident whole-step kernel, 4 steps per launch": 4_320_896 + 3_374_720,
                     "whole-step kernel, 4 steps per launch": 13_065_152 + 3_926_848}
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0  # dense, no sparsity
