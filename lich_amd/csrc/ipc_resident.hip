@@ -9,8 +9,9 @@
 //   workgroup l (l = 0 .. L-2) owns W[l] (d_l x d_{l+1}, fp32 master in MFMA
 //   result registers, 16-bit hi / lo / transposed operand copies in LDS),
 //   x[l] and x[l+1] for the whole batch; the top layer's W[L-1], whose
-//   contraction runs over the input width, is split into column chunks, one
-//   workgroup each, every one holding f(x[L]) for its chunk (x[L] is clamped).
+//   contraction runs over the input width, is split into column chunks and
+//   row blocks, one workgroup per chunk and block, every one holding f(x[L])
+//   for its chunk (x[L] is clamped).
 //
 // A step, per workgroup:
 //   1. P = W f(x[l+1]) with split-3 16-bit MFMA (hi*hi + lo*hi + hi*lo);
@@ -23,12 +24,13 @@
 //   3. x[l] += gamma(-eps[l] + f'(x[l]) g[l]) with g[l] from workgroup l-1 and
 //      x[l+1] += gamma(-eps[l+1] + f'(x[l+1]) g) with eps[l+1] from workgroup
 //      l+1.  eps[L-1] = x[L-1] minus the top chunks' partials summed in chunk
-//      order; top chunk 0 hands it to workgroup L-2 as one record under a
-//      second flag.  The chunks apply x[L-1]'s update one step late (with
-//      workgroup L-2's g of the previous step), so they never wait for
-//      workgroup L-2's current step.  Both neighbours evaluate every shared
-//      state with the same operands in the same order, so their copies stay
-//      bit-identical without a second exchange.
+//      order (per row block); each block's chunk 0 hands its rows to workgroup
+//      L-2 as one record under a flag of its own.  The top workgroups apply
+//      x[L-1]'s update one step late (with workgroup L-2's g of the previous
+//      step), so they never wait for workgroup L-2's current step.  Both
+//      neighbours evaluate every shared state with the same operands in the
+//      same order, so their copies stay bit-identical without a second
+//      exchange.
 //   4. W[l] += alpha eps[l] f(x_new[l+1])^T over the batch with MFMA, operand
 //      copies restaged in LDS.
 // One flag exchange per step replaces the two grid barriers; W, the states
@@ -626,7 +628,7 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
       }
     }
     {
-      // eps[l+1] from workgroup l+1, or eps[L-1] as summed by top chunk 0
+      // eps[l+1] from workgroup l+1, or eps[L-1] as summed by the row blocks' chunk 0
       const float* xeu = (from_top ? p.xs : p.xe[l + 1]) + (long long)buf * ninf * RES_TILE;
 #pragma unroll
       for (int i = 0; i < MAXT; ++i) {
@@ -707,8 +709,8 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
     }
   }
   if (from_top) {
-    // x[L-1] after the last step: the top chunks apply each step's update one
-    // step late, so the final one is written here, from this workgroup's copy
+    // x[L-1] after the last step: the top workgroups apply each step's update
+    // one step late, so the final one is written here, from this workgroup's copy
     float* XU = p.x[l + 1];
     float* FXU = p.fx[l + 1];
 #pragma unroll
@@ -730,8 +732,9 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
   }
 }
 
-// Top-layer chunk j: columns [k0, k0 + K) of W[L-1] at the update tiles,
-// x[L-1] at the prediction tiles, f(x[L]) of the chunk in LDS.
+// Top-layer chunk j, row block h: rows [row0, row0 + M) and columns
+// [k0, k0 + K) of W[L-1] at the update tiles, the same rows of x[L-1] at the
+// prediction tiles, f(x[L]) of the chunk in LDS.
 template <typename OT, int SPLIT, int ACT>
 __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const ResidentArgs& p, int* peers,
                                         int& npeers_lds) {
