@@ -12,7 +12,9 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <functional>
 #include <new>
+#include <queue>
 #include <string>
 #include <vector>
 
@@ -413,6 +415,8 @@ struct ipc_plan {
   // wide GEMM path
   bool wide = false;
   std::vector<WideProblem> wpred, winfer, wweight, wfwd;  // wfwd: l = L-1 .. 1
+  int pred_ksplit = 1;                                    // > 1: layer 0's prediction is k-split (last in wpred)
+  WideReduce wreduce{};                                   // its epilogue
   std::vector<WideCopy> wsync, wsync_init;               // wsync_init: W and x[L] only
   long long ws_bytes = 0;
 };
@@ -444,6 +448,10 @@ struct WideLayout {
   struct Buf { long long off = -1, ld = 0, rows = 0; };
   std::vector<Buf> wh, wl, wt, f, ft, e, et;
   long long total = 256;
+  // fp32 partial products of a k-split layer-0 prediction: up to part_smax
+  // slices of [d_0][B], part_stride floats apart
+  int part_smax = 1;
+  long long part_off = -1, part_stride = 0;
 
   Buf add(long long rows, long long cols) {
     Buf b;
@@ -468,8 +476,51 @@ struct WideLayout {
       e[l] = add(d[l], B);                      // [d_l][B]        weight A
       if (l <= L - 2) et[l] = add(B, d[l]);     // [B][d_l]        infer B (layer l+1)
     }
+    // the k-split prediction cuts layer 0's tiles into at most 512 slices in all
+    int bm = 0, bn = 0;
+    wide_pred_tile(split2 ? 2 : 1, &bm, &bn);
+    const long long t0 = ((d[0] + bm - 1) / bm) * (long long)((B + bn - 1) / bn);
+    for (int sl = 16; sl >= 2; sl /= 2)
+      if (sl * t0 <= 512 && wh[0].ld % (sl * WIDE_BK) == 0) { part_smax = sl; break; }
+    if (part_smax > 1) {
+      part_stride = (long long)d[0] * B;
+      part_off = total;
+      total += wide_pad(part_smax * part_stride * 4, 256);
+    }
   }
 };
+
+// Slices of layer 0's prediction (1 = not split): the count, up to
+// part_smax, with the shortest estimated launch when the tiles are handed to
+// `ncu` CUs in dispatch order (every whole tile of layers 1..L-1, then the
+// slices), one workgroup per CU, each tile costing its k-steps and each slice
+// two more (prologue and partial-product store); a split pays four k-steps
+// for the reduce launch.
+int wide_pred_ksplit(const std::vector<int>& d, int L, int B, bool split2, const WideLayout& lay, int ncu) {
+  int bm = 0, bn = 0;
+  wide_pred_tile(split2 ? 2 : 1, &bm, &bn);
+  auto tiles = [&](int l) { return ((d[l] + bm - 1) / bm) * (long long)((B + bn - 1) / bn); };
+  auto makespan = [&](int sl) {
+    std::priority_queue<double, std::vector<double>, std::greater<double>> cu;
+    for (int i = 0; i < ncu; ++i) cu.push(0.0);
+    auto run = [&](double cost) { const double t = cu.top() + cost; cu.pop(); cu.push(t); };
+    for (int l = 1; l < L; ++l)
+      for (long long t = 0; t < tiles(l); ++t) run((double)(lay.wh[l].ld / WIDE_BK));
+    const double c0 = (double)(lay.wh[0].ld / WIDE_BK) / sl + (sl > 1 ? 2.0 : 0.0);
+    for (long long t = 0; t < tiles(0) * sl; ++t) run(c0);
+    double end = 0.0;
+    while (!cu.empty()) { end = cu.top(); cu.pop(); }
+    return end + (sl > 1 ? 4.0 : 0.0);
+  };
+  int best = 1;
+  double best_t = makespan(1);
+  for (int sl = 2; sl <= lay.part_smax; sl *= 2) {
+    if (lay.wh[0].ld % (sl * WIDE_BK) != 0) continue;
+    const double t = makespan(sl);
+    if (t < best_t) { best = sl; best_t = t; }
+  }
+  return best;
+}
 
 bool narrow_outer(int B, int wmode) {
   return B <= NARROW_OUTER_MAX_B && (wmode == IPC_WMODE_OUTER || (wmode == IPC_WMODE_AUTO && B <= 16));
@@ -691,6 +742,7 @@ int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w
     auto buf = [&](const WideLayout::Buf& b) -> void* { return b.off < 0 ? nullptr : ws + b.off; };
     auto a16 = [](const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
     plan->wpred.clear(); plan->winfer.clear(); plan->wweight.clear(); plan->wsync.clear();
+    std::vector<WideProblem> pred_layer;
     for (int l = 0; l < L; ++l) {
       WideProblem q{};
       q.M = d[l]; q.N = B; q.K = (int)lay.wh[l].ld;
@@ -701,7 +753,33 @@ int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w
       q.h = buf(lay.e[l]); q.ldh = lay.e[l].ld;
       q.t = buf(lay.et[l]); q.ldt = lay.et[l].ld;
       q.vec = B % 4 == 0 && a16(e[l]) && a16(x[l]);
+      pred_layer.push_back(q);
+    }
+    int ncu = 0, dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
+      ncu = 256;
+    plan->pred_ksplit = wide_pred_ksplit(d, L, B, plan->split == IPC_SPLIT_W, lay, ncu);
+    if (plan->pred_ksplit > 1) {
+      // layer 0 last, as slices writing partial products; the reduce launch writes eps[0], E, ET
+      for (int l = 1; l < L; ++l) plan->wpred.push_back(pred_layer[l]);
+      WideProblem q = pred_layer[0];
+      q.ksplit = plan->pred_ksplit;
+      q.out = ws + lay.part_off; q.ldo = B;
+      q.part_stride = lay.part_stride;
+      q.aux = nullptr; q.h = nullptr; q.t = nullptr;
       plan->wpred.push_back(q);
+      WideReduce& r = plan->wreduce;
+      r = WideReduce{};
+      r.part = reinterpret_cast<const float*>(ws + lay.part_off); r.part_stride = lay.part_stride; r.ldp = B;
+      r.slices = plan->pred_ksplit; r.M = d[0]; r.N = B;
+      r.x = static_cast<const float*>(x[0]); r.ldx = B;
+      r.eps = static_cast<float*>(e[0]); r.lde = B;
+      r.h = buf(lay.e[0]); r.ldh = lay.e[0].ld;
+      r.t = buf(lay.et[0]); r.ldt = lay.et[0].ld;
+      r.vec = pred_layer[0].vec;
+    } else {
+      plan->wpred = pred_layer;
     }
     for (int l = 1; l < L; ++l) {
       WideProblem q{};
@@ -751,7 +829,7 @@ int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w
     plan->wsync_init.push_back(plan->wsync.back());                         // x[L] copies
     plan->wfwd.clear();
     for (int l = L - 1; l >= 1; --l) {
-      WideProblem q = plan->wpred[l];
+      WideProblem q = pred_layer[l];
       q.out = x[l]; q.ldo = B;
       q.aux = nullptr; q.ldx = 0;
       q.h = buf(lay.f[l]); q.ldh = lay.f[l].ld;
@@ -761,7 +839,7 @@ int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w
     }
     TRY(launch_rc(wide_prepare(), "wide path LDS limit"));
     auto chunks = [](int n) { return (n + WIDE_MAX_BATCH - 1) / WIDE_MAX_BATCH; };
-    plan->launches = 2 * chunks(L) + chunks(L - 1);
+    plan->launches = 2 * chunks(L) + chunks(L - 1) + (plan->pred_ksplit > 1 ? 1 : 0);
   }
   plan->bound = true;
   return ok();
@@ -775,8 +853,11 @@ int run_phase(ipc_plan* plan, int phase, hipStream_t s) {
   if (plan->wide) {
     switch (phase) {
       case IPC_PHASE_PRED:
-        return launch_rc(launch_wide(WIDE_PRED, plan->wpred.data(), (int)plan->wpred.size(), plan->operand,
-                                     plan->split == IPC_SPLIT_W ? 2 : 1, plan->act, s), "wide prediction phase");
+        TRY(launch_rc(launch_wide(WIDE_PRED, plan->wpred.data(), (int)plan->wpred.size(), plan->operand,
+                                  plan->split == IPC_SPLIT_W ? 2 : 1, plan->act, s), "wide prediction phase"));
+        if (plan->pred_ksplit > 1)
+          return launch_rc(launch_wide_reduce(plan->wreduce, plan->operand, s), "wide prediction reduce");
+        return ok();
       case IPC_PHASE_INFER:
         return launch_rc(launch_wide(WIDE_INFER, plan->winfer.data(), (int)plan->winfer.size(), plan->operand, 1,
                                      plan->act, s), "wide inference phase");

@@ -26,7 +26,11 @@
 //   * fragments of the next 16-k slice are read while the current slice's
 //     MFMAs run; split 2 adds the A_lo B products (error compensation);
 //   * workgroups are renumbered so that the tiles one XCD runs are consecutive
-//     (the tiles sharing rows of A share that XCD's L2).
+//     (the tiles sharing rows of A share that XCD's L2);
+//   * a k-split prediction problem (last in its launch) runs each tile as
+//     ksplit slices of the contraction that store raw fp32 partial products;
+//     their workgroups come after every whole tile's, so the slices fill the
+//     CUs that the last round of whole tiles leaves idle.
 //
 // Epilogue: the accumulator tile goes through LDS (the stages are free by
 // then) so that every global access is a coalesced row-major 4-column group;
@@ -117,6 +121,7 @@ struct Batch {
   WideProblem p[WIDE_MAX_BATCH];
   int start[WIDE_MAX_BATCH + 1];  // first tile of each problem
   int count;
+  int tail;                       // first k-split problem (count if none)
 };
 
 // ACT: the epilogue activation (WIDE_INFER, WIDE_FWD, S16_INFER) or the
@@ -142,16 +147,23 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
   static_assert(!BREG || S16, "register-path operands belong to the standalone kernels");
 
   // XCD-aware renumbering: workgroup b runs on XCD b % 8; give every XCD a
-  // contiguous range of tiles.
-  const int G = gridDim.x, b = blockIdx.x;
-  const int xcd = b & 7, per = G >> 3, rem = G & 7;
-  const int tile = xcd * per + (xcd < rem ? xcd : rem) + (b >> 3);
+  // contiguous range of tiles, first of the whole tiles, then (workgroups
+  // numbered after all whole tiles, so dispatched last) of the k-split slices.
+  const int b = blockIdx.x, n_whole = bt.start[bt.tail];
+  const int gb = b < n_whole ? b : b - n_whole, gG = b < n_whole ? n_whole : (int)gridDim.x - n_whole;
+  const int xcd = gb & 7, per = gG >> 3, rem = gG & 7;
+  const int tile = (b < n_whole ? 0 : n_whole) + xcd * per + (xcd < rem ? xcd : rem) + (gb >> 3);
   int pi = 0;
 #pragma unroll 1
   while (pi + 1 < bt.count && tile >= bt.start[pi + 1]) ++pi;
   const WideProblem& p = bt.p[pi];
   const int tn = (p.N + BN - 1) / BN;
-  const int local = tile - bt.start[pi];
+  // k-split prediction: the tile's slice of the contraction
+  const bool partial = MODE == WIDE_PRED && p.ksplit > 1;
+  const int tmn = ((p.M + BM - 1) / BM) * tn;
+  const int slice = partial ? (tile - bt.start[pi]) / tmn : 0;
+  const int local = tile - bt.start[pi] - slice * tmn;
+  const int kslice = partial ? p.K / p.ksplit : p.K;
   const int m0 = (local / tn) * BM, n0 = (local % tn) * BN;
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -161,11 +173,11 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
   const OT* Bg = reinterpret_cast<const OT*>(p.b);
   const long long lda = p.lda, ldb = p.ldb;
   const int alim = p.a_lim, blim = p.b_lim;
-  const int nk = p.K / WIDE_BK;
+  const int nk = kslice / WIDE_BK, kbase = slice * kslice;
 
   auto issue_dma = [&](int kt, int stage) {
     unsigned char* st = smem + stage * STAGE;
-    const int k0 = kt * WIDE_BK;
+    const int k0 = kbase + kt * WIDE_BK;
 #pragma unroll
     for (int q = 0; q < IA; ++q) {
       const int blk = q * NW + w;
@@ -193,7 +205,7 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
 #pragma unroll
       for (int i = 0; i < RB; ++i)
         breg[i] = *reinterpret_cast<const uint4*>(
-            slot_src<OT, BMN, BN>(Bg, ldb, n0, blim, kt * WIDE_BK, i * NT + tid));
+            slot_src<OT, BMN, BN>(Bg, ldb, n0, blim, kbase + kt * WIDE_BK, i * NT + tid));
     }
   };
   auto store_breg = [&](int stage) {
@@ -246,7 +258,7 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
   constexpr bool PRE = MODE != WIDE_FWD && MODE != S16_FWD;
   const bool pre_from_aux = MODE == WIDE_PRED || MODE == S16_PRED;
   float pre[PRE ? IT : 1][4];
-  if (PRE) {
+  if (PRE && !partial) {
 #pragma unroll
     for (int u = 0; u < IT; ++u)
       load_group(pre_from_aux ? p.aux : p.out, pre_from_aux ? p.ldx : p.ldo, u, pre[PRE ? u : 0]);
@@ -375,6 +387,22 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
   }
 
   // ------------------------------------------------------------ epilogue
+  if (partial) {
+    // raw partial product of this slice; lanes 0-31 of a row store 32
+    // consecutive columns
+    float* po = reinterpret_cast<float*>(p.out) + slice * p.part_stride;
+#pragma unroll
+    for (int i = 0; i < RM; ++i)
+#pragma unroll
+      for (int j = 0; j < RN; ++j)
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          const int m = m0 + wm * WTM + i * 32 + 8 * (q >> 2) + 4 * lk + (q & 3);
+          const int n = n0 + wn * WTN + j * 32 + lr;
+          if (m < M && n < N) po[(long long)m * p.ldo + n] = acc[i][j][q];
+        }
+    return;
+  }
   // The accumulator tile goes through LDS (the pipeline stages are free now)
   // so that every global access of the epilogue is coalesced: pass 1 walks
   // the tile row-major, 4 columns per thread (fp32 master, natural 16-bit
@@ -507,6 +535,7 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
 template <typename OT, int MODE, int SPLIT, int ACT, bool BREG, int BM, int BN, int S, int WGM, int WGN>
 struct Cfg {
   static constexpr int smem = smem_bytes(BM, BN, S, SPLIT == 2);
+  static constexpr int BM_ = BM, BN_ = BN;
   static const void* fn() {
     return reinterpret_cast<const void*>(&dma_gemm_kernel<OT, MODE, SPLIT, ACT, BREG, BM, BN, S, WGM, WGN>);
   }
@@ -519,11 +548,19 @@ struct Cfg {
     if (pe != hipSuccess) return pe;
     Batch bt;
     bt.count = count;
+    bt.tail = count;
     int total = 0;
     for (int i = 0; i < count; ++i) {
+      const int ks = MODE == WIDE_PRED && probs[i].ksplit > 1 ? probs[i].ksplit : 1;
+      if (ks > 1) {
+        if (probs[i].K % (ks * WIDE_BK) != 0) return hipErrorInvalidValue;
+        if (bt.tail == count) bt.tail = i;
+      } else if (bt.tail != count) {
+        return hipErrorInvalidValue;  // k-split problems must come last
+      }
       bt.p[i] = probs[i];
       bt.start[i] = total;
-      total += ((probs[i].M + BM - 1) / BM) * ((probs[i].N + BN - 1) / BN);
+      total += ((probs[i].M + BM - 1) / BM) * ((probs[i].N + BN - 1) / BN) * ks;
     }
     for (int i = count; i <= WIDE_MAX_BATCH; ++i) bt.start[i] = total;
     if (total == 0) return hipSuccess;

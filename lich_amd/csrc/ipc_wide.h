@@ -71,7 +71,31 @@ struct WideProblem {
   void* out2; long long ld2;       // infer, save mode: f(x_new) (fp32 for WIDE, 16-bit for S16), or null
   float scal;                      // infer: gamma, weight: alpha
   int vec;                         // 1: out/aux/out2 rows allow 4-element vector access, h/hl rows 8-byte aligned
+  // WIDE_PRED only: ksplit > 1 cuts the contraction into ksplit equal slices
+  // (K / ksplit a multiple of WIDE_BK); slice s stores its raw fp32 partial
+  // product at out + s * part_stride ([M][ldo]) and nothing else, and
+  // launch_wide_reduce finishes the epilogue.  Split problems come last in a
+  // launch: their tiles are dispatched after every whole tile, so they fill
+  // the launch's last round of CUs.
+  int ksplit;
+  long long part_stride;
 };
+
+// The epilogue of a k-split prediction: eps = x - sum of the slices (added in
+// slice order), written with its 16-bit copy E and transposed copy ET.
+struct WideReduce {
+  const float* part; long long part_stride; long long ldp;
+  int slices, M, N;
+  const float* x; long long ldx;
+  float* eps; long long lde;
+  void* h; long long ldh;
+  void* t; long long ldt;
+  int vec;  // 1: part, x and eps rows allow 4-element vector access
+};
+hipError_t launch_wide_reduce(const WideReduce& r, int operand, hipStream_t s);
+
+// Output tile of the prediction kernel for `split` (1 or 2).
+void wide_pred_tile(int split, int* bm, int* bn);
 
 // Launches one phase of the wide path over `count` layers (one launch per
 // WIDE_MAX_BATCH layers).  `operand` is DT_F16 or DT_BF16, `split` 1 or 2

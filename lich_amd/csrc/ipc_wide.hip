@@ -117,6 +117,117 @@ __global__ void __launch_bounds__(256) wide_copy_kernel(const WideCopyBatch cb) 
   }
 }
 
+// Epilogue of a k-split prediction, 64 x 64 block per workgroup: the slices'
+// partial products are added in slice order, then eps = x - sum and its
+// copies, with the rounding steps of the whole-tile prediction epilogue.  A
+// thread owns 4 columns of 4 rows (16 rows apart); the loads of all four rows
+// are issued before their sums, and the transposed copy goes through LDS so
+// that each thread stores 4 consecutive rows of one column at once.
+template <typename OT>
+__global__ void __launch_bounds__(256) wide_reduce_kernel(const WideReduce r) {
+  __shared__ float tile[CP_T][CP_T + 1];
+  const int tc = (r.N + CP_T - 1) / CP_T;
+  const int r0 = (blockIdx.x / tc) * CP_T, c0 = (blockIdx.x % tc) * CP_T;
+  const int cq = (threadIdx.x & 15) * 4, ty = threadIdx.x >> 4;
+  const int n = c0 + cq;
+  const int nv = n < r.N ? (r.N - n < 4 ? r.N - n : 4) : 0;
+  const bool vec = r.vec && nv == 4;
+  OT* h = reinterpret_cast<OT*>(r.h);
+  float a[4][4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int m = r0 + u * 16 + ty;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) a[u][j] = 0.0f;
+    if (m >= r.M || nv == 0) continue;
+    const float* src = r.part + (long long)m * r.ldp + n;
+    if (vec) {
+      const float4 t = *reinterpret_cast<const float4*>(src);
+      a[u][0] = t.x; a[u][1] = t.y; a[u][2] = t.z; a[u][3] = t.w;
+    } else {
+      for (int j = 0; j < nv; ++j) a[u][j] = src[j];
+    }
+  }
+#pragma unroll 2
+  for (int q = 1; q < r.slices; ++q) {
+    float b[4][4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int m = r0 + u * 16 + ty;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[u][j] = 0.0f;
+      if (m >= r.M || nv == 0) continue;
+      const float* src = r.part + q * r.part_stride + (long long)m * r.ldp + n;
+      if (vec) {
+        const float4 t = *reinterpret_cast<const float4*>(src);
+        b[u][0] = t.x; b[u][1] = t.y; b[u][2] = t.z; b[u][3] = t.w;
+      } else {
+        for (int j = 0; j < nv; ++j) b[u][j] = src[j];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) a[u][j] = a[u][j] + b[u][j];
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int rr = u * 16 + ty, m = r0 + rr;
+    float hv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (m < r.M && nv > 0) {
+#pragma clang fp contract(off)
+      const float* xs = r.x + (long long)m * r.ldx + n;
+      float* es = r.eps + (long long)m * r.lde + n;
+      OT* hs = h + (long long)m * r.ldh + n;
+      float v[4];
+      OT o[4];
+      if (vec) {
+        const float4 t = *reinterpret_cast<const float4*>(xs);
+        v[0] = t.x - a[u][0]; v[1] = t.y - a[u][1]; v[2] = t.z - a[u][2]; v[3] = t.w - a[u][3];
+        *reinterpret_cast<float4*>(es) = make_float4(v[0], v[1], v[2], v[3]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = cvt<OT>(v[j]);
+        uint2 pk;
+        pk.x = dma::pack2(o[0], o[1]);
+        pk.y = dma::pack2(o[2], o[3]);
+        *reinterpret_cast<uint2*>(hs) = pk;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) hv[j] = to_f32(o[j]);
+      } else {
+        for (int j = 0; j < nv; ++j) {
+          v[j] = xs[j] - a[u][j];
+          es[j] = v[j];
+          o[j] = cvt<OT>(v[j]);
+          hs[j] = o[j];
+          hv[j] = to_f32(o[j]);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) tile[rr][cq + j] = hv[j];
+  }
+  if (!r.t) return;
+  __syncthreads();
+  OT* t = reinterpret_cast<OT*>(r.t);
+  // 64 columns x 16 groups of 4 rows: one 8-byte store of 4 consecutive rows
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int idx = it * 256 + threadIdx.x;
+    const int cc = idx >> 4, mg = (idx & 15) * 4;
+    const int nn = c0 + cc, m = r0 + mg;
+    if (nn >= r.N || m >= r.M) continue;
+    OT* dst = t + (long long)nn * r.ldt + m;
+    if (m + 4 <= r.M) {
+      uint2 pk;
+      pk.x = dma::pack2(cvt<OT>(tile[mg][cc]), cvt<OT>(tile[mg + 1][cc]));
+      pk.y = dma::pack2(cvt<OT>(tile[mg + 2][cc]), cvt<OT>(tile[mg + 3][cc]));
+      *reinterpret_cast<uint2*>(dst) = pk;
+    } else {
+      for (int j = 0; m + j < r.M; ++j) dst[j] = cvt<OT>(tile[mg + j][cc]);
+    }
+  }
+}
+
 template <typename OT>
 hipError_t launch_phase(int mode, const WideProblem* probs, int count, int split, int act, hipStream_t s) {
   return dma::by_act<Phase<OT>::template Run>(act, mode, split, probs, count, s);
@@ -141,6 +252,28 @@ hipError_t launch_wide(int mode, const WideProblem* probs, int count, int operan
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
+}
+
+hipError_t launch_wide_reduce(const WideReduce& r, int operand, hipStream_t s) {
+  if (r.slices < 1 || r.M <= 0 || r.N <= 0) return hipErrorInvalidValue;
+  const dim3 grid(((r.M + CP_T - 1) / CP_T) * ((r.N + CP_T - 1) / CP_T));
+  if (operand == DT_F16)
+    hipLaunchKernelGGL(wide_reduce_kernel<f16>, grid, dim3(256), 0, s, r);
+  else if (operand == DT_BF16)
+    hipLaunchKernelGGL(wide_reduce_kernel<bf16>, grid, dim3(256), 0, s, r);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+void wide_pred_tile(int split, int* bm, int* bn) {
+  if (split == 2) {
+    *bm = PredCfg2<bf16, 0>::BM_;
+    *bn = PredCfg2<bf16, 0>::BN_;
+  } else {
+    *bm = PredCfg1<bf16, 0>::BM_;
+    *bn = PredCfg1<bf16, 0>::BN_;
+  }
 }
 
 hipError_t launch_wide_copy(const WideCopy* copies, int count, int operand, hipStream_t s) {

@@ -141,7 +141,8 @@ def _wide_layout_bytes(dims, B, split2):
     """The wide path's workspace layout restated: 256 bytes, then one 256-byte
     aligned 16-bit buffer per operand copy, rows and columns padded to 64:
     W hi [and lo] and its transpose (for l < L-1), f(x[l]) and its transpose
-    for l = 1..L, eps[l] for l < L and its transpose for l < L-1."""
+    for l = 1..L, eps[l] for l < L and its transpose for l < L-1, then the
+    partial products of a k-split prediction of layer 0."""
     pad = lambda v, m: (v + m - 1) // m * m  # noqa: E731
     L = len(dims) - 1
     total = 256
@@ -163,6 +164,15 @@ def _wide_layout_bytes(dims, B, split2):
         add(dims[l], B)
         if l <= L - 2:
             add(B, dims[l])
+    # fp32 partial products of a k-split layer-0 prediction: as many [d_0][B]
+    # slices as keep all of layer 0's prediction tiles within 512 slices and
+    # each slice a multiple of 64 long (at most 16)
+    bm, bn = (128, 128) if split2 else (256, 128)
+    t0 = -(-dims[0] // bm) * -(-B // bn)
+    for sl in (16, 8, 4, 2):
+        if sl * t0 <= 512 and pad(dims[1], 64) % (sl * 64) == 0:
+            total += pad(sl * dims[0] * B * 4, 256)
+            break
     return total
 
 
