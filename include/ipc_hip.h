@@ -214,7 +214,8 @@ int ipc_plan_path(const ipc_plan* plan);
  * double-buffered eps / W^T eps exchange and the top chunks' cached 16-bit
  * copies of f(x[L]) after those.  The wide path keeps its
  * 16-bit operand copies there (W as hi and lo terms, W^T, f(x) and eps in
- * both layouts, zero padded); their padding must stay zero. */
+ * both layouts, zero padded; their padding must stay zero), then the fp32
+ * partial products of a k-split output-layer prediction. */
 long long ipc_plan_workspace_bytes(const ipc_plan* plan);
 
 /* Binds the caller's buffers: x and e hold L+1 pointers ([d_l, B] each; e[L]
