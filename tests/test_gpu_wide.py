@@ -102,11 +102,13 @@ def test_wide_equals_phased_path(case):
     assert s <= 1e-5 and w <= 1e-5 and e <= 1e-4 and dw <= 1e-4
 
 
-def test_wide_k_split_prediction():
-    """Layer 0 (999 rows, K = 4096) after 256 tiles of layer 1 (K = 512): the
-    plan cuts layer 0's prediction tiles into k-slices that fill the CUs left
-    idle by the last round of whole tiles, and a fourth launch adds the slices'
-    partial products (ragged: M = 999 and B = 1000 end inside a tile).
+@pytest.mark.parametrize("op,split", [(BF16, 2), (F16, 1)], ids=["bf16-s2", "f16-s1"])
+def test_wide_k_split_prediction(op, split):
+    """Layer 0 (999 rows, K = 4096) after the whole tiles of layer 1 (K = 512):
+    the plan cuts layer 0's prediction tiles into k-slices that fill the CUs
+    left idle by the whole tiles, and a fourth launch adds the slices' partial
+    products (ragged: M = 999 and B = 1000 end inside a tile), for both
+    prediction tile configurations (split 2: 128 x 128, split 1: 256 x 128).
 
     The first step's prediction sees the same operands on both paths, so its
     eps[0] differs from the unsplit phased path only by the fp32 summation
@@ -114,12 +116,12 @@ def test_wide_k_split_prediction():
     copies (an element on a rounding boundary moves by one 16-bit ulp), so
     from there on the paths are compared through their distance to the
     oracle, which the split must not increase."""
-    dims, B, act, op, T = (999, 4096, 512), 1000, "tanh", BF16, 4
-    report("wide-k-split", dims=dims, B=B)
+    dims, B, act, T = (999, 4096, 512), 1000, "tanh", 4
+    report("wide-k-split", dims=dims, B=B, op=op, split=split)
     w0, x_in, y = _setup(dims, B, seed=11, input_dist="normal")
     _x0, x_t, w_t, _e = _oracle_run(w0, x_in, y, act, T)
-    m = _model(dims, B, act, op, "wide", w0, x_in, y, 1, pred_split=2)
-    ph = _model(dims, B, act, op, "phased", w0, x_in, y, 1, pred_split=2)
+    m = _model(dims, B, act, op, "wide", w0, x_in, y, 1, pred_split=split)
+    ph = _model(dims, B, act, op, "phased", w0, x_in, y, 1, pred_split=split)
     assert m.path == "wide" and m.launches_per_step() == 4
     e1 = O.global_rel_err([m.e[0]], [ph.e[0]])
     for mod in (m, ph):
@@ -127,10 +129,10 @@ def test_wide_k_split_prediction():
     torch.cuda.synchronize()
     s_err, dw_err = _errors(m, w0, x_t, w_t)
     s_ph, dw_ph = _errors(ph, w0, x_t, w_t)
-    x_m, w_m = _model_run(dims, w0, x_in, y, act, T, op, 2)
+    x_m, w_m = _model_run(dims, w0, x_in, y, act, T, op, split)
     s_m, dw_m = _errors(m, w0, x_m, w_m)
-    print(f"wide k-split: step-1 eps[0] vs phased {e1:.2e} | oracle state={s_err:.3e} dW={dw_err:.3e} "
-          f"(phased {s_ph:.3e} {dw_ph:.3e}) | model state={s_m:.3e} dW={dw_m:.3e}")
+    print(f"wide k-split {op} split {split}: step-1 eps[0] vs phased {e1:.2e} | oracle state={s_err:.3e} "
+          f"dW={dw_err:.3e} (phased {s_ph:.3e} {dw_ph:.3e}) | model state={s_m:.3e} dW={dw_m:.3e}")
     assert e1 <= 1e-5
     assert s_err <= 2e-2 and dw_err <= 5e-3
     assert s_err <= 1.1 * s_ph + 1e-4 and dw_err <= 1.1 * dw_ph + 1e-4
