@@ -16,7 +16,7 @@ The same run also reports
 * the CPU baseline: the oracle's fp32 step on this host's cores.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-wide] [--no-cpu]
-       python bench.py --wide-only | --sweep | --copy-calibration
+       python bench.py --wide-only | --sweep | --small-batch | --copy-calibration
 """
 from __future__ import annotations
 
@@ -323,6 +323,9 @@ def main() -> int:
     ap.add_argument("--sweep", action="store_true",
                     help="run only the per-kernel roofline sweep (M=K in {1024,4096,8192}, "
                          "B in {256,2048,8192}, bf16) and print it as one JSON line")
+    ap.add_argument("--small-batch", action="store_true",
+                    help="run only the small-batch online configuration (10, 64^4, 784), fp32, tanh, T=8, "
+                         "B in {1,4,8}, next to the oracle's fp32 step on the host cores, as one JSON line")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain device copy of a known size (the reference point that scales the "
                          "FETCH_SIZE / WRITE_SIZE counters of a rocprofv3 --pmc run to bytes)")
@@ -331,6 +334,33 @@ def main() -> int:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
               "(this build has no multi-GPU path)", file=sys.stderr)
         return 2
+    if args.small_batch:
+        import torch
+
+        dims, T = (10,) + (64,) * 4 + (784,), 8
+        rows = []
+        threads = torch.get_num_threads()
+        for B in (1, 4, 8):
+            model, x, y = make_model(dims, B, "tanh", torch.float32, seed=B)
+            el, done, replay_us = run_steady(model, x, y, T, 800, 40000)
+            # the oracle on all host cores and on one (these matrices are small enough for
+            # thread start-up to dominate); the faster of the two is the baseline
+            cpu = [cpu_baseline(dims, B, "tanh", n, warmup=20, steps=400, repeats=5) + (n,) for n in (threads, 1)]
+            cpu_val, cpu_step, cpu_cores = max(cpu)
+            gpu_val = done * B / el
+            rows.append({"B": B, "path": model.path, "launches_per_step": model.launches_per_step(),
+                         "us_per_step": round(el * 1e6 / done, 3), "us_per_replay": round(replay_us, 2),
+                         "samples_per_s": round(gpu_val, 1), "cpu_samples_per_s": round(cpu_val, 1),
+                         "cpu_us_per_step": round(cpu_step * 1e6, 2), "cpu_cores": cpu_cores,
+                         "cpu_samples_per_s_by_cores": {str(n): round(v, 1) for v, _s, n in cpu},
+                         "gpu_over_cpu": round(gpu_val / cpu_val, 2)})
+            del model
+        print(json.dumps({"small_batch": {
+            "workload": "small-batch online iPC MLP dims (10, 64x4, 784), fp32, tanh, T=8 steps per graph replay, "
+                        "rank-B outer-product weight update",
+            "data": "synthetic (seeded U[0,1] inputs, uniform labels, Xavier W)",
+            "cpu_kind": "port (oracle fp32 step on the host cores)", "rows": rows}}), flush=True)
+        return 0
     if args.copy_calibration:
         import torch
 
