@@ -311,12 +311,41 @@ def wide_config(T):
     return wide
 
 
+def small_batch_config():
+    """The small-batch online configuration (10, 64^4, 784), fp32, tanh, T=8,
+    B in {1, 4, 8}, next to the oracle's fp32 step on the host cores."""
+    import torch
+
+    dims, T = (10,) + (64,) * 4 + (784,), 8
+    rows = []
+    threads = torch.get_num_threads()
+    for B in (1, 4, 8):
+        model, x, y = make_model(dims, B, "tanh", torch.float32, seed=B)
+        el, done, replay_us = run_steady(model, x, y, T, 800, 40000)
+        # the oracle on all host cores and on one (these matrices are small enough for
+        # thread start-up to dominate); the faster of the two is the baseline
+        cpu = [cpu_baseline(dims, B, "tanh", n, warmup=20, steps=400, repeats=5) + (n,) for n in (threads, 1)]
+        cpu_val, cpu_step, cpu_cores = max(cpu)
+        gpu_val = done * B / el
+        rows.append({"B": B, "path": model.path, "launches_per_step": model.launches_per_step(),
+                     "us_per_step": round(el * 1e6 / done, 3), "us_per_replay": round(replay_us, 2),
+                     "samples_per_s": round(gpu_val, 1), "cpu_samples_per_s": round(cpu_val, 1),
+                     "cpu_us_per_step": round(cpu_step * 1e6, 2), "cpu_cores": cpu_cores,
+                     "cpu_samples_per_s_by_cores": {str(n): round(v, 1) for v, _s, n in cpu},
+                     "gpu_over_cpu": round(gpu_val / cpu_val, 2)})
+        del model
+    return {"workload": "small-batch online iPC MLP dims (10, 64x4, 784), fp32, tanh, T=8 steps per graph replay, "
+                        "rank-B outer-product weight update",
+            "data": "synthetic (seeded U[0,1] inputs, uniform labels, Xavier W)",
+            "cpu_kind": "port (oracle fp32 step on the host cores)", "rows": rows}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20000)
     ap.add_argument("--warmup", type=int, default=400)
-    ap.add_argument("--no-wide", action="store_true")
+    ap.add_argument("--no-wide", action="store_true", help="skip the wide and small-batch configurations")
     ap.add_argument("--wide-only", action="store_true",
                     help="run only the wide configuration and print its JSON object")
     ap.add_argument("--no-cpu", action="store_true")
@@ -335,31 +364,7 @@ def main() -> int:
               "(this build has no multi-GPU path)", file=sys.stderr)
         return 2
     if args.small_batch:
-        import torch
-
-        dims, T = (10,) + (64,) * 4 + (784,), 8
-        rows = []
-        threads = torch.get_num_threads()
-        for B in (1, 4, 8):
-            model, x, y = make_model(dims, B, "tanh", torch.float32, seed=B)
-            el, done, replay_us = run_steady(model, x, y, T, 800, 40000)
-            # the oracle on all host cores and on one (these matrices are small enough for
-            # thread start-up to dominate); the faster of the two is the baseline
-            cpu = [cpu_baseline(dims, B, "tanh", n, warmup=20, steps=400, repeats=5) + (n,) for n in (threads, 1)]
-            cpu_val, cpu_step, cpu_cores = max(cpu)
-            gpu_val = done * B / el
-            rows.append({"B": B, "path": model.path, "launches_per_step": model.launches_per_step(),
-                         "us_per_step": round(el * 1e6 / done, 3), "us_per_replay": round(replay_us, 2),
-                         "samples_per_s": round(gpu_val, 1), "cpu_samples_per_s": round(cpu_val, 1),
-                         "cpu_us_per_step": round(cpu_step * 1e6, 2), "cpu_cores": cpu_cores,
-                         "cpu_samples_per_s_by_cores": {str(n): round(v, 1) for v, _s, n in cpu},
-                         "gpu_over_cpu": round(gpu_val / cpu_val, 2)})
-            del model
-        print(json.dumps({"small_batch": {
-            "workload": "small-batch online iPC MLP dims (10, 64x4, 784), fp32, tanh, T=8 steps per graph replay, "
-                        "rank-B outer-product weight update",
-            "data": "synthetic (seeded U[0,1] inputs, uniform labels, Xavier W)",
-            "cpu_kind": "port (oracle fp32 step on the host cores)", "rows": rows}}), flush=True)
+        print(json.dumps({"small_batch": small_batch_config()}), flush=True)
         return 0
     if args.copy_calibration:
         import torch
@@ -430,6 +435,8 @@ def main() -> int:
     del pmodel
 
     wide = None if args.no_wide else wide_config(T)
+    # the small-batch configuration times the host oracle as well: skipped with --no-cpu
+    small = None if args.no_wide or args.no_cpu else small_batch_config()
 
     cpu = None
     if not args.no_cpu:
@@ -450,7 +457,7 @@ def main() -> int:
                                "T=4 steps per hipGraph replay, fp32 master x/eps/W, fp16 operands, fp32 accumulate",
                    "global_batch": B, "seq_len": None, "parallelism": "single GPU",
                    "fused_whole_step_kernel": model.fused, "path": model.path, "phases": phases},
-        "roofline": roofline, "cpu_baseline": cpu, "wide": wide,
+        "roofline": roofline, "cpu_baseline": cpu, "wide": wide, "small_batch": small,
     }
     print(json.dumps(line), flush=True)
     return 0
