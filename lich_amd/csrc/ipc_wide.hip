@@ -13,11 +13,12 @@ using dma::Cfg;
 #ifndef WIDE_PRED1_CFG
 #define WIDE_PRED1_CFG 256, 128, 3, 4, 2
 #endif
-// split-2 prediction: 128 x 128 tiles (3 stages in 144 KiB of LDS).  The wide
-// configuration's 256 x 128 tiles came to 544 for 256 CUs (three rounds, the last
-// one 1/8 full); 1,088 half-size tiles fill 4.25 rounds: 341 us instead of 377 us.
+// split-2 prediction: 128 x 256 tiles, waves 2 x 4, 2 stages (128 KiB of LDS); the
+// k-split of the output layer fills the last round.  Measured on the wide
+// configuration: 281 us per prediction against 317 us on 128 x 128 tiles (3 stages)
+// and 349 us on 256 x 128 tiles (2 stages, all of the LDS).
 #ifndef WIDE_PRED2_CFG
-#define WIDE_PRED2_CFG 128, 128, 3, 4, 2
+#define WIDE_PRED2_CFG 128, 256, 2, 2, 4
 #endif
 // inference and weight update: 128 x 256 tiles, waves 2 x 4 (64 x 64 each, as in
 // 256 x 128 / 4 x 2).  Measured on the wide configuration: inference 183 -> 177 us,

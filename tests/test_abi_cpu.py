@@ -167,7 +167,7 @@ def _wide_layout_bytes(dims, B, split2):
     # fp32 partial products of a k-split layer-0 prediction: as many [d_0][B]
     # slices as keep all of layer 0's prediction tiles within 512 slices and
     # each slice a multiple of 64 long (at most 16)
-    bm, bn = (128, 128) if split2 else (256, 128)
+    bm, bn = (128, 256) if split2 else (256, 128)
     t0 = -(-dims[0] // bm) * -(-B // bn)
     for sl in (16, 8, 4, 2):
         if sl * t0 <= 512 and pad(dims[1], 64) % (sl * 64) == 0:
