@@ -3,7 +3,9 @@
 Workload (the headline metric's configuration): the paper efficiency profile
 at depth 6, dims (10, 64 x 6, 784), batch 128, tanh, alpha=1e-4, gamma=0.5,
 fp32 master states/weights with fp16 GEMM operands and fp32 accumulation,
-T=4 steps captured in one hipGraph.  A "step" is one iPC step (prediction
+T=4 steps captured for replay (``prepare_steady_state(use_graph=True)``: for
+this plan the T steps are one launch of the layer-resident whole-step kernel,
+which the capture records and each replay relaunches).  A "step" is one iPC step (prediction
 errors, inference updates, weight updates) over the batch; ``value`` is
 batch * steps / elapsed with inputs resident in HBM.
 
@@ -32,13 +34,18 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 METRIC = "iPC train samples/sec (L=6,h=64,B=128); fused-GEMM TFLOP/s vs MFMA peak"
-# HBM bytes that one launch of the dominant kernel moves, measured with
-# rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes (one counter per pass) over
-# `bench.py --no-cpu --no-wide`, each scaled by the same counter's reading for
-# a plain device copy of known size (`bench.py --copy-calibration`: FETCH_SIZE
-# x 2.0, WRITE_SIZE x 1.0).  Keyed by kernel; re-measure after a kernel change.
-MEASURED_TRAFFIC = {"layer-resident whole-step kernel, 4 steps per launch": 4_320_896 + 3_374_720,
-                    "whole-step kernel, 4 steps per launch": 13_065_152 + 3_926_848}
+# HBM bytes that one launch of the dominant kernel moved in an earlier
+# profiling pass (not measured by this run): rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE passes (one counter per pass) over `bench.py --no-cpu --no-wide`,
+# each scaled by the same counter's reading for a plain device copy of known
+# size (`bench.py --copy-calibration`: FETCH_SIZE x 2.0, WRITE_SIZE x 1.0).
+# Keyed by kernel, with the profile summary that records the pass.
+MEASURED_TRAFFIC = {
+    "layer-resident whole-step kernel, 4 steps per launch":
+        (4_320_896 + 3_374_720, "profiles/resident_whole_step_d6_h64_B128.md"),
+    "whole-step kernel, 4 steps per launch":
+        (13_065_152 + 3_926_848, "profiles/narrow_whole_step_d6_h64_B128.md"),
+}
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0  # dense, no sparsity
 FP16_PEAK_TFLOPS = 2500.0
@@ -46,6 +53,34 @@ FP16_PEAK_TFLOPS = 2500.0
 
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
+
+
+def step_bytes(dims, B, s=4):
+    """Algorithmic HBM bytes of one iPC step at storage size s: W read and
+    written, hidden states read and written, target and input read
+    (s * [2S + 2 sum_hidden d B + (d_0 + d_L) B]); eps stays on chip."""
+    L = len(dims) - 1
+    S = sum(dims[l] * dims[l + 1] for l in range(L))
+    hidden = sum(dims[l] for l in range(1, L))
+    return s * (2 * S + 2 * hidden * B + (dims[0] + dims[L]) * B)
+
+
+def host_cpu():
+    """CPU model and core counts of this host."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        avail = os.cpu_count()
+    return {"cpu_model": model, "host_logical_cpus": os.cpu_count(), "cpus_available_to_process": avail}
 
 
 def phase_bytes_flops(dims, B, s=4):
@@ -136,24 +171,24 @@ def time_step_launch(model, T, reps=50, replays=5):
 
 
 def run_steady(model, x, y, T, warmup_steps, steps):
-    """Replays a hipGraph of T steps; returns (wall seconds, steps done, GPU
+    """Replays the captured T steps (prepare_steady_state with use_graph=True); returns (wall seconds, steps done, GPU
     microseconds per replay from HIP events on the replay stream)."""
     import torch
 
     assert model.prepare_steady_state(x, y, steps=T, use_graph=True)
-    for _ in range(max(1, warmup_steps // T)):
-        model._steady_state_runner.replay()
+    runner = model._steady_state_runner
+    runner.replay(max(1, warmup_steps // T))
     torch.cuda.synchronize()
     replays = steps // T
     stream = torch.cuda.current_stream()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     start.record(stream)
-    for _ in range(replays):
-        model._steady_state_runner.replay()
+    runner.replay(replays)  # the replays, enqueued by one library call
     end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    model.check_steps()  # raises if a whole-step launch gave up a wait (outside the timed region)
     return wall, replays * T, start.elapsed_time(end) * 1e3 / replays
 
 
@@ -407,7 +442,7 @@ def main() -> int:
         f"{model.launches_per_step()} launch(es) per step call, {replay_us:.2f} us per {T}-step replay")
 
     bf = phase_bytes_flops(dims, B)
-    step_bytes = sum(v[0] for v in bf.values())
+    per_step_bytes = step_bytes(dims, B, s=4)
     step_flops = sum(v[1] for v in bf.values())
     # per-phase kernel durations on a fresh model (the timing loops disturb state)
     pmodel, px, py = make_model(dims, B, "tanh", torch.float16, seed=1)
@@ -421,16 +456,21 @@ def main() -> int:
         launch_us = time_step_launch(pmodel, T)
         name = "layer-resident whole-step kernel" if model.path == "resident" else "whole-step kernel"
         kernel = f"{name}, {T} steps per launch"
-        launch_bytes, launch_flops = T * step_bytes, T * step_flops
+        launch_bytes, launch_flops = T * per_step_bytes, T * step_flops
     else:
         dom = max(phase_us, key=phase_us.get)
         launch_us = phase_us[dom]
         kernel = f"{dom} phase"
         launch_bytes, launch_flops = bf[dom]
     achieved = launch_bytes / (launch_us * 1e-6) / 1e9
+    traffic, traffic_src = MEASURED_TRAFFIC.get(kernel, (None, None))
     roofline = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": MEASURED_TRAFFIC.get(kernel), "kernel": kernel,
-                "algorithmic_bytes_per_launch": launch_bytes, "avg_launch_us": round(launch_us, 3),
+                "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": traffic, "kernel": kernel,
+                "traffic_source": f"earlier rocprofv3 --pmc pass, {traffic_src}" if traffic_src else None,
+                "algorithmic_bytes_per_launch": launch_bytes,
+                "algorithmic_bytes_rule": f"{per_step_bytes} B per step (storage s=4: 2S + 2 sum_hidden d B + "
+                                          f"(d_0+d_L) B) x {T if model.fused else 1} steps per launch",
+                "avg_launch_us": round(launch_us, 3),
                 "achieved_tflops": round(launch_flops / (launch_us * 1e-6) / 1e12, 4)}
     del pmodel
 
@@ -443,7 +483,7 @@ def main() -> int:
         threads = torch.get_num_threads()
         cpu_val, cpu_step = cpu_baseline(dims, B, "tanh", threads)
         cpu1_val, _ = cpu_baseline(dims, B, "tanh", 1, warmup=10, steps=100, repeats=3)
-        cpu = {"value": round(cpu_val, 1), "unit": "samples/s", "cores": threads, "kind": "port",
+        cpu = {"value": round(cpu_val, 1), "unit": "samples/s", "cores": threads, "kind": "port", **host_cpu(),
                "sample": f"oracle fp32 step, same dims/B/tanh, 20 warm-up + 5x200 timed steps, median "
                          f"({cpu_step * 1e3:.3f} ms/step); 1 thread: {cpu1_val:.1f} samples/s",
                "gpu_over_cpu": round(value / cpu_val, 2)}
@@ -454,7 +494,8 @@ def main() -> int:
         "warmup": warmup, "ms_per_step": round(ms_per_step, 6), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f16", "data": "synthetic (seeded U[0,1] inputs, uniform labels, Xavier W)",
         "config": {"workload": "paper profile depth 6: dims (10,64x6,784), B=128, tanh, alpha=1e-4, gamma=0.5, "
-                               "T=4 steps per hipGraph replay, fp32 master x/eps/W, fp16 operands, fp32 accumulate",
+                               "T=4 steps per replay of the captured steps (one whole-step kernel launch), fp32 master x/eps/W, "
+                               "fp16 operands, fp32 accumulate",
                    "global_batch": B, "seq_len": None, "parallelism": "single GPU",
                    "fused_whole_step_kernel": model.fused, "path": model.path, "phases": phases},
         "roofline": roofline, "cpu_baseline": cpu, "wide": wide, "small_batch": small,

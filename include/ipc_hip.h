@@ -13,7 +13,8 @@
  *   contiguous [groups, rows, cols] tensors.
  *
  * Ownership: the caller owns every buffer.  Kernels mutate their outputs in
- * place, allocate nothing and never synchronise the stream.  Every call is
+ * place, allocate nothing and never synchronise the stream (ipc_plan_check
+ * is the one entry point that synchronises).  Every call is
  * enqueued on the hipStream_t passed as `stream` (NULL = the null stream), so
  * calls can be captured into a hipGraph.
  *
@@ -28,7 +29,7 @@
 extern "C" {
 #endif
 
-#define IPC_ABI_VERSION 4
+#define IPC_ABI_VERSION 5
 
 /* status codes */
 #define IPC_OK 0
@@ -41,6 +42,8 @@ extern "C" {
 #define IPC_ERR_LAUNCH (-7)   /* the HIP launch failed                        */
 #define IPC_ERR_CONFIG (-8)   /* unknown tile config or plan option           */
 #define IPC_ERR_STATE (-9)    /* plan used before its buffers were bound      */
+#define IPC_ERR_TIMEOUT (-10) /* a whole-step kernel's wait ran past its spin
+                                 limit: that launch's outputs are invalid     */
 
 /* element types (storage and GEMM operand) */
 #define IPC_DT_F32 0
@@ -261,6 +264,57 @@ int ipc_plan_set_tiles(ipc_plan* plan, int tile_pred, int tile_infer, int tile_w
 
 /* Kernel launches one ipc_plan_step(steps=1) enqueues. */
 int ipc_plan_launch_count(const ipc_plan* plan);
+
+/*
+ * Health of the whole-step kernels.  Their workgroups wait for each other
+ * (grid barriers, per-workgroup step flags), which needs every workgroup of a
+ * launch running at once: ipc_plan_create takes the co-resident capacity of
+ * the device into account (an AUTO plan falls back from the layer-resident to
+ * the column kernel, an explicit IPC_PATH_RESIDENT plan fails with
+ * IPC_ERR_CONFIG, the column kernel's grid is capped), but a kernel on
+ * another stream or in another process can still hold CUs the launch needs.
+ * Every wait is therefore bounded: after `spin limit` polls it gives up, sets
+ * word 2 of the workspace (non-zero word 2 = the outputs of the steps since it
+ * was last cleared are invalid) and the kernel runs to its end.
+ *
+ * ipc_plan_check synchronises `stream`, then returns IPC_ERR_TIMEOUT (and
+ * clears word 2) if a wait gave up since the last check, IPC_OK otherwise;
+ * for plans without a whole-step kernel it only synchronises.  This is
+ * TileLangIPC's own addition: the reference's per-layer launches never wait
+ * for each other.
+ *
+ * ipc_plan_set_spin_limit sets the polls per wait (< 0: the default,
+ * 4194304 polls of ~64 clocks); 0 gives up at the first unsatisfied poll,
+ * which lets a host test force the timeout path while every kernel still
+ * exits normally.
+ */
+int ipc_plan_check(ipc_plan* plan, void* stream);
+int ipc_plan_set_spin_limit(ipc_plan* plan, int limit);
+
+/*
+ * Captured steps: the native counterpart of IPCGraphRunner
+ * (cuda_graph.py:6-36) and of the steady-state graph of
+ * TileLangIPC.prepare_steady_state / run_prepared_steady_state
+ * (trainer.py:693-781).  ipc_plan_graph_capture records `steps` steps of the
+ * bound plan (what ipc_plan_step(plan, steps, ...) enqueues) into a hipGraph
+ * on a private stream of default priority and instantiates it; it enqueues
+ * no work.  ipc_plan_graph_launch replays it `repeats` times on `stream` (any
+ * stream, the null stream included) with one hipGraphLaunch each.  A plan
+ * whose `steps` steps are one launch of a whole-step kernel records that
+ * launch instead and replays it directly: a one-node graph would run the same
+ * kernel with the same arguments, after ~5 us more of graph-launch overhead
+ * per replay on MI355X.
+ * ipc_plan_bind discards the graph (it holds the previous buffers' addresses);
+ * ipc_plan_graph_steps reports the captured step count (0: none).
+ */
+int ipc_plan_graph_capture(ipc_plan* plan, int steps);
+int ipc_plan_graph_launch(ipc_plan* plan, int repeats, void* stream);
+int ipc_plan_graph_steps(const ipc_plan* plan);
+
+/* Test hook: > 0 replaces the device's co-resident workgroup capacity in the
+ * checks of ipc_plan_create (a compute-partitioned device can be modelled
+ * without one); 0 restores the device query.  Not thread-safe. */
+int ipc_set_coresident_limit(int blocks);
 
 void ipc_plan_destroy(ipc_plan* plan);
 

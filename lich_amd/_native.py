@@ -17,8 +17,8 @@ LIB_PATH = Path(__file__).resolve().parent / "libipc_hip.so"
 
 # status codes (include/ipc_hip.h)
 IPC_OK = 0
-ERR_NULL, ERR_SHAPE, ERR_DTYPE, ERR_ACT, ERR_ALIGN, ERR_DEVICE, ERR_LAUNCH, ERR_CONFIG, ERR_STATE = (
-    -1, -2, -3, -4, -5, -6, -7, -8, -9)
+ERR_NULL, ERR_SHAPE, ERR_DTYPE, ERR_ACT, ERR_ALIGN, ERR_DEVICE, ERR_LAUNCH, ERR_CONFIG, ERR_STATE, ERR_TIMEOUT = (
+    -1, -2, -3, -4, -5, -6, -7, -8, -9, -10)
 
 DT_F32, DT_F16, DT_BF16 = 0, 1, 2
 ACT_CODES = {"identity": 0, "linear": 0, "relu": 1, "tanh": 2, "sigmoid": 3, "silu": 4, "gelu": 5}
@@ -87,6 +87,12 @@ def _declare(lib):
         "ipc_plan_sync": ([vp, vp], i),
         "ipc_plan_phase": ([vp, i, i, vp], i),
         "ipc_plan_launch_count": ([vp], i),
+        "ipc_plan_check": ([vp, vp], i),
+        "ipc_plan_set_spin_limit": ([vp, i], i),
+        "ipc_set_coresident_limit": ([i], i),
+        "ipc_plan_graph_capture": ([vp, i], i),
+        "ipc_plan_graph_launch": ([vp, i, vp], i),
+        "ipc_plan_graph_steps": ([vp], i),
         "ipc_plan_destroy": ([vp], None),
     }
     for name, (args, res) in sig.items():

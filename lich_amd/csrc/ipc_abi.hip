@@ -3,7 +3,8 @@
 // Every entry point validates its arguments on the host before any HIP call
 // (so the error paths are testable without a GPU), converts them to
 // GemmProblem / OuterProblem records and enqueues on the caller's stream.
-// No entry point allocates device memory or synchronises.
+// No entry point allocates device memory; only ipc_plan_check synchronises
+// (it reads the whole-step kernels' timeout word).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -419,11 +420,54 @@ struct ipc_plan {
   WideReduce wreduce{};                                   // its epilogue
   std::vector<WideCopy> wsync, wsync_init;               // wsync_init: W and x[L] only
   long long ws_bytes = 0;
+  void* workspace = nullptr;
+  // whole-step kernels: polls before a wait gives up (and raises the timeout
+  // word), and the most workgroups of the column kernel that can run at once
+  int spin_limit = 0;
+  int narrow_cap = 256;
+  // captured steps (ipc_plan_graph_capture): the graph, its executable and
+  // the private stream it was captured on
+  hipStream_t cap_stream = nullptr;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t graph_exec = nullptr;
+  int graph_steps = 0;
+  bool graph_direct = false;  // the captured steps are one whole-step launch, replayed as such
+
+  void release_graph() {
+    if (graph_exec) (void)hipGraphExecDestroy(graph_exec);
+    if (graph) (void)hipGraphDestroy(graph);
+    graph_exec = nullptr;
+    graph = nullptr;
+    graph_steps = 0;
+    graph_direct = false;
+  }
+  ~ipc_plan() {
+    release_graph();
+    if (cap_stream) (void)hipStreamDestroy(cap_stream);
+  }
 };
 
 namespace {
 
 constexpr int kNarrowSpinLimit = 1 << 22;
+
+// > 0: the co-resident workgroup capacity used instead of the device's
+// (ipc_set_coresident_limit, a test hook).
+int g_coresident_limit = 0;
+
+// Workgroups of a whole-step kernel instantiation that the current device
+// can run at once (workgroups per CU x CUs), or -1 when it cannot be
+// determined (no device).  `occupancy` reports the workgroups per CU after
+// the instantiation's LDS limit has been raised by `prepare`.
+int coresident_capacity(const std::function<hipError_t()>& prepare,
+                        const std::function<hipError_t(int*)>& occupancy) {
+  if (g_coresident_limit > 0) return g_coresident_limit;
+  int dev = 0, ncu = 0, per_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return -1;
+  if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0) return -1;
+  if (prepare() != hipSuccess || occupancy(&per_cu) != hipSuccess) return -1;
+  return per_cu * ncu;
+}
 
 bool narrow_eligible(int L, const int* dims, int storage, int operand, int split) {
   if (storage != IPC_DT_F32 || L > NARROW_MAX_L) return false;
@@ -545,7 +589,9 @@ int launch_narrow_mode(ipc_plan* plan, int mode, int steps, hipStream_t s) {
   a.steps = steps;
   if (mode == NMODE_PHASE_A || mode == NMODE_FORWARD) a.nblocks = (plan->B + NARROW_NC - 1) / NARROW_NC;
   if (mode == NMODE_PHASE_B) a.nblocks = a.wtile_start[plan->L];
-  if (a.nblocks > 256) a.nblocks = 256;
+  // the grid barriers of a multi-step launch need every workgroup running at
+  // once; the phases' loops stride by the grid, so fewer workgroups only serialise
+  if (a.nblocks > plan->narrow_cap) a.nblocks = plan->narrow_cap;
   return launch_rc(launch_narrow(a, plan->operand, plan->split, s), "whole-step kernel");
 }
 
@@ -571,11 +617,36 @@ int ipc_plan_create(ipc_plan** out, int L, const int* dims, int B, int storage, 
   const int esplit = effective_split(storage, operand, split);
   const bool eligible = narrow_eligible(L, dims, storage, operand, esplit);
   ResidentArgs ra{};
-  const long long res_bytes = resident_eligible(L, dims, B, operand, esplit, weight_mode, eligible, ra);
+  long long res_bytes = resident_eligible(L, dims, B, operand, esplit, weight_mode, eligible, ra);
   if (path == IPC_PATH_RESIDENT && res_bytes < 0)
     return fail(IPC_ERR_CONFIG,
                 "the layer-resident kernel needs a narrow net with fp16/bf16 operands, split 1 or 3, L >= 2, "
                 "widths d_0..d_{L-1} <= %d, B <= %d and the GEMM weight update", RES_MAX_WIDTH, RES_MAX_B);
+  // Every workgroup of a layer-resident launch waits for others, so all of
+  // them must be able to run at once on this device (a compute-partitioned
+  // device, or a smaller part, may hold fewer); otherwise an AUTO plan takes
+  // the column kernel, whose grid is capped at the capacity below.
+  if (res_bytes >= 0 && (path == IPC_PATH_RESIDENT || path == IPC_PATH_AUTO)) {
+    const int cap = coresident_capacity(
+        [&] { return resident_prepare(operand, esplit, act, ra.lds_bytes); },
+        [&](int* n) { return resident_occupancy(operand, esplit, act, ra.lds_bytes, n); });
+    const int need = resident_launch_blocks(ra);
+    if (cap >= 0 && need > cap) {
+      if (path == IPC_PATH_RESIDENT)
+        return fail(IPC_ERR_CONFIG,
+                    "the layer-resident kernel needs %d co-resident workgroups; this device holds %d of them",
+                    need, cap);
+      res_bytes = -1;
+    }
+  }
+  int narrow_cap = 256;
+  if (eligible && (path == IPC_PATH_AUTO || path == IPC_PATH_NARROW || path == IPC_PATH_RESIDENT)) {
+    const int lds = narrow_lds_bytes(dims, L, operand, esplit);
+    const int cap = coresident_capacity([&] { return narrow_prepare(operand, esplit, act, lds); },
+                                        [&](int* n) { return narrow_occupancy(operand, esplit, act, lds, n); });
+    if (cap == 0) return fail(IPC_ERR_CONFIG, "the whole-step kernel cannot run on this device (capacity 0)");
+    if (cap > 0 && cap < narrow_cap) narrow_cap = cap;
+  }
   if (path == IPC_PATH_NARROW && !eligible)
     return fail(IPC_ERR_CONFIG,
                 "the whole-step kernel needs fp32 storage, L <= %d, widths d_0..d_{L-1} <= %d and a column "
@@ -591,6 +662,8 @@ int ipc_plan_create(ipc_plan** out, int L, const int* dims, int B, int storage, 
   p->alpha = alpha; p->gamma = gamma; p->recompute = recompute ? 1 : 0;
   p->wmode = weight_mode;
   p->dims.assign(dims, dims + L + 1);
+  p->spin_limit = kNarrowSpinLimit;
+  p->narrow_cap = narrow_cap;
   p->resident = path == IPC_PATH_RESIDENT || (path == IPC_PATH_AUTO && res_bytes >= 0);
   p->narrow = p->resident || path == IPC_PATH_NARROW || (path == IPC_PATH_AUTO && eligible);
   p->wide = !p->narrow && (path == IPC_PATH_WIDE || (path == IPC_PATH_AUTO && weligible));
@@ -618,6 +691,7 @@ long long ipc_plan_workspace_bytes(const ipc_plan* plan) { return plan ? plan->w
 int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w, void* const* a,
                   void* workspace) {
   if (!plan) return fail(IPC_ERR_NULL, "plan is NULL");
+  plan->release_graph();  // a captured graph holds the previous buffers' addresses
   if (plan->ws_bytes) {
     TRY(check_ptr(workspace, "workspace", 4));
     if (reinterpret_cast<uintptr_t>(workspace) % 256) return fail(IPC_ERR_ALIGN, "workspace must be 256-byte aligned");
@@ -679,7 +753,7 @@ int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w
     na = NarrowArgs{};
     na.L = L; na.B = B; na.act = plan->act;
     na.alpha = plan->alpha; na.gamma = plan->gamma;
-    na.spin_limit = kNarrowSpinLimit;
+    na.spin_limit = plan->spin_limit;
     na.outer = narrow_outer(B, plan->wmode);
     int tiles = 0;
     for (int l = 0; l <= L; ++l) {
@@ -707,7 +781,7 @@ int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w
     }
     na.lds_bytes = narrow_lds_bytes(d.data(), L, plan->operand, plan->split);
     const int ncb = (B + NARROW_NC - 1) / NARROW_NC;
-    na.nblocks = std::min(256, std::max(ncb, tiles));
+    na.nblocks = std::min(plan->narrow_cap, std::max(ncb, tiles));
     na.bar = static_cast<unsigned*>(workspace);
     if (plan->recompute) {
       // pre-evaluated f(x[l]) buffers follow the barrier counters in the workspace
@@ -721,7 +795,7 @@ int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w
     if (plan->resident) {
       ResidentArgs& ra = plan->rargs;
       ra.alpha = plan->alpha; ra.gamma = plan->gamma;
-      ra.spin_limit = kNarrowSpinLimit;
+      ra.spin_limit = plan->spin_limit;
       for (int l = 0; l <= L; ++l) {
         ra.x[l] = na.x[l];
         ra.e[l] = na.e[l];
@@ -841,6 +915,7 @@ int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w
     auto chunks = [](int n) { return (n + WIDE_MAX_BATCH - 1) / WIDE_MAX_BATCH; };
     plan->launches = 2 * chunks(L) + chunks(L - 1) + (plan->pred_ksplit > 1 ? 1 : 0);
   }
+  plan->workspace = workspace;
   plan->bound = true;
   return ok();
 }
@@ -965,6 +1040,105 @@ int ipc_plan_set_tiles(ipc_plan* plan, int tile_pred, int tile_infer, int tile_w
 }
 
 int ipc_plan_launch_count(const ipc_plan* plan) { return plan ? plan->launches : 0; }
+
+int ipc_plan_set_spin_limit(ipc_plan* plan, int limit) {
+  if (!plan) return fail(IPC_ERR_NULL, "plan is NULL");
+  plan->spin_limit = limit < 0 ? kNarrowSpinLimit : limit;
+  plan->nargs.spin_limit = plan->spin_limit;
+  plan->rargs.spin_limit = plan->spin_limit;
+  return ok();
+}
+
+int ipc_plan_check(ipc_plan* plan, void* stream) {
+  if (!plan) return fail(IPC_ERR_NULL, "plan is NULL");
+  if (!plan->bound) return fail(IPC_ERR_STATE, "plan has no bound buffers");
+  hipStream_t s = (hipStream_t)stream;
+  if (!plan->narrow || !plan->workspace) {
+    if (hipStreamSynchronize(s) != hipSuccess) return fail(IPC_ERR_LAUNCH, "stream synchronisation failed");
+    return ok();
+  }
+  unsigned* word = static_cast<unsigned*>(plan->workspace) + 2;
+  unsigned flag = 0;
+  if (hipMemcpyAsync(&flag, word, sizeof(flag), hipMemcpyDeviceToHost, s) != hipSuccess ||
+      hipStreamSynchronize(s) != hipSuccess)
+    return fail(IPC_ERR_LAUNCH, "reading the whole-step kernel's timeout word failed");
+  if (flag == 0) return ok();
+  const unsigned zero = 0;
+  if (hipMemcpyAsync(word, &zero, sizeof(zero), hipMemcpyHostToDevice, s) != hipSuccess ||
+      hipStreamSynchronize(s) != hipSuccess)
+    return fail(IPC_ERR_LAUNCH, "clearing the whole-step kernel's timeout word failed");
+  return fail(IPC_ERR_TIMEOUT,
+              "a wait of the whole-step kernel ran past its spin limit: the workgroups of a launch were not all "
+              "running at once (another kernel held CUs), and the outputs of the steps since the last check are "
+              "invalid");
+}
+
+int ipc_plan_graph_capture(ipc_plan* plan, int steps) {
+  if (!plan) return fail(IPC_ERR_NULL, "plan is NULL");
+  if (!plan->bound) return fail(IPC_ERR_STATE, "plan has no bound buffers");
+  if (steps < 1) return fail(IPC_ERR_SHAPE, "steps must be >= 1 (got %d)", steps);
+  plan->release_graph();
+  if (plan->narrow) {
+    // `steps` steps of a whole-step plan are one kernel launch with fixed
+    // arguments: replaying that launch is what a one-node graph would do,
+    // without the graph launch's own cost (measured on MI355X: 49.1 us per
+    // replay of a one-node hipGraph of the d6 layer-resident launch against
+    // 44.3 us per direct launch, back to back)
+    plan->graph_steps = steps;
+    plan->graph_direct = true;
+    return ok();
+  }
+  if (!plan->cap_stream && hipStreamCreateWithFlags(&plan->cap_stream, hipStreamNonBlocking) != hipSuccess) {
+    plan->cap_stream = nullptr;
+    return fail(IPC_ERR_LAUNCH, "creating the capture stream failed");
+  }
+  if (hipStreamBeginCapture(plan->cap_stream, hipStreamCaptureModeThreadLocal) != hipSuccess)
+    return fail(IPC_ERR_LAUNCH, "hipStreamBeginCapture failed");
+  const int rc = ipc_plan_step(plan, steps, plan->cap_stream);
+  hipGraph_t g = nullptr;
+  const hipError_t ec = hipStreamEndCapture(plan->cap_stream, &g);
+  if (rc != IPC_OK) {
+    if (g) (void)hipGraphDestroy(g);
+    return rc;
+  }
+  if (ec != hipSuccess || !g) return fail(IPC_ERR_LAUNCH, "hipStreamEndCapture failed: %s", hipGetErrorString(ec));
+  const hipError_t ei = hipGraphInstantiate(&plan->graph_exec, g, nullptr, nullptr, 0);
+  if (ei != hipSuccess) {
+    plan->graph_exec = nullptr;
+    (void)hipGraphDestroy(g);
+    return fail(IPC_ERR_LAUNCH, "hipGraphInstantiate failed: %s", hipGetErrorString(ei));
+  }
+  plan->graph = g;
+  plan->graph_steps = steps;
+  return ok();
+}
+
+int ipc_plan_graph_launch(ipc_plan* plan, int repeats, void* stream) {
+  if (!plan) return fail(IPC_ERR_NULL, "plan is NULL");
+  if (!plan->graph_exec && !plan->graph_direct)
+    return fail(IPC_ERR_STATE, "the plan has no captured graph (ipc_plan_graph_capture)");
+  if (repeats < 0) return fail(IPC_ERR_SHAPE, "repeats must be >= 0");
+  if (plan->graph_direct) {
+    for (int r = 0; r < repeats; ++r)
+      TRY(launch_narrow_mode(plan, NMODE_STEPS, plan->graph_steps, (hipStream_t)stream));
+    return ok();
+  }
+  for (int r = 0; r < repeats; ++r) {
+    const hipError_t e = hipGraphLaunch(plan->graph_exec, (hipStream_t)stream);
+    if (e != hipSuccess) return fail(IPC_ERR_LAUNCH, "hipGraphLaunch failed: %s", hipGetErrorString(e));
+  }
+  return ok();
+}
+
+int ipc_plan_graph_steps(const ipc_plan* plan) {
+  return plan && (plan->graph_exec || plan->graph_direct) ? plan->graph_steps : 0;
+}
+
+int ipc_set_coresident_limit(int blocks) {
+  if (blocks < 0) return fail(IPC_ERR_CONFIG, "the co-resident limit must be >= 0 (got %d)", blocks);
+  g_coresident_limit = blocks;
+  return ok();
+}
 
 void ipc_plan_destroy(ipc_plan* plan) { delete plan; }
 

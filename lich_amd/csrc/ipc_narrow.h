@@ -168,6 +168,12 @@ void resident_bind(ResidentArgs& a, char* ws);
 hipError_t resident_invalidate(const ResidentArgs& a, hipStream_t s);
 
 hipError_t resident_prepare(int operand, int split, int act, int lds_bytes);
+// Workgroups one launch of the layer-resident kernel starts (the working
+// ones and the spare blocks of its XCD-aware grid): all of them must be able
+// to run at once.
+int resident_launch_blocks(const ResidentArgs& a);
+// Workgroups of the plan's instantiation that one CU can hold at once.
+hipError_t resident_occupancy(int operand, int split, int act, int lds_bytes, int* per_cu);
 hipError_t launch_resident(const ResidentArgs& a, int operand, int split, int act, hipStream_t s);
 
 // Number of 64x64 weight-update tiles of all layers.
@@ -178,6 +184,8 @@ int narrow_lds_bytes(const int* dims, int L, int operand, int split);
 
 // Raises the dynamic-LDS limit of the kernel instantiation a plan uses.
 hipError_t narrow_prepare(int operand, int split, int act, int lds_bytes);
+// Workgroups of that instantiation that one CU can hold at once.
+hipError_t narrow_occupancy(int operand, int split, int act, int lds_bytes, int* per_cu);
 
 // `operand` is a DT_* code, `split` 1 or 3 (16-bit operands only).
 hipError_t launch_narrow(const NarrowArgs& p, int operand, int split, hipStream_t s);

@@ -606,6 +606,13 @@ struct SetLds {
 };
 
 template <typename OT, int SPLIT, int ACT>
+struct Occupancy {
+  static hipError_t run(int bytes, int* per_cu) {
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, KernelRef<OT, SPLIT, ACT>::get(), NT, (size_t)bytes);
+  }
+};
+
+template <typename OT, int SPLIT, int ACT>
 struct Launch {
   static hipError_t run(const NarrowArgs& p, hipStream_t s) {
     KernelRef<OT, SPLIT, ACT>::launch(p, dim3(p.nblocks), dim3(NT), (size_t)p.lds_bytes, s);
@@ -630,6 +637,11 @@ int narrow_lds_bytes(const int* dims, int L, int operand, int split) {
 
 hipError_t narrow_prepare(int operand, int split, int act, int lds_bytes) {
   return by_type<SetLds>(operand, split, act, lds_bytes);
+}
+
+hipError_t narrow_occupancy(int operand, int split, int act, int lds_bytes, int* per_cu) {
+  *per_cu = 0;
+  return by_type<Occupancy>(operand, split, act, lds_bytes, per_cu);
 }
 
 hipError_t launch_narrow(const NarrowArgs& p, int operand, int split, hipStream_t s) {

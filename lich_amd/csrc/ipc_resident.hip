@@ -1017,29 +1017,39 @@ struct ResLaunch {
                        (size_t)a.lds_bytes, s, a);
     return hipGetLastError();
   }
+  static hipError_t occupancy(int bytes, int* per_cu) {
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(
+        per_cu, reinterpret_cast<const void*>(&resident_kernel<OT, SPLIT, ACT>), NT, (size_t)bytes);
+  }
 };
 
 template <typename OT, int SPLIT>
-hipError_t by_act(int act, bool prep, int bytes, const ResidentArgs* a, hipStream_t s) {
+hipError_t by_act(int act, bool prep, int bytes, const ResidentArgs* a, hipStream_t s, int* occ) {
 #define IPC_RES_CASE(A)                                                                  \
   case A:                                                                                \
-    return prep ? ResLaunch<OT, SPLIT, A>::prepare(bytes) : ResLaunch<OT, SPLIT, A>::launch(*a, s);
+    return occ ? ResLaunch<OT, SPLIT, A>::occupancy(bytes, occ)                           \
+               : prep ? ResLaunch<OT, SPLIT, A>::prepare(bytes) : ResLaunch<OT, SPLIT, A>::launch(*a, s);
   switch (act) {
     IPC_RES_CASE(ACT_RELU)
     IPC_RES_CASE(ACT_TANH)
     IPC_RES_CASE(ACT_SIGMOID)
     IPC_RES_CASE(ACT_SILU)
     IPC_RES_CASE(ACT_GELU)
+    IPC_RES_CASE(ACT_IDENTITY)
     default:
-      return prep ? ResLaunch<OT, SPLIT, ACT_IDENTITY>::prepare(bytes) : ResLaunch<OT, SPLIT, ACT_IDENTITY>::launch(*a, s);
+      return hipErrorInvalidValue;
   }
 #undef IPC_RES_CASE
 }
 
-hipError_t dispatch(int operand, int split, int act, bool prep, int bytes, const ResidentArgs* a, hipStream_t s) {
-  if (operand == DT_F16) return split >= 3 ? by_act<f16, 3>(act, prep, bytes, a, s) : by_act<f16, 1>(act, prep, bytes, a, s);
+// One of three operations on the instantiation for (operand, split, act):
+// raise its LDS limit (prep), report its workgroups per CU (occ) or launch it.
+hipError_t dispatch(int operand, int split, int act, bool prep, int bytes, const ResidentArgs* a, hipStream_t s,
+                    int* occ = nullptr) {
+  if (operand == DT_F16)
+    return split >= 3 ? by_act<f16, 3>(act, prep, bytes, a, s, occ) : by_act<f16, 1>(act, prep, bytes, a, s, occ);
   if (operand == DT_BF16)
-    return split >= 3 ? by_act<bf16, 3>(act, prep, bytes, a, s) : by_act<bf16, 1>(act, prep, bytes, a, s);
+    return split >= 3 ? by_act<bf16, 3>(act, prep, bytes, a, s, occ) : by_act<bf16, 1>(act, prep, bytes, a, s, occ);
   return hipErrorInvalidValue;
 }
 
@@ -1115,6 +1125,13 @@ hipError_t resident_invalidate(const ResidentArgs& a, hipStream_t s) {
 
 hipError_t resident_prepare(int operand, int split, int act, int lds_bytes) {
   return dispatch(operand, split, act, true, lds_bytes, nullptr, nullptr);
+}
+
+int resident_launch_blocks(const ResidentArgs& a) { return resident_grid(a.L - 1, a.chunks, a.halves); }
+
+hipError_t resident_occupancy(int operand, int split, int act, int lds_bytes, int* per_cu) {
+  *per_cu = 0;
+  return dispatch(operand, split, act, false, lds_bytes, nullptr, nullptr, per_cu);
 }
 
 hipError_t launch_resident(const ResidentArgs& a, int operand, int split, int act, hipStream_t s) {

@@ -139,11 +139,13 @@ class HierarchicalPolicy:
         best = row.get("best") if isinstance(row, dict) else None
         return best if isinstance(best, dict) else {}
 
-    def selected_grid_z(self, *, default: int, **kw) -> int:
+    def selected_grid_z(self, *, default, **kw):
+        """The entry's grid.z cap, else ``default`` (which may be None)."""
+        value = self._best(**kw).get("grid_z_max_layers")
         try:
-            return int(self._best(**kw).get("grid_z_max_layers", default))
+            return default if value is None else int(value)
         except (TypeError, ValueError):
-            return int(default)
+            return default
 
     def selected_recompute_activation(self, *, default: bool, **kw) -> bool:
         return bool(self._best(**kw).get("recompute_activation", default))

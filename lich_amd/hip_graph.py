@@ -1,14 +1,24 @@
 """Graph capture of a fixed number of iPC steps.
 
-Mirrors ``IPCGraphRunner`` (``src/ipc_tilelang/cuda_graph.py:6-36``).  On
-ROCm ``torch.cuda.CUDAGraph`` records a hipGraph: the plan's launches read
-torch's current stream at call time, so the ``steps`` steps land on the
-capture stream and replay as one graph launch.  Buffer addresses stay fixed because the model reuses its buffers for
-every batch of the same shape.
+Mirrors ``IPCGraphRunner`` (``src/ipc_tilelang/cuda_graph.py:6-36``): warm
+the kernels (``precompile``, which restores every buffer), capture ``steps``
+steps into a graph, replay it.  The graph is the plan's own
+(``ipc_plan_graph_capture``): a hipGraph recorded on a private stream inside
+the library and replayed with one ``hipGraphLaunch`` per replay on torch's
+current stream, holding the plan's launches only.  When the captured steps
+are a single launch of a whole-step kernel the library records that launch
+and replays it directly instead, which is what a one-node graph does, without
+the ~5 us of graph-launch overhead per replay measured on MI355X (49.1 us per
+replay of the depth-6 layer-resident launch against 44.3 us direct).  Buffer
+addresses stay fixed because the model reuses its buffers for every batch of
+the same shape; a new plan (another batch size) discards the graph, and
+replaying a discarded graph raises.
 """
 from __future__ import annotations
 
 import torch
+
+from . import _native as nat
 
 
 class IPCGraphRunner:
@@ -17,22 +27,25 @@ class IPCGraphRunner:
             raise ValueError("steps must be >= 1")
         self.model = model
         self.steps = int(steps)
-        self.graph = None
-        self._captured = False
+        self._plan = None
+        self._generation = None
 
     def capture(self) -> None:
         torch.cuda.synchronize()
         self.model.precompile()
         torch.cuda.synchronize()
-        self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
-            # the same `steps` steps as a loop of step_initialized calls, enqueued
-            # by one library call (the whole-step kernel runs them in one launch)
-            self.model.run_steps(self.steps)
-        torch.cuda.synchronize()
-        self._captured = True
+        plan = self.model._plan
+        nat.check(nat.lib().ipc_plan_graph_capture(plan, self.steps))
+        self.model._graph_generation = getattr(self.model, "_graph_generation", 0) + 1
+        self._plan = plan
+        self._generation = self.model._graph_generation
 
-    def replay(self) -> None:
-        if not self._captured:
-            raise RuntimeError("Graph has not been captured")
-        self.graph.replay()
+    def replay(self, repeats: int = 1) -> None:
+        """Launch the captured steps ``repeats`` times on the current stream
+        (one library call however many replays)."""
+        plan = self.model._plan
+        if (self._plan is None or plan is None or plan.value != self._plan.value
+                or self._generation != getattr(self.model, "_graph_generation", None)):
+            raise RuntimeError("Graph has not been captured (or was discarded by a later capture or a new plan)")
+        # the library refuses a plan whose graph a rebind discarded (IPC_ERR_STATE)
+        nat.check(nat.lib().ipc_plan_graph_launch(plan, int(repeats), nat.current_stream_handle(self.model.device)))

@@ -104,6 +104,7 @@ def train(a: argparse.Namespace):
             correct += batch_correct(model, x, labels)
             total += int(labels.numel())
         n_correct = int(correct.item())
+        model.check_steps()                   # raises if a whole-step launch of this epoch timed out
         dt = time.perf_counter() - t0
         rec = {"epoch": epoch + 1, "time_s": round(dt, 3), "train_acc": n_correct / max(total, 1),
                "samples_per_s": round(total / dt, 1), "samples": total, "path": model.path, "dataset": ds.name}

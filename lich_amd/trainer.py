@@ -31,8 +31,10 @@ from typing import Sequence
 import torch
 
 from . import _native as nat
+from .gridz_tuning import lookup_grid_z_cap
 from .hierarchical_policy import kernel_signature, load_hierarchical_policy
 from .kernels import KernelConfig, build_forward
+from .layer_batching import find_internal_square_groups
 from .tuning import config_to_dict
 
 
@@ -48,10 +50,12 @@ class IPCConfig:
     # A lich_amd.tuning.TuningTable, consulted after the hierarchical policy
     # (precedence of trainer.py:183-216); its configs pick the phased path's tiles.
     tuning_table: object | None = None
-    # The reference's grid.z layer batching knobs (trainer.py:38-41) are
-    # accepted; every phase is already one multi-layer launch here.  The
-    # hierarchical policy file, when present, selects recompute and graph use
-    # per net (its grid.z choice is recorded in ``grid_z_cap``).
+    # The reference's grid.z layer batching knobs (trainer.py:38-41): the cap
+    # comes from the hierarchical policy, else from the grid.z policy file
+    # (gridz_tuning.py:50-73), else grid_z_max_layers, and is recorded in
+    # ``grid_z_cap`` / ``layer_groups``; it changes no launch here, since every
+    # phase is already one multi-layer launch.  The hierarchical policy file,
+    # when present, also selects recompute and graph use per net.
     use_grid_z: bool = True
     grid_z_max_layers: int = 2
     grid_z_auto: bool = True
@@ -59,7 +63,7 @@ class IPCConfig:
     hierarchical_policy_auto: bool = True
     hierarchical_policy_path: str = "results/hierarchical_policy.json"
     steady_state_graph_auto: bool = True
-    steady_state_graph_default: bool = True
+    steady_state_graph_default: bool = False
     weight_update_mode: str = "gemm"
     weight_update_policy_path: str = "results/weight_update_policy.json"
     weight_update_outer_max_batch: int = 16
@@ -172,7 +176,8 @@ class HipIPC:
             except (OSError, ValueError):
                 self._hierarchical_policy = None
         self._runtime_recompute: bool = bool(cfg.recompute_activation)
-        self.grid_z_cap: int = int(cfg.grid_z_max_layers)
+        self.grid_z_cap: int = max(0, int(cfg.grid_z_max_layers))
+        self.layer_groups = self._groups_for(self.grid_z_cap)
         self._signature_cache: dict[int, str] = {}
 
     # ------------------------------------------------------------------ tuning artefacts
@@ -224,16 +229,30 @@ class HipIPC:
         return dict(dims=tuple(int(d) for d in self.cfg.dims), batch=int(B), activation=self.cfg.activation,
                     dtype=str(self.cfg.dtype).split(".")[-1], kernel_sig=self._active_kernel_signature(B))
 
+    def _groups_for(self, cap: int):
+        if not self.cfg.use_grid_z or cap < 2:
+            return ()
+        return find_internal_square_groups(tuple(int(d) for d in self.cfg.dims), max_group_count=cap)
+
     def _apply_execution_policy(self, B: int) -> None:
-        """Recompute and grid.z choices of the policy for this net and batch
-        (reference ``trainer.py:158-177``)."""
+        """Recompute and grid.z choices for this net and batch (reference
+        ``trainer.py:158-177`` and ``:273-300``): the hierarchical policy
+        first, then for grid.z the grid.z policy file keyed by this device."""
         self._runtime_recompute = bool(self.cfg.recompute_activation)
-        self.grid_z_cap = int(self.cfg.grid_z_max_layers)
+        cap = None
         pol = self._hierarchical_policy
         if pol is not None:
             kw = self._policy_kw(B)
             self._runtime_recompute = pol.selected_recompute_activation(default=self._runtime_recompute, **kw)
-            self.grid_z_cap = pol.selected_grid_z(default=self.grid_z_cap, **kw)
+            if self.cfg.use_grid_z and self.cfg.grid_z_auto:
+                cap = pol.selected_grid_z(default=None, **kw)
+        if cap is None and self.cfg.use_grid_z and self.cfg.grid_z_auto:
+            cap = lookup_grid_z_cap(self.cfg.grid_z_policy_path, device_name=torch.cuda.get_device_name(self.device),
+                                    capability=torch.cuda.get_device_capability(self.device), dims=self.cfg.dims,
+                                    batch=B, activation=self.cfg.activation, dtype=self.cfg.dtype,
+                                    default=int(self.cfg.grid_z_max_layers))
+        self.grid_z_cap = max(0, int(self.cfg.grid_z_max_layers if cap is None else cap))
+        self.layer_groups = self._groups_for(self.grid_z_cap)
 
     def phase_tiles(self, B: int) -> tuple[int, int, int]:
         """Tile ids of the phased path's launches: the tuned configuration of
@@ -321,11 +340,25 @@ class HipIPC:
             nat.check(nat.lib().ipc_plan_sync(self._plan, nat.current_stream_handle(self.device)))
 
     def barrier_timeouts(self) -> int:
-        """Non-zero if a grid-barrier wait of the whole-step kernel ever hit its
-        spin limit (synchronises the device)."""
+        """Non-zero if a wait of a whole-step kernel hit its spin limit since
+        the last ``check_steps`` (synchronises the device, clears nothing)."""
         if self._workspace is None:
             return 0
         return int(self._workspace[2].item())
+
+    def check_steps(self) -> None:
+        """Synchronise and raise ``RuntimeError`` if a wait of a whole-step
+        kernel gave up since the last check: those steps' states and weights
+        are invalid (their workgroups were not all running at once).  Every
+        synchronising call of this class runs it."""
+        if self._plan is not None:
+            nat.check(nat.lib().ipc_plan_check(self._plan, nat.current_stream_handle(self.device)))
+
+    def set_spin_limit(self, limit: int | None) -> None:
+        """Polls per wait of the whole-step kernels (None: the default)."""
+        if self._plan is None:
+            raise RuntimeError("Call initialize_batch first")
+        nat.check(nat.lib().ipc_plan_set_spin_limit(self._plan, -1 if limit is None else int(limit)))
 
     # ------------------------------------------------------------------ batch
     def initialize_batch(self, x_input: torch.Tensor, y_target: torch.Tensor) -> None:
@@ -365,6 +398,7 @@ class HipIPC:
     def metrics(self) -> dict[str, float]:
         """``max_abs_error`` over eps[0..L-1] of the last step (device reduction, one sync)."""
         assert self.e is not None
+        self.check_steps()
         return {"max_abs_error": float(torch.stack([v.abs().max().float() for v in self.e[:-1]]).max().item())}
 
     @torch.no_grad()
@@ -429,12 +463,14 @@ class HipIPC:
         if use_graph:
             if not self.steady_state_graph_ready(steps):
                 raise RuntimeError("Requested graph replay without a matching captured graph")
-            for _ in range(repeats):
-                self._steady_state_runner.replay()
+            self._steady_state_runner.replay(repeats)
         else:
             self.run_steps(steps * repeats)
         torch.cuda.synchronize(self.device)
-        return self.metrics() if collect_metrics else {}
+        if collect_metrics:
+            return self.metrics()
+        self.check_steps()
+        return {}
 
     def reset_steady_state(self) -> None:
         self._invalidate_steady_state_graph()
@@ -459,7 +495,7 @@ class HipIPC:
         # the workspace holds the wide path's 16-bit operand copies
         ws_backup = None if self._workspace is None else self._workspace.clone()
         self.step_initialized(collect_metrics=False)
-        torch.cuda.synchronize(self.device)
+        self.check_steps()
         for dst_list, src_list in zip((self.w, self.x, self.e), backup):
             for dst, src in zip(dst_list, src_list):
                 dst.copy_(src)

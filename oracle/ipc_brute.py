@@ -84,3 +84,27 @@ def step(x, w, act: str, alpha: float, gamma: float):
                 new_w[l][m][k] = w[l][m][k] + alpha * sum(
                     eps[l][m][b] * f(act, new_x[l + 1][k][b]) for b in range(B))
     return new_x, new_w, eps
+
+
+# ---------------------------------------------------------------------------
+# single kernels of the operator API (tilelang_kernels.py:114-349), by loops
+# ---------------------------------------------------------------------------
+def pred_err(x_upper, w, x_lower, act: str):
+    """``E[m][b] = X_lower[m][b] - sum_k W[m][k] f(X_upper[k][b])``."""
+    pred = matmul_act(w, x_upper, act)
+    return [[x_lower[m][b] - pred[m][b] for b in range(len(x_lower[0]))] for m in range(len(x_lower))]
+
+
+def infer_update(x, e, w_lower, e_lower, act: str, gamma: float):
+    """``X_new[m][b] = X + gamma(-E + f'(X) sum_k W_lower[k][m] E_lower[k][b])``
+    with ``W_lower`` of shape ``[K][M]``; returns ``(X_new, f(X_new))``."""
+    M, B, K = len(x), len(x[0]), len(e_lower)
+    x_new = [[x[m][b] + gamma * (-e[m][b] + df(act, x[m][b]) * sum(w_lower[k][m] * e_lower[k][b] for k in range(K)))
+              for b in range(B)] for m in range(M)]
+    return x_new, [[f(act, v) for v in row] for row in x_new]
+
+
+def weight_update(w, e, a, alpha: float):
+    """``W[m][k] + alpha sum_b E[m][b] A[k][b]`` (``A`` already activated)."""
+    return [[w[m][k] + alpha * sum(e[m][b] * a[k][b] for b in range(len(e[0]))) for k in range(len(w[0]))]
+            for m in range(len(w))]

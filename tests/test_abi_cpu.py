@@ -396,3 +396,63 @@ def test_trainer_refuses_cpu_device():
     from lich_amd.trainer import HipIPC, IPCConfig
     with pytest.raises(ValueError):
         HipIPC(IPCConfig(dims=(10, 64, 784)), device="cpu")
+
+
+def test_health_entry_points_validate_arguments():
+    lib = _lib()
+    assert lib.ipc_plan_check(None, None) == nat.ERR_NULL
+    assert lib.ipc_plan_set_spin_limit(None, 0) == nat.ERR_NULL
+    assert lib.ipc_set_coresident_limit(-1) == nat.ERR_CONFIG
+    dims = (ctypes.c_int * 4)(10, 64, 64, 784)
+    h = ctypes.c_void_p()
+    assert lib.ipc_plan_create(ctypes.byref(h), 3, dims, 128, 0, 0, 1, 2, 1e-4, 0.5, 1, 0, -1) == nat.IPC_OK
+    try:
+        assert lib.ipc_plan_check(h, None) == nat.ERR_STATE  # unbound: nothing to check yet
+        assert lib.ipc_plan_set_spin_limit(h, 0) == nat.IPC_OK
+        assert lib.ipc_plan_set_spin_limit(h, -1) == nat.IPC_OK
+    finally:
+        lib.ipc_plan_destroy(h)
+
+
+def test_resident_plan_refused_when_its_workgroups_cannot_run_at_once():
+    """A device that holds fewer workgroups at once than a layer-resident
+    launch starts (modelled with the co-resident limit hook): an explicit
+    resident plan fails with IPC_ERR_CONFIG, an AUTO plan takes the column
+    kernel.  Without a device (this container) the capacity is unknown and the
+    choice is the usual one."""
+    lib = _lib()
+    d6 = (ctypes.c_int * 8)(10, 64, 64, 64, 64, 64, 64, 784)
+    h = ctypes.c_void_p()
+    try:
+        assert lib.ipc_set_coresident_limit(8) == nat.IPC_OK
+        rc = lib.ipc_plan_create(ctypes.byref(h), 7, d6, 128, 0, 1, 3, 2, 1e-4, 0.5, 1, 0, nat.PATH_RESIDENT)
+        assert rc == nat.ERR_CONFIG and "co-resident" in nat.last_error()
+        assert lib.ipc_plan_create(ctypes.byref(h), 7, d6, 128, 0, 1, 3, 2, 1e-4, 0.5, 1, 0, -1) == nat.IPC_OK
+        assert lib.ipc_plan_path(h) == nat.PATH_NARROW
+        lib.ipc_plan_destroy(h)
+        assert lib.ipc_set_coresident_limit(64) == nat.IPC_OK
+        assert lib.ipc_plan_create(ctypes.byref(h), 7, d6, 128, 0, 1, 3, 2, 1e-4, 0.5, 1, 0, -1) == nat.IPC_OK
+        assert lib.ipc_plan_path(h) == nat.PATH_RESIDENT
+        lib.ipc_plan_destroy(h)
+    finally:
+        assert lib.ipc_set_coresident_limit(0) == nat.IPC_OK
+    assert lib.ipc_plan_create(ctypes.byref(h), 7, d6, 128, 0, 1, 3, 2, 1e-4, 0.5, 1, 0, -1) == nat.IPC_OK
+    assert lib.ipc_plan_path(h) == nat.PATH_RESIDENT
+    lib.ipc_plan_destroy(h)
+
+
+def test_graph_entry_points_validate_arguments():
+    lib = _lib()
+    assert lib.ipc_plan_graph_capture(None, 4) == nat.ERR_NULL
+    assert lib.ipc_plan_graph_launch(None, 1, None) == nat.ERR_NULL
+    assert lib.ipc_plan_graph_steps(None) == 0
+    dims = (ctypes.c_int * 4)(10, 64, 64, 784)
+    h = ctypes.c_void_p()
+    assert lib.ipc_plan_create(ctypes.byref(h), 3, dims, 128, 0, 0, 1, 2, 1e-4, 0.5, 1, 0, -1) == nat.IPC_OK
+    try:
+        assert lib.ipc_plan_graph_capture(h, 4) == nat.ERR_STATE  # unbound
+        assert lib.ipc_plan_graph_launch(h, 1, None) == nat.ERR_STATE  # nothing captured
+        assert "no captured graph" in nat.last_error()
+        assert lib.ipc_plan_graph_steps(h) == 0
+    finally:
+        lib.ipc_plan_destroy(h)

@@ -301,3 +301,28 @@ def test_fused_and_unfused_paths_agree():
     assert O.global_rel_err(res[0].x[1:-1], res[1].x[1:-1]) <= 1e-5
     assert O.global_rel_err([w.cpu() - w00 for w, w00 in zip(res[0].w, w0)],
                             [w.cpu() - w00 for w, w00 in zip(res[1].w, w0)]) <= 1e-4
+
+
+def test_native_graph_runner_replays_many_and_refuses_stale_graphs():
+    """The plan's own hipGraph: `repeats` replays in one call equal the same
+    steps launched directly (column kernel, fp32), a later capture or a new
+    plan discards the graph a runner holds, and replaying it then raises."""
+    dims, B, T = (10, 64, 64, 784), 128, 4
+    w0, x_in, y = _setup(dims, B, seed=13)
+    direct = HipIPC(IPCConfig(dims=dims, activation="tanh", dtype=torch.float32), device=DEV, weights=w0)
+    direct.initialize_batch(x_in.to(DEV), y.to(DEV))
+    direct.run_steps(3 * T)
+    g = HipIPC(IPCConfig(dims=dims, activation="tanh", dtype=torch.float32), device=DEV, weights=w0)
+    assert g.prepare_steady_state(x_in.to(DEV), y.to(DEV), steps=T, use_graph=True)
+    g.run_prepared_steady_state(steps=T, repeats=3, use_graph=True)
+    for a, b in zip(direct.w + direct.x + direct.e[:-1], g.w + g.x + g.e[:-1]):
+        assert torch.equal(a, b)
+    runner = g._steady_state_runner
+    r2 = g.capture_graph(2)
+    with pytest.raises(RuntimeError):
+        runner.replay()
+    r2.replay(2)
+    g.initialize_batch(x_in[:, :64].to(DEV), y[:, :64].to(DEV))  # another batch size: a new plan
+    with pytest.raises(RuntimeError):
+        r2.replay()
+    g.check_steps()

@@ -206,3 +206,47 @@ def test_flops_per_sample_matches_published_derivation():
     assert O.flops_per_sample((10,) + (64,) * 4 + (784,)) == 278_272
     assert O.flops_per_sample((10,) + (64,) * 6 + (784,)) == 327_424
     assert O.flops_per_sample((1000,) + (4096,) * 4 + (4096,)) == 393_674_752
+
+
+SHAPES = [(1, 1, 1), (3, 5, 2), (7, 4, 3), (10, 13, 6)]
+
+
+def _rand(shape, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(shape, generator=g, dtype=torch.float64) * scale
+
+
+@pytest.mark.parametrize("act", ACTS)
+@pytest.mark.parametrize("M,K,B", SHAPES)
+def test_single_kernel_helpers_match_loops(act, M, K, B):
+    """The helpers the standalone-kernel GPU tests check against, each against
+    the float64 loops on ragged shapes with non-zero errors everywhere
+    (a transposed W_lower, a dropped -E term or f' taken of the wrong tensor
+    changes these results)."""
+    seed = 1000 * M + 10 * K + B
+    xu, w, xl = _rand((K, B), seed), _rand((M, K), seed + 1, 0.5), _rand((M, B), seed + 2)
+    e, wlo, elo = _rand((M, B), seed + 3), _rand((K, M), seed + 4, 0.5), _rand((K, B), seed + 5)
+    got = O.pred_err(xu, w, xl, act)
+    assert _tol(got, brute.pred_err(_to_list(xu), _to_list(w), _to_list(xl), act)) < 1e-12
+    assert _tol(O.forward_pred(xu, w, act), brute.matmul_act(_to_list(w), _to_list(xu), act)) < 1e-12
+    x_new, a_new = O.infer_update(xl, e, wlo, elo, act, 0.375)
+    bx, ba = brute.infer_update(_to_list(xl), _to_list(e), _to_list(wlo), _to_list(elo), act, 0.375)
+    assert _tol(x_new, bx) < 1e-12 and _tol(a_new, ba) < 1e-12
+    a = [[brute.f(act, v) for v in row] for row in _to_list(xu)]
+    assert _tol(O.weight_update(w, e, xu, act, 0.01), brute.weight_update(_to_list(w), _to_list(e), a, 0.01)) < 1e-12
+    assert _tol(O.weight_update(w, e, torch.tensor(a, dtype=torch.float64), act, 0.01, recompute=False),
+                brute.weight_update(_to_list(w), _to_list(e), a, 0.01)) < 1e-12
+
+
+def test_single_kernel_helpers_special_cases():
+    """Closed forms: W = 0 gives E = X_lower; relu of a negative X_upper gives
+    E = X_lower; gamma = 0 leaves X; E_lower = 0 gives X - gamma E; a W_lower
+    that is not square exposes a transposed read."""
+    xu, w, xl = _rand((5, 3), 1), _rand((4, 5), 2), _rand((4, 3), 3)
+    assert torch.equal(O.pred_err(xu, torch.zeros_like(w), xl, "tanh"), xl)
+    assert torch.equal(O.pred_err(-xu.abs() - 1, w, xl, "relu"), xl)
+    e, wlo, elo = _rand((4, 3), 4), _rand((6, 4), 5), _rand((6, 3), 6)
+    assert torch.equal(O.infer_update(xl, e, wlo, elo, "silu", 0.0)[0], xl)
+    assert _tol(O.infer_update(xl, e, wlo, torch.zeros_like(elo), "silu", 0.5)[0], xl - 0.5 * e) < 1e-15
+    with pytest.raises(RuntimeError):
+        O.infer_update(xl, e, wlo.T.contiguous(), elo, "silu", 0.5)

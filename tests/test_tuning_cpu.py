@@ -84,3 +84,33 @@ def test_policy_skips_malformed_rows_and_missing_files(tmp_path):
     assert HP.load_hierarchical_policy(tmp_path / "none.json") is None
     with pytest.raises(ValueError):
         HP.HierarchicalPolicy(data=[1, 2])
+
+
+GRIDZ = Path(__file__).parent / "golden" / "gridz_policy_excerpt.json"
+RTX = dict(device_name="NVIDIA GeForce RTX 3060 Laptop GPU", capability=(8, 6), batch=128, activation="relu")
+
+
+def test_gridz_key_format_reproduces_the_reference_keys():
+    from lich_amd import gridz_tuning as GZ
+
+    keys = set(json.loads(GRIDZ.read_text())["entries"])
+    for dims in ((10, 64, 64, 64, 64, 784), (10,) + (64,) * 6 + (784,)):
+        import torch
+        assert GZ.make_policy_key(dims=dims, dtype=torch.float16, **RTX) in keys
+
+
+def test_gridz_lookup_rules(tmp_path):
+    from lich_amd import gridz_tuning as GZ
+
+    d4, d6 = (10, 64, 64, 64, 64, 784), (10,) + (64,) * 6 + (784,)
+    assert GZ.lookup_grid_z_cap(GRIDZ, dims=d4, dtype="float16", default=0, **RTX) == 3
+    assert GZ.lookup_grid_z_cap(GRIDZ, dims=d6, dtype="float16", default=0, **RTX) == 2
+    # another device, batch or dtype has no entry: the caller's default
+    other = dict(RTX, device_name="AMD Instinct MI355X", capability=(9, 5))
+    assert GZ.lookup_grid_z_cap(GRIDZ, dims=d4, dtype="float16", default=5, **other) == 5
+    assert GZ.lookup_grid_z_cap(GRIDZ, dims=d4, dtype="bfloat16", default=4, **RTX) == 4
+    assert GZ.lookup_grid_z_cap(tmp_path / "missing.json", dims=d4, dtype="float16", default=2, **RTX) == 2
+    bad = tmp_path / "bad.json"
+    bad.write_text(json.dumps({"entries": []}))
+    with pytest.raises(ValueError):
+        GZ.lookup_grid_z_cap(bad, dims=d4, dtype="float16", **RTX)
