@@ -311,6 +311,30 @@ int ipc_plan_graph_capture(ipc_plan* plan, int steps);
 int ipc_plan_graph_launch(ipc_plan* plan, int repeats, void* stream);
 int ipc_plan_graph_steps(const ipc_plan* plan);
 
+/*
+ * No counterpart in the reference: an entry point for callers that cannot
+ * allocate device memory (code under hipGraph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Runs `steps` iPC steps of a narrow net
+ * on the whole-step kernels exactly as a plan created with IPC_PATH_AUTO,
+ * fp32 storage and recompute mode would (ipc_plan_create + ipc_plan_bind +
+ * ipc_plan_step: same kernels, same results), without a plan or a caller
+ * workspace: the kernels' barrier words, f(x) buffers and exchange records
+ * live in the library's static device scratch, 8 MiB per GPU, held until the
+ * process ends.  A net that needs more is refused with IPC_ERR_SHAPE; one the
+ * whole-step kernels do not take (a width above 128, L above 16, split 2)
+ * with IPC_ERR_CONFIG.  x (L+1 pointers), e (L pointers, e[L] unused) and w
+ * (L pointers) are laid out as for ipc_plan_bind; the caller does the forward
+ * initialisation.  Each call clears the scratch words that must start at
+ * zero; calls that overlap on one GPU (other streams or threads) race on the
+ * scratch and must be serialised.  A wait that gives up (see ipc_plan_check)
+ * marks only the scratch, which the next call clears: callers that need that
+ * report use a plan.  Calls no hipMalloc, hipFree or other allocating
+ * routine.
+ */
+int ipc_steps_noalloc(int L, const int* dims, int B, void* const* x, void* const* e, void* const* w,
+                      int operand, int split, int act, float alpha, float gamma, int weight_mode, int steps,
+                      void* stream);
+
 /* Test hook: > 0 replaces the device's co-resident workgroup capacity in the
  * checks of ipc_plan_create (a compute-partitioned device can be modelled
  * without one); 0 restores the device query.  Not thread-safe. */

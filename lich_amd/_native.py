@@ -93,6 +93,8 @@ def _declare(lib):
         "ipc_plan_graph_capture": ([vp, i], i),
         "ipc_plan_graph_launch": ([vp, i, vp], i),
         "ipc_plan_graph_steps": ([vp], i),
+        "ipc_steps_noalloc": ([i, POINTER(c_int), i, POINTER(vp), POINTER(vp), POINTER(vp), i, i, i, f, f, i, i, vp],
+                              i),
         "ipc_plan_destroy": ([vp], None),
     }
     for name, (args, res) in sig.items():

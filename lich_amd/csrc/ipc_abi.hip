@@ -14,6 +14,7 @@
 #include <cstdio>
 #include <cstring>
 #include <functional>
+#include <mutex>
 #include <new>
 #include <queue>
 #include <string>
@@ -455,12 +456,47 @@ constexpr int kNarrowSpinLimit = 1 << 22;
 // (ipc_set_coresident_limit, a test hook).
 int g_coresident_limit = 0;
 
+// Static device scratch of the no-allocation entry point (ipc_steps_noalloc):
+// every GPU the library runs on holds its own copy for the life of the
+// process.  Host code never uses the array's name as an address (on the host
+// it is a stand-in symbol): scratch_address looks up the device copy with
+// hipGetSymbolAddress once per device and keeps it.
+constexpr long long kScratchBytes = 8LL << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+char* g_scratch_ptr[kMaxDevices] = {};
+
+// Address of the current device's copy of `scratch`.
+int scratch_address(char** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(IPC_ERR_DEVICE, "no current device");
+  if (dev < 0 || dev >= kMaxDevices) return fail(IPC_ERR_DEVICE, "device index %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !p)
+      return fail(IPC_ERR_DEVICE, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev, hipGetErrorString(err));
+    g_scratch_ptr[dev] = static_cast<char*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return ok();
+}
+
+// Zeroes the column kernel's barrier words and, when given, the resident
+// kernel's flag words (64 words each) before a launch on the scratch.
+__global__ void scratch_clear_kernel(unsigned* bar, unsigned* flags) {
+  bar[threadIdx.x] = 0u;
+  if (flags) flags[threadIdx.x] = 0u;
+}
+
 // Workgroups of a whole-step kernel instantiation that the current device
 // can run at once (workgroups per CU x CUs), or -1 when it cannot be
 // determined (no device).  `occupancy` reports the workgroups per CU after
 // the instantiation's LDS limit has been raised by `prepare`.
-int coresident_capacity(const std::function<hipError_t()>& prepare,
-                        const std::function<hipError_t(int*)>& occupancy) {
+template <typename Prepare, typename Occupancy>
+int coresident_capacity(const Prepare& prepare, const Occupancy& occupancy) {
   if (g_coresident_limit > 0) return g_coresident_limit;
   int dev = 0, ncu = 0, per_cu = 0;
   if (hipGetDevice(&dev) != hipSuccess) return -1;
@@ -593,6 +629,77 @@ int launch_narrow_mode(ipc_plan* plan, int mode, int steps, hipStream_t s) {
   // once; the phases' loops stride by the grid, so fewer workgroups only serialise
   if (a.nblocks > plan->narrow_cap) a.nblocks = plan->narrow_cap;
   return launch_rc(launch_narrow(a, plan->operand, plan->split, s), "whole-step kernel");
+}
+
+// Arguments of the whole-step kernels for bound buffers: the column kernel's
+// `na` and, when `ra` is given (already laid out by resident_plan), the
+// layer-resident kernel's.  `a` is NULL in recompute mode; `ws` is the
+// workspace (barrier words, then the f(x) buffers of recompute mode, the
+// resident exchange at `res_ws_off`).  Builds everything in place without
+// heap allocation, so the no-allocation entry point shares it.
+int bind_whole_step(NarrowArgs& na, ResidentArgs* ra, int L, const int* d, int B, void* const* x, void* const* e,
+                    void* const* w, void* const* a, int act, int operand, int split, float alpha, float gamma,
+                    bool outer, int spin_limit, int cap, char* ws, long long res_ws_off) {
+  na = NarrowArgs{};
+  na.L = L; na.B = B; na.act = act;
+  na.alpha = alpha; na.gamma = gamma;
+  na.spin_limit = spin_limit;
+  na.outer = outer;
+  int tiles = 0;
+  for (int l = 0; l <= L; ++l) {
+    na.dims[l] = d[l];
+    na.x[l] = static_cast<float*>(x[l]);
+    na.e[l] = l < L ? static_cast<float*>(e[l]) : nullptr;
+    na.a[l] = (a && l >= 1) ? static_cast<float*>(a[l]) : nullptr;
+    na.fx[l] = na.a[l];
+    if (l < L) na.w[l] = static_cast<float*>(w[l]);
+    na.wtile_start[l] = tiles;
+    if (l < L) tiles += narrow_tiles(&d[l], 1);
+  }
+  // prediction/inference units (layer, 16-row tile), the longest contraction
+  // first; insertion keeps units of equal contraction in (layer, tile) order
+  int n = 0;
+  for (int l = 0; l < L; ++l)
+    for (int rt = 0; rt * 16 < d[l]; ++rt) {
+      if (n >= NARROW_MAX_UNITS) return fail(IPC_ERR_SHAPE, "too many prediction units for the whole-step kernel");
+      int i = n++;
+      while (i > 0 && d[na.unit_l[i - 1] + 1] < d[l + 1]) {
+        na.unit_l[i] = na.unit_l[i - 1];
+        na.unit_rt[i] = na.unit_rt[i - 1];
+        --i;
+      }
+      na.unit_l[i] = (unsigned char)l;
+      na.unit_rt[i] = (unsigned char)rt;
+    }
+  na.n_units = n;
+  na.lds_bytes = narrow_lds_bytes(d, L, operand, split);
+  const int ncb = (B + NARROW_NC - 1) / NARROW_NC;
+  na.nblocks = std::min(cap, std::max(ncb, tiles));
+  na.bar = reinterpret_cast<unsigned*>(ws);
+  if (!a) {
+    // pre-evaluated f(x[l]) buffers follow the barrier counters in the workspace
+    char* at = ws + 256;
+    for (int l = 1; l <= L; ++l) {
+      na.fx[l] = reinterpret_cast<float*>(at);
+      at += ((long long)d[l] * B * 4 + 255) / 256 * 256;
+    }
+  }
+  TRY(launch_rc(narrow_prepare(operand, split, act, na.lds_bytes), "whole-step kernel LDS limit"));
+  if (ra) {
+    ra->alpha = alpha; ra->gamma = gamma;
+    ra->spin_limit = spin_limit;
+    for (int l = 0; l <= L; ++l) {
+      ra->x[l] = na.x[l];
+      ra->e[l] = na.e[l];
+      ra->fx[l] = na.fx[l];
+      if (l < L) ra->w[l] = na.w[l];
+    }
+    ra->bar = na.bar;
+    resident_bind(*ra, ws + res_ws_off);
+    na.res_image_flag = ra->flags + RES_MAX_WG;
+    TRY(launch_rc(resident_prepare(operand, split, act, ra->lds_bytes), "layer-resident kernel LDS limit"));
+  }
+  return ok();
 }
 
 }  // namespace
@@ -749,65 +856,10 @@ int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w
   if (plan->tile_override[2] != IPC_TILE_AUTO) plan->tile_weight = plan->tile_override[2];
   plan->launches = 1 + (plan->infer.empty() ? 0 : 1) + (plan->weight.empty() ? 0 : 1) + (int)plan->outer.size();
   if (plan->narrow) {
-    NarrowArgs& na = plan->nargs;
-    na = NarrowArgs{};
-    na.L = L; na.B = B; na.act = plan->act;
-    na.alpha = plan->alpha; na.gamma = plan->gamma;
-    na.spin_limit = plan->spin_limit;
-    na.outer = narrow_outer(B, plan->wmode);
-    int tiles = 0;
-    for (int l = 0; l <= L; ++l) {
-      na.dims[l] = d[l];
-      na.x[l] = static_cast<float*>(x[l]);
-      na.e[l] = l < L ? static_cast<float*>(e[l]) : nullptr;
-      na.a[l] = (!plan->recompute && l >= 1) ? static_cast<float*>(a[l]) : nullptr;
-      na.fx[l] = na.a[l];
-      if (l < L) na.w[l] = static_cast<float*>(w[l]);
-      na.wtile_start[l] = tiles;
-      if (l < L) tiles += narrow_tiles(&d[l], 1);
-    }
-    // prediction/inference units (layer, 16-row tile), the longest contraction first
-    std::vector<std::pair<int, int>> units;
-    for (int l = 0; l < L; ++l)
-      for (int rt = 0; rt * 16 < d[l]; ++rt) units.push_back({l, rt});
-    std::stable_sort(units.begin(), units.end(),
-                     [&](const std::pair<int, int>& u, const std::pair<int, int>& v) {
-                       return d[u.first + 1] > d[v.first + 1];
-                     });
-    na.n_units = (int)units.size();
-    for (int i = 0; i < na.n_units; ++i) {
-      na.unit_l[i] = (unsigned char)units[i].first;
-      na.unit_rt[i] = (unsigned char)units[i].second;
-    }
-    na.lds_bytes = narrow_lds_bytes(d.data(), L, plan->operand, plan->split);
-    const int ncb = (B + NARROW_NC - 1) / NARROW_NC;
-    na.nblocks = std::min(plan->narrow_cap, std::max(ncb, tiles));
-    na.bar = static_cast<unsigned*>(workspace);
-    if (plan->recompute) {
-      // pre-evaluated f(x[l]) buffers follow the barrier counters in the workspace
-      char* ws = static_cast<char*>(workspace) + 256;
-      for (int l = 1; l <= L; ++l) {
-        na.fx[l] = reinterpret_cast<float*>(ws);
-        ws += ((long long)d[l] * B * 4 + 255) / 256 * 256;
-      }
-    }
-    TRY(launch_rc(narrow_prepare(plan->operand, plan->split, plan->act, na.lds_bytes), "whole-step kernel LDS limit"));
-    if (plan->resident) {
-      ResidentArgs& ra = plan->rargs;
-      ra.alpha = plan->alpha; ra.gamma = plan->gamma;
-      ra.spin_limit = plan->spin_limit;
-      for (int l = 0; l <= L; ++l) {
-        ra.x[l] = na.x[l];
-        ra.e[l] = na.e[l];
-        ra.fx[l] = na.fx[l];
-        if (l < L) ra.w[l] = na.w[l];
-      }
-      ra.bar = na.bar;
-      resident_bind(ra, static_cast<char*>(workspace) + plan->res_ws_off);
-      na.res_image_flag = ra.flags + RES_MAX_WG;
-      TRY(launch_rc(resident_prepare(plan->operand, plan->split, plan->act, ra.lds_bytes),
-                    "layer-resident kernel LDS limit"));
-    }
+    TRY(bind_whole_step(plan->nargs, plan->resident ? &plan->rargs : nullptr, L, d.data(), B, x, e, w,
+                        plan->recompute ? nullptr : a, plan->act, plan->operand, plan->split, plan->alpha,
+                        plan->gamma, narrow_outer(B, plan->wmode), plan->spin_limit, plan->narrow_cap,
+                        static_cast<char*>(workspace), plan->res_ws_off));
     plan->launches = 1;
   }
   if (plan->wide) {
@@ -1132,6 +1184,81 @@ int ipc_plan_graph_launch(ipc_plan* plan, int repeats, void* stream) {
 
 int ipc_plan_graph_steps(const ipc_plan* plan) {
   return plan && (plan->graph_exec || plan->graph_direct) ? plan->graph_steps : 0;
+}
+
+int ipc_steps_noalloc(int L, const int* dims, int B, void* const* x, void* const* e, void* const* w, int operand,
+                      int split, int act, float alpha, float gamma, int weight_mode, int steps, void* stream) {
+  if (!dims) return fail(IPC_ERR_NULL, "dims is NULL");
+  if (!x || !e || !w) return fail(IPC_ERR_NULL, "x, e and w pointer arrays are required");
+  if (L < 1 || L > NARROW_MAX_L) return fail(IPC_ERR_SHAPE, "L must be in [1, %d] (got %d)", NARROW_MAX_L, L);
+  TRY(check_dtypes(IPC_DT_F32, operand));
+  TRY(check_split(split));
+  TRY(check_act(act));
+  if (weight_mode < IPC_WMODE_GEMM || weight_mode > IPC_WMODE_AUTO)
+    return fail(IPC_ERR_CONFIG, "unknown weight mode %d", weight_mode);
+  for (int l = 0; l < L; ++l) TRY(check_dims(dims[l], dims[l + 1], B, 1));
+  if (weight_mode == IPC_WMODE_OUTER && B > kOuterMaxB)
+    return fail(IPC_ERR_SHAPE, "outer weight mode supports B <= %d (got %d)", kOuterMaxB, B);
+  if (steps < 0) return fail(IPC_ERR_SHAPE, "steps must be >= 0");
+  const int esplit = effective_split(IPC_DT_F32, operand, split);
+  if (!narrow_eligible(L, dims, IPC_DT_F32, operand, esplit))
+    return fail(IPC_ERR_CONFIG,
+                "ipc_steps_noalloc runs the whole-step kernels only: widths d_0..d_{L-1} <= %d, L <= %d, split 1 "
+                "or 3 and a column block that fits in LDS", NARROW_MAX_WIDTH, NARROW_MAX_L);
+  char name[32];
+  for (int l = 0; l <= L; ++l) {
+    snprintf(name, sizeof(name), "x[%d]", l);
+    TRY(check_ptr(x[l], name, 4));
+    if (l < L) {
+      snprintf(name, sizeof(name), "e[%d]", l);
+      TRY(check_ptr(e[l], name, 4));
+      snprintf(name, sizeof(name), "w[%d]", l);
+      TRY(check_ptr(w[l], name, 4));
+    }
+  }
+  // scratch the launch needs: the column kernel's barrier words and f(x)
+  // buffers, then the layer-resident kernel's flags and exchange records
+  ResidentArgs ra{};
+  long long res_bytes = resident_eligible(L, dims, B, operand, esplit, weight_mode, true, ra);
+  long long need = narrow_workspace_bytes(dims, L, B, true), res_off = 0;
+  if (res_bytes >= 0) {
+    res_off = (need + 255) / 256 * 256;
+    need = res_off + res_bytes;
+  }
+  if (need > kScratchBytes)
+    return fail(IPC_ERR_SHAPE,
+                "this net needs %lld bytes of scratch; the library's static scratch holds %lld (use a plan with a "
+                "caller workspace)", need, kScratchBytes);
+  if (steps == 0) return ok();
+  char* ws = nullptr;
+  TRY(scratch_address(&ws));
+  if (res_bytes >= 0) {
+    const int cap = coresident_capacity([&] { return resident_prepare(operand, esplit, act, ra.lds_bytes); },
+                                        [&](int* n) { return resident_occupancy(operand, esplit, act, ra.lds_bytes, n); });
+    if (cap >= 0 && resident_launch_blocks(ra) > cap) res_bytes = -1;
+  }
+  const int lds = narrow_lds_bytes(dims, L, operand, esplit);
+  int cap = coresident_capacity([&] { return narrow_prepare(operand, esplit, act, lds); },
+                                [&](int* n) { return narrow_occupancy(operand, esplit, act, lds, n); });
+  if (cap == 0) return fail(IPC_ERR_CONFIG, "the whole-step kernel cannot run on this device (capacity 0)");
+  cap = cap < 0 || cap > 256 ? 256 : cap;
+  NarrowArgs na{};
+  TRY(bind_whole_step(na, res_bytes >= 0 ? &ra : nullptr, L, dims, B, x, e, w, nullptr, act, operand, esplit, alpha,
+                      gamma, narrow_outer(B, weight_mode), kNarrowSpinLimit, cap, ws, res_off));
+  hipStream_t s = (hipStream_t)stream;
+  // the scratch keeps the previous call's contents: the barrier words and the
+  // resident flags (their word RES_MAX_WG marks the cached input images
+  // valid) must start at zero; everything else is written before it is read
+  hipLaunchKernelGGL(scratch_clear_kernel, dim3(1), dim3(64), 0, s, reinterpret_cast<unsigned*>(ws),
+                     res_bytes >= 0 ? reinterpret_cast<unsigned*>(ws + res_off) : nullptr);
+  TRY(launch_rc(hipGetLastError(), "scratch clear"));
+  if (res_bytes >= 0) {
+    ra.steps = steps;
+    return launch_rc(launch_resident(ra, operand, esplit, act, s), "layer-resident whole-step kernel");
+  }
+  na.mode = NMODE_STEPS;
+  na.steps = steps;
+  return launch_rc(launch_narrow(na, operand, esplit, s), "whole-step kernel");
 }
 
 int ipc_set_coresident_limit(int blocks) {

@@ -456,3 +456,20 @@ def test_graph_entry_points_validate_arguments():
         assert lib.ipc_plan_graph_steps(h) == 0
     finally:
         lib.ipc_plan_destroy(h)
+
+
+def test_noalloc_entry_point_validates_on_the_host():
+    lib = _lib()
+    d = (ctypes.c_int * 4)(10, 64, 64, 784)
+    arr = (ctypes.c_void_p * 4)(P, P, P, P)
+    args = (3, d, 128, arr, arr, arr, nat.DT_F16, 3, 2, 1e-4, 0.5, 0)
+    assert lib.ipc_steps_noalloc(3, None, 128, arr, arr, arr, nat.DT_F16, 3, 2, 1e-4, 0.5, 0, 1, None) == nat.ERR_NULL
+    assert lib.ipc_steps_noalloc(*args[:3], None, arr, arr, *args[6:], 1, None) == nat.ERR_NULL
+    assert lib.ipc_steps_noalloc(*args, -1, None) == nat.ERR_SHAPE
+    wide = (ctypes.c_int * 3)(1000, 4096, 4096)
+    assert lib.ipc_steps_noalloc(2, wide, 1024, arr, arr, arr, nat.DT_BF16, 2, 2, 1e-4, 0.5, 0, 1, None) == nat.ERR_CONFIG
+    # the f(x) buffers of B = 4096 exceed the 8 MiB static scratch: refused before any HIP call
+    assert lib.ipc_steps_noalloc(3, d, 4096, arr, arr, arr, nat.DT_F16, 3, 2, 1e-4, 0.5, 0, 1, None) == nat.ERR_SHAPE
+    assert "scratch" in nat.last_error()
+    # zero steps of an acceptable net: validated, nothing enqueued
+    assert lib.ipc_steps_noalloc(*args, 0, None) == nat.IPC_OK

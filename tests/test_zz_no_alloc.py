@@ -1,0 +1,70 @@
+"""``ipc_steps_noalloc`` (the static-scratch entry point) against the plan path.
+
+Both run the same whole-step kernel with the same arithmetic; only the home
+of the kernels' barrier words, f(x) buffers and exchange records differs
+(the library's static device scratch against the plan's workspace), so the
+states, errors and weights must agree bit for bit.  Two calls in a row per
+net, the second with a smaller batch, so the second runs on the scratch the
+first left behind.
+"""
+import ctypes
+
+import pytest
+import torch
+
+from lich_amd import _native as nat
+from lich_amd.trainer import HipIPC, IPCConfig, _ptr_array
+from oracle import ipc_oracle as O
+from tests.helpers import DEV, report
+
+pytestmark = pytest.mark.gpu
+
+T = 4
+D6 = (10,) + (64,) * 6 + (784,)
+
+
+def _noalloc(dims, B, x, e, w, operand, split, act, wmode, steps):
+    L = len(dims) - 1
+    d = (ctypes.c_int * (L + 1))(*dims)
+    return nat.lib().ipc_steps_noalloc(L, d, B, _ptr_array(x), _ptr_array(e), _ptr_array(w), operand, split, act,
+                                       1e-4, 0.5, wmode, steps, nat.current_stream_handle(DEV))
+
+
+@pytest.mark.parametrize("dims,dtype,wmode,path,batches", [
+    (D6, torch.float16, "gemm", "resident", (128, 64)),
+    (D6, torch.bfloat16, "gemm", "resident", (96, 40)),
+    ((10, 64, 64, 64, 784), torch.float32, "gemm", "narrow", (128, 48)),
+    ((10, 64, 64, 64, 64, 784), torch.float32, "auto", "narrow", (8, 4)),
+])
+def test_noalloc_steps_equal_the_plan_path(dims, dtype, wmode, path, batches):
+    for B in batches:
+        report("noalloc", dims=len(dims) - 1, dtype=str(dtype), B=B, path=path)
+        w0 = O.init_weights(dims, seed=B, init="xavier_uniform")
+        x_in, _l, y = O.make_batch(dims, B, seed=B)
+        m = HipIPC(IPCConfig(dims=dims, activation="tanh", dtype=dtype, weight_update_mode=wmode,
+                             hierarchical_policy_auto=False), device=DEV, weights=w0)
+        m.initialize_batch(x_in.to(DEV), y.to(DEV))
+        assert m.path == path
+        xs, es, ws = [t.clone() for t in m.x], [t.clone() for t in m.e], [t.clone() for t in m.w]
+        m.run_steps(T)
+        nat.check(_noalloc(dims, B, xs, es, ws, nat.dtype_code(dtype), m.pred_split, nat.act_code("tanh"),
+                           nat.WMODE[wmode], T))
+        torch.cuda.synchronize()
+        m.check_steps()
+        for a, b in zip(m.x + m.e[:-1] + m.w, xs + es[:-1] + ws):
+            assert torch.equal(a, b)
+
+
+def test_noalloc_refuses_what_it_cannot_run():
+    report("noalloc-refuse")
+    # the wide net is not a whole-step net
+    dims = (1000, 4096, 4096)
+    P = [None] * 3
+    rc = _noalloc(dims, 1024, P, P, P, nat.DT_BF16, 2, nat.act_code("tanh"), 0, 1)
+    assert rc in (nat.ERR_NULL, nat.ERR_CONFIG)
+    # a whole-step net whose f(x) buffers exceed the 8 MiB scratch (B = 4096)
+    dims = (10, 64, 64, 784)
+    t = [torch.zeros((d, 4096), device=DEV) for d in dims]
+    ws = [torch.zeros((a, b), device=DEV) for a, b in zip(dims[:-1], dims[1:])]
+    rc = _noalloc(dims, 4096, t, t, ws, nat.DT_F16, 3, nat.act_code("tanh"), 0, 1)
+    assert rc == nat.ERR_SHAPE and "scratch" in nat.last_error()
