@@ -117,6 +117,24 @@ constexpr int smem_bytes(int BM, int BN, int S, bool LO) {
                                                                      : BM * (BN + 1) * 4;
 }
 
+// Position (tile row mb, tile column nb) of tile `t` of a tm x tn tile grid
+// walked in supertiles of ST_R x ST_C tiles: row-major inside a supertile,
+// supertiles row-major, the last band and column of supertiles cut to what is
+// left.  The tiles one XCD runs at once (32 CUs) then form one 8 x 4 block,
+// which reads 8 row blocks of A and 4 of B, instead of 2 x 16 (the whole of
+// B) in row-major order; with at most 4 tile columns the order is row-major.
+constexpr int ST_R = 8, ST_C = 4;
+__device__ __forceinline__ void supertile_pos(int t, int tm, int tn, int& mb, int& nb) {
+  const int band = t / (ST_R * tn);
+  const int rows = tm - band * ST_R < ST_R ? tm - band * ST_R : ST_R;
+  const int w = t - band * ST_R * tn;
+  const int cs = w / (rows * ST_C);
+  const int cols = tn - cs * ST_C < ST_C ? tn - cs * ST_C : ST_C;
+  const int w2 = w - cs * rows * ST_C;
+  mb = band * ST_R + w2 / cols;
+  nb = cs * ST_C + w2 % cols;
+}
+
 struct Batch {
   WideProblem p[WIDE_MAX_BATCH];
   int start[WIDE_MAX_BATCH + 1];  // first tile of each problem
@@ -164,7 +182,9 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
   const int slice = partial ? (tile - bt.start[pi]) / tmn : 0;
   const int local = tile - bt.start[pi] - slice * tmn;
   const int kslice = partial ? p.K / p.ksplit : p.K;
-  const int m0 = (local / tn) * BM, n0 = (local % tn) * BN;
+  int mblk, nblk;
+  supertile_pos(local, (p.M + BM - 1) / BM, tn, mblk, nblk);
+  const int m0 = mblk * BM, n0 = nblk * BN;
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int wm = w / WGN, wn = w % WGN;
@@ -551,6 +571,7 @@ struct Cfg {
     bt.tail = count;
     int total = 0;
     for (int i = 0; i < count; ++i) {
+      if (SPLIT == 2 && MODE == WIDE_PRED && !probs[i].a_lo) return hipErrorInvalidValue;
       const int ks = MODE == WIDE_PRED && probs[i].ksplit > 1 ? probs[i].ksplit : 1;
       if (ks > 1) {
         if (probs[i].K % (ks * WIDE_BK) != 0) return hipErrorInvalidValue;

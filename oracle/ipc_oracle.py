@@ -254,6 +254,8 @@ def global_rel_err(got: Sequence[torch.Tensor], ref: Sequence[torch.Tensor]) -> 
     for g, r in zip(got, ref):
         g64 = g.detach().double().cpu()
         r64 = r.detach().double().cpu()
+        if not (bool(torch.isfinite(g64).all()) and bool(torch.isfinite(r64).all())):
+            return float("inf")  # a NaN would otherwise drop out of max() and read as agreement
         num = max(num, float((g64 - r64).abs().max()) if g64.numel() else 0.0)
         den = max(den, float(r64.abs().max()) if r64.numel() else 0.0)
     if den == 0.0:

@@ -20,6 +20,8 @@ def rel_err(got, ref) -> float:
     """max |got - ref| / max |ref| (both moved to fp64 on the CPU)."""
     got = got.detach().double().cpu()
     ref = ref.detach().double().cpu()
+    if not (bool(torch.isfinite(got).all()) and bool(torch.isfinite(ref).all())):
+        return float("inf")  # NaN must never read as agreement
     den = float(ref.abs().max())
     num = float((got - ref).abs().max())
     if den == 0.0:

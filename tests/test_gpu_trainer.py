@@ -83,7 +83,7 @@ def _gate_fraction(got, ref, tol=2e-2):
     for g, r in zip(got, ref):
         g = g.detach().double().cpu()
         r = r.double()
-        bad += int(((g - r).abs() > tol + tol * r.abs()).sum())
+        bad += int((~((g - r).abs() <= tol + tol * r.abs())).sum())  # NaN counts as outside
         total += r.numel()
     return bad / total
 

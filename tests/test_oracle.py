@@ -250,3 +250,11 @@ def test_single_kernel_helpers_special_cases():
     assert _tol(O.infer_update(xl, e, wlo, torch.zeros_like(elo), "silu", 0.5)[0], xl - 0.5 * e) < 1e-15
     with pytest.raises(RuntimeError):
         O.infer_update(xl, e, wlo.T.contiguous(), elo, "silu", 0.5)
+
+
+def test_global_rel_err_never_reads_nan_as_agreement():
+    a = [torch.ones(3), torch.tensor([1.0, float("nan")])]
+    b = [torch.ones(3), torch.tensor([1.0, 2.0])]
+    assert O.global_rel_err(a, b) == float("inf")
+    assert O.global_rel_err(b, a) == float("inf")
+    assert O.global_rel_err(b, b) == 0.0
