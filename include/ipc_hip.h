@@ -262,6 +262,21 @@ int ipc_plan_phase(ipc_plan* plan, int phase, int reps, void* stream);
  * ignore it.  Valid before or after ipc_plan_bind. */
 int ipc_plan_set_tiles(ipc_plan* plan, int tile_pred, int tile_infer, int tile_weight);
 
+/* Tile configurations of the wide path (the tuning surface of
+ * IPC_PATH_WIDE plans, the counterpart of the reference's per-shape
+ * KernelConfig search, scripts/autotune.py:51-131).  ipc_plan_wide_config_count
+ * gives the configurations a phase offers (IPC_PHASE_PRED with split
+ * IPC_SPLIT_NONE or IPC_SPLIT_W, IPC_PHASE_INFER, IPC_PHASE_WEIGHT); 0 is the
+ * default, and every configuration of a phase gives bit-identical results.
+ * ipc_plan_set_wide_config selects one per phase (-1 = default) and the
+ * number of k-slices of the output layer's prediction (-1 = chosen at bind
+ * from the device's CU count; 1 = none; else a power of two up to 16).  It is
+ * called after ipc_plan_create and before ipc_plan_workspace_bytes /
+ * ipc_plan_bind (the prediction tile sets the workspace size); a k-split the
+ * net cannot take fails at bind with IPC_ERR_CONFIG. */
+int ipc_plan_wide_config_count(int phase, int split);
+int ipc_plan_set_wide_config(ipc_plan* plan, int pred_cfg, int infer_cfg, int weight_cfg, int ksplit);
+
 /* Kernel launches one ipc_plan_step(steps=1) enqueues. */
 int ipc_plan_launch_count(const ipc_plan* plan);
 

@@ -418,6 +418,8 @@ struct ipc_plan {
   bool wide = false;
   std::vector<WideProblem> wpred, winfer, wweight, wfwd;  // wfwd: l = L-1 .. 1
   int pred_ksplit = 1;                                    // > 1: layer 0's prediction is k-split (last in wpred)
+  int wcfg[3] = {0, 0, 0};                                // tile configuration of the pred / infer / weight launches
+  int ksplit_request = 0;                                 // > 0: layer 0's k-split as set by the caller (1 = none)
   WideReduce wreduce{};                                   // its epilogue
   std::vector<WideCopy> wsync, wsync_init;               // wsync_init: W and x[L] only
   long long ws_bytes = 0;
@@ -541,7 +543,7 @@ struct WideLayout {
     total += wide_pad(b.rows * b.ld * 2, 256);
     return b;
   }
-  WideLayout(const std::vector<int>& d, int L, int B, bool split2) {
+  WideLayout(const std::vector<int>& d, int L, int B, bool split2, int pred_cfg) {
     wh.resize(L); wl.resize(L); wt.resize(L); f.resize(L + 1); ft.resize(L + 1); e.resize(L); et.resize(L);
     for (int l = 0; l < L; ++l) {
       wh[l] = add(d[l], d[l + 1]);                  // [d_l][d_{l+1}]  pred A
@@ -558,7 +560,7 @@ struct WideLayout {
     }
     // the k-split prediction cuts layer 0's tiles into at most 512 slices in all
     int bm = 0, bn = 0;
-    wide_pred_tile(split2 ? 2 : 1, &bm, &bn);
+    wide_pred_tile(split2 ? 2 : 1, pred_cfg, &bm, &bn);
     const long long t0 = ((d[0] + bm - 1) / bm) * (long long)((B + bn - 1) / bn);
     for (int sl = 16; sl >= 2; sl /= 2)
       if (sl * t0 <= 512 && wh[0].ld % (sl * WIDE_BK) == 0) { part_smax = sl; break; }
@@ -576,9 +578,10 @@ struct WideLayout {
 // slices), one workgroup per CU, each tile costing its k-steps and each slice
 // two more (prologue and partial-product store); a split pays four k-steps
 // for the reduce launch.
-int wide_pred_ksplit(const std::vector<int>& d, int L, int B, bool split2, const WideLayout& lay, int ncu) {
+int wide_pred_ksplit(const std::vector<int>& d, int L, int B, bool split2, int pred_cfg, const WideLayout& lay,
+                     int ncu) {
   int bm = 0, bn = 0;
-  wide_pred_tile(split2 ? 2 : 1, &bm, &bn);
+  wide_pred_tile(split2 ? 2 : 1, pred_cfg, &bm, &bn);
   auto tiles = [&](int l) { return ((d[l] + bm - 1) / bm) * (long long)((B + bn - 1) / bn); };
   auto makespan = [&](int sl) {
     std::priority_queue<double, std::vector<double>, std::greater<double>> cu;
@@ -780,7 +783,7 @@ int ipc_plan_create(ipc_plan** out, int L, const int* dims, int B, int storage, 
     p->res_ws_off = (p->ws_bytes + 255) / 256 * 256;
     p->ws_bytes = p->res_ws_off + res_bytes;
   }
-  if (p->wide) p->ws_bytes = WideLayout(p->dims, L, B, p->split == IPC_SPLIT_W).total;
+  if (p->wide) p->ws_bytes = WideLayout(p->dims, L, B, p->split == IPC_SPLIT_W, 0).total;
   *out = p;
   return ok();
 }
@@ -863,7 +866,7 @@ int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w
     plan->launches = 1;
   }
   if (plan->wide) {
-    const WideLayout lay(d, L, B, plan->split == IPC_SPLIT_W);
+    const WideLayout lay(d, L, B, plan->split == IPC_SPLIT_W, plan->wcfg[0]);
     char* ws = static_cast<char*>(workspace);
     auto buf = [&](const WideLayout::Buf& b) -> void* { return b.off < 0 ? nullptr : ws + b.off; };
     auto a16 = [](const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
@@ -885,7 +888,14 @@ int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
       ncu = 256;
-    plan->pred_ksplit = wide_pred_ksplit(d, L, B, plan->split == IPC_SPLIT_W, lay, ncu);
+    plan->pred_ksplit = wide_pred_ksplit(d, L, B, plan->split == IPC_SPLIT_W, plan->wcfg[0], lay, ncu);
+    if (plan->ksplit_request > 0) {
+      const int k = plan->ksplit_request;
+      if (k > lay.part_smax || (k > 1 && lay.wh[0].ld % ((long long)k * WIDE_BK) != 0))
+        return fail(IPC_ERR_CONFIG, "k-split %d is not available for this net (at most %d slices of whole k-steps)",
+                    k, lay.part_smax);
+      plan->pred_ksplit = k;
+    }
     if (plan->pred_ksplit > 1) {
       // layer 0 last, as slices writing partial products; the reduce launch writes eps[0], E, ET
       for (int l = 1; l < L; ++l) plan->wpred.push_back(pred_layer[l]);
@@ -981,16 +991,17 @@ int run_phase(ipc_plan* plan, int phase, hipStream_t s) {
     switch (phase) {
       case IPC_PHASE_PRED:
         TRY(launch_rc(launch_wide(WIDE_PRED, plan->wpred.data(), (int)plan->wpred.size(), plan->operand,
-                                  plan->split == IPC_SPLIT_W ? 2 : 1, plan->act, s), "wide prediction phase"));
+                                  plan->split == IPC_SPLIT_W ? 2 : 1, plan->act, s, plan->wcfg[0]),
+                      "wide prediction phase"));
         if (plan->pred_ksplit > 1)
           return launch_rc(launch_wide_reduce(plan->wreduce, plan->operand, s), "wide prediction reduce");
         return ok();
       case IPC_PHASE_INFER:
         return launch_rc(launch_wide(WIDE_INFER, plan->winfer.data(), (int)plan->winfer.size(), plan->operand, 1,
-                                     plan->act, s), "wide inference phase");
+                                     plan->act, s, plan->wcfg[1]), "wide inference phase");
       default:
         return launch_rc(launch_wide(WIDE_WEIGHT, plan->wweight.data(), (int)plan->wweight.size(), plan->operand, 1,
-                                     plan->act, s), "wide weight phase");
+                                     plan->act, s, plan->wcfg[2]), "wide weight phase");
     }
   }
   switch (phase) {
@@ -1092,6 +1103,33 @@ int ipc_plan_set_tiles(ipc_plan* plan, int tile_pred, int tile_infer, int tile_w
 }
 
 int ipc_plan_launch_count(const ipc_plan* plan) { return plan ? plan->launches : 0; }
+
+int ipc_plan_wide_config_count(int phase, int split) {
+  if (phase == IPC_PHASE_PRED) return split == IPC_SPLIT_W ? wide_config_count(WIDE_PRED, 2)
+                                                           : split == IPC_SPLIT_NONE ? wide_config_count(WIDE_PRED, 1) : 0;
+  if (phase == IPC_PHASE_INFER) return wide_config_count(WIDE_INFER, 1);
+  if (phase == IPC_PHASE_WEIGHT) return wide_config_count(WIDE_WEIGHT, 1);
+  return 0;
+}
+
+int ipc_plan_set_wide_config(ipc_plan* plan, int pred_cfg, int infer_cfg, int weight_cfg, int ksplit) {
+  if (!plan) return fail(IPC_ERR_NULL, "plan is NULL");
+  if (!plan->wide) return fail(IPC_ERR_CONFIG, "the plan does not run the wide path");
+  if (plan->bound) return fail(IPC_ERR_STATE, "set the wide configuration before ipc_plan_bind");
+  const int c[3] = {pred_cfg, infer_cfg, weight_cfg};
+  for (int ph = 0; ph < 3; ++ph) {
+    const int n = ipc_plan_wide_config_count(ph, plan->split);
+    if (c[ph] < -1 || c[ph] >= n)
+      return fail(IPC_ERR_CONFIG, "phase %d has tile configurations 0..%d (-1 = default); got %d", ph, n - 1, c[ph]);
+  }
+  if (ksplit < -1 || ksplit == 0 || ksplit > 16 || (ksplit > 0 && (ksplit & (ksplit - 1))))
+    return fail(IPC_ERR_CONFIG, "k-split must be -1 (automatic) or a power of two in [1, 16]; got %d", ksplit);
+  for (int ph = 0; ph < 3; ++ph) plan->wcfg[ph] = c[ph] < 0 ? 0 : c[ph];
+  plan->ksplit_request = ksplit < 0 ? 0 : ksplit;
+  // the prediction tile sets how many k-split slices the workspace holds
+  plan->ws_bytes = WideLayout(plan->dims, plan->L, plan->B, plan->split == IPC_SPLIT_W, plan->wcfg[0]).total;
+  return ok();
+}
 
 int ipc_plan_set_spin_limit(ipc_plan* plan, int limit) {
   if (!plan) return fail(IPC_ERR_NULL, "plan is NULL");

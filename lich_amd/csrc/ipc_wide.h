@@ -94,14 +94,19 @@ struct WideReduce {
 };
 hipError_t launch_wide_reduce(const WideReduce& r, int operand, hipStream_t s);
 
-// Output tile of the prediction kernel for `split` (1 or 2).
-void wide_pred_tile(int split, int* bm, int* bn);
+// Tile configurations a phase offers (WIDE_PRED with split 1 or 2,
+// WIDE_INFER, WIDE_WEIGHT; 1 for WIDE_FWD); configuration 0 is the default.
+int wide_config_count(int mode, int split);
+
+// Output tile of prediction configuration `cfg` for `split` (1 or 2).
+void wide_pred_tile(int split, int cfg, int* bm, int* bn);
 
 // Launches one phase of the wide path over `count` layers (one launch per
-// WIDE_MAX_BATCH layers).  `operand` is DT_F16 or DT_BF16, `split` 1 or 2
-// (pred and fwd), `act` the activation of the infer / fwd epilogues.
+// WIDE_MAX_BATCH layers) on tile configuration `cfg`.  `operand` is DT_F16
+// or DT_BF16, `split` 1 or 2 (pred and fwd), `act` the activation of the
+// infer / fwd epilogues.
 hipError_t launch_wide(int mode, const WideProblem* probs, int count, int operand, int split, int act,
-                       hipStream_t s);
+                       hipStream_t s, int cfg = 0);
 
 // Raises the dynamic-LDS limit of every wide-path kernel instantiation.
 hipError_t wide_prepare();

@@ -9,72 +9,77 @@ namespace {
 
 using dma::Cfg;
 
-// BM, BN, stages, waves along M, waves along N
-#ifndef WIDE_PRED1_CFG
-#define WIDE_PRED1_CFG 256, 128, 3, 4, 2
-#endif
-// split-2 prediction: 128 x 256 tiles, waves 2 x 4, 2 stages (128 KiB of LDS); the
-// k-split of the output layer fills the last round.  Measured on the wide
-// configuration: 281 us per prediction against 317 us on 128 x 128 tiles (3 stages)
-// and 349 us on 256 x 128 tiles (2 stages, all of the LDS).
-#ifndef WIDE_PRED2_CFG
-#define WIDE_PRED2_CFG 128, 256, 2, 2, 4
-#endif
-// inference and weight update: 128 x 256 tiles, waves 2 x 4 (64 x 64 each, as in
-// 256 x 128 / 4 x 2).  Measured on the wide configuration: inference 183 -> 177 us,
-// weight update 353 -> 330 us, whole step 0.922-0.929 -> 0.911-0.916 ms.
-#ifndef WIDE_INFER_CFG
-#define WIDE_INFER_CFG 128, 256, 3, 2, 4
-#endif
-#ifndef WIDE_WEIGHT_CFG
-#define WIDE_WEIGHT_CFG 128, 256, 3, 2, 4
-#endif
+// Tile configurations (BM, BN, stages, waves along M, waves along N) of each
+// phase; index 0 is the default, the others are the alternatives a plan can
+// select (ipc_plan_set_wide_config) after tuning.  The configurations of one
+// phase give bit-identical results: every output element sums its
+// contraction in the same k order whatever the tile.
+//   split-1 prediction: 256 x 128 (3 stages, waves 4 x 2); 128 x 256 (3, 2 x 4)
+//   split-2 prediction: 128 x 256 (2 stages, waves 2 x 4): 281 us per launch on the wide
+//       configuration against 317 us for 128 x 128 (3 stages, 4 x 2), the alternative;
+//       256 x 128 (2 stages) measured 349 us
+//   inference: 128 x 256 (3, 2 x 4): 177 us against 183 us for 256 x 128 (3, 4 x 2)
+//   weight update: 128 x 256 (3, 2 x 4): 330 us against 353 us for 256 x 128 (3, 4 x 2)
+//       and 128 x 128 (4 stages, 4 x 2)
+#define WIDE_PRED1_CFGS(X) X(256, 128, 3, 4, 2) X(128, 256, 3, 2, 4)
+#define WIDE_PRED2_CFGS(X) X(128, 256, 2, 2, 4) X(128, 128, 3, 4, 2)
+#define WIDE_INFER_CFGS(X) X(128, 256, 3, 2, 4) X(256, 128, 3, 4, 2)
+#define WIDE_WEIGHT_CFGS(X) X(128, 256, 3, 2, 4) X(256, 128, 3, 4, 2) X(128, 128, 4, 4, 2)
+#define IPC_COUNT1(...) +1
+constexpr int kPred1Cfgs = 0 WIDE_PRED1_CFGS(IPC_COUNT1), kPred2Cfgs = 0 WIDE_PRED2_CFGS(IPC_COUNT1);
+constexpr int kInferCfgs = 0 WIDE_INFER_CFGS(IPC_COUNT1), kWeightCfgs = 0 WIDE_WEIGHT_CFGS(IPC_COUNT1);
 
-template <typename OT, int ACT> using PredCfg1 = Cfg<OT, WIDE_PRED, 1, ACT_IDENTITY, false, WIDE_PRED1_CFG>;
-template <typename OT, int ACT> using PredCfg2 = Cfg<OT, WIDE_PRED, 2, ACT_IDENTITY, false, WIDE_PRED2_CFG>;
-template <typename OT, int ACT> using InferCfg = Cfg<OT, WIDE_INFER, 1, ACT, false, WIDE_INFER_CFG>;
-template <typename OT, int ACT> using WeightCfg = Cfg<OT, WIDE_WEIGHT, 1, ACT_IDENTITY, false, WIDE_WEIGHT_CFG>;
-// forward initialisation: the pred tiles (one layer per launch)
-template <typename OT, int ACT> using FwdCfg1 = Cfg<OT, WIDE_FWD, 1, ACT, false, WIDE_PRED1_CFG>;
-// (one layer per launch: the 128 x 128 tiles of one 4096-row layer fill all CUs once,
-// 82 us per layer against 120 us on the prediction's 128 x 256 tiles; the sums per
+// forward initialisation: the split-1 prediction tiles; split 2 keeps 128 x 128
+// (one layer per launch: its tiles fill all CUs once per 4096-row layer, 82 us
+// per layer against 120 us on the prediction's 128 x 256 tiles; the sums per
 // element do not depend on the tile, so the first prediction errors stay exactly 0)
-#ifndef WIDE_FWD2_CFG
-#define WIDE_FWD2_CFG 128, 128, 3, 4, 2
-#endif
-template <typename OT, int ACT> using FwdCfg2 = Cfg<OT, WIDE_FWD, 2, ACT, false, WIDE_FWD2_CFG>;
+template <typename OT, int ACT> using FwdCfg1 = Cfg<OT, WIDE_FWD, 1, ACT, false, 256, 128, 3, 4, 2>;
+template <typename OT, int ACT> using FwdCfg2 = Cfg<OT, WIDE_FWD, 2, ACT, false, 128, 128, 3, 4, 2>;
+
+// Launches (or prepares) configuration `cfg` of a list: the i-th X(...) entry.
+#define IPC_CFG_CASE(MODE_, SPLIT_, ACT_, BM_, BN_, S_, WM_, WN_)                                     \
+  if (cfg == i++) return prep ? Cfg<OT, MODE_, SPLIT_, ACT_, false, BM_, BN_, S_, WM_, WN_>::prepare()   \
+                              : Cfg<OT, MODE_, SPLIT_, ACT_, false, BM_, BN_, S_, WM_, WN_>::launch(probs, count, s);
+#define IPC_P1(BM_, BN_, S_, WM_, WN_) IPC_CFG_CASE(WIDE_PRED, 1, ACT_IDENTITY, BM_, BN_, S_, WM_, WN_)
+#define IPC_P2(BM_, BN_, S_, WM_, WN_) IPC_CFG_CASE(WIDE_PRED, 2, ACT_IDENTITY, BM_, BN_, S_, WM_, WN_)
+#define IPC_IN(BM_, BN_, S_, WM_, WN_) IPC_CFG_CASE(WIDE_INFER, 1, ACT, BM_, BN_, S_, WM_, WN_)
+#define IPC_WT(BM_, BN_, S_, WM_, WN_) IPC_CFG_CASE(WIDE_WEIGHT, 1, ACT_IDENTITY, BM_, BN_, S_, WM_, WN_)
 
 template <typename OT>
 struct Phase {
   template <int ACT>
   struct Run {
-    static hipError_t run(int mode, int split, const WideProblem* probs, int count, hipStream_t s) {
+    // prep: raise the LDS limit of configuration `cfg` instead of launching it
+    static hipError_t run(int mode, int split, int cfg, bool prep, const WideProblem* probs, int count,
+                          hipStream_t s) {
+      int i = 0;
       switch (mode) {
         case WIDE_PRED:
-          return split == 2 ? PredCfg2<OT, ACT>::launch(probs, count, s) : PredCfg1<OT, ACT>::launch(probs, count, s);
-        case WIDE_INFER: return InferCfg<OT, ACT>::launch(probs, count, s);
-        case WIDE_FWD:
+          if (split == 2) { WIDE_PRED2_CFGS(IPC_P2) }
+          else { WIDE_PRED1_CFGS(IPC_P1) }
+          return hipErrorInvalidValue;
+        case WIDE_INFER: { WIDE_INFER_CFGS(IPC_IN) } return hipErrorInvalidValue;
+        case WIDE_WEIGHT: { WIDE_WEIGHT_CFGS(IPC_WT) } return hipErrorInvalidValue;
+        default:  // WIDE_FWD
+          if (prep) return split == 2 ? FwdCfg2<OT, ACT>::prepare() : FwdCfg1<OT, ACT>::prepare();
           return split == 2 ? FwdCfg2<OT, ACT>::launch(probs, count, s) : FwdCfg1<OT, ACT>::launch(probs, count, s);
-        default: return WeightCfg<OT, ACT>::launch(probs, count, s);
       }
-    }
-  };
-  template <int ACT>
-  struct Prep {
-    static hipError_t run() {
-      hipError_t e;
-      if ((e = InferCfg<OT, ACT>::prepare()) != hipSuccess) return e;
-      if ((e = FwdCfg1<OT, ACT>::prepare()) != hipSuccess) return e;
-      return FwdCfg2<OT, ACT>::prepare();
     }
   };
   static hipError_t prepare() {
     hipError_t e;
-    if ((e = PredCfg1<OT, 0>::prepare()) != hipSuccess) return e;
-    if ((e = PredCfg2<OT, 0>::prepare()) != hipSuccess) return e;
-    if ((e = WeightCfg<OT, 0>::prepare()) != hipSuccess) return e;
-    for (int act = 0; act < 6; ++act)
-      if ((e = dma::by_act<Prep>(act)) != hipSuccess) return e;
+    for (int act = 0; act < 6; ++act) {
+      for (int c = 0; c < kInferCfgs; ++c)
+        if ((e = dma::by_act<Run>(act, WIDE_INFER, 1, c, true, nullptr, 0, nullptr)) != hipSuccess) return e;
+      for (int sp = 1; sp <= 2; ++sp)
+        if ((e = dma::by_act<Run>(act, WIDE_FWD, sp, 0, true, nullptr, 0, nullptr)) != hipSuccess) return e;
+    }
+    for (int c = 0; c < kPred1Cfgs; ++c)
+      if ((e = Run<0>::run(WIDE_PRED, 1, c, true, nullptr, 0, nullptr)) != hipSuccess) return e;
+    for (int c = 0; c < kPred2Cfgs; ++c)
+      if ((e = Run<0>::run(WIDE_PRED, 2, c, true, nullptr, 0, nullptr)) != hipSuccess) return e;
+    for (int c = 0; c < kWeightCfgs; ++c)
+      if ((e = Run<0>::run(WIDE_WEIGHT, 1, c, true, nullptr, 0, nullptr)) != hipSuccess) return e;
     return hipSuccess;
   }
 };
@@ -239,8 +244,8 @@ __global__ void __launch_bounds__(256) wide_reduce_kernel(const WideReduce r) {
 }
 
 template <typename OT>
-hipError_t launch_phase(int mode, const WideProblem* probs, int count, int split, int act, hipStream_t s) {
-  return dma::by_act<Phase<OT>::template Run>(act, mode, split, probs, count, s);
+hipError_t launch_phase(int mode, const WideProblem* probs, int count, int split, int act, int cfg, hipStream_t s) {
+  return dma::by_act<Phase<OT>::template Run>(act, mode, split, cfg, false, probs, count, s);
 }
 
 }  // namespace
@@ -252,12 +257,13 @@ hipError_t wide_prepare() {
 }
 
 hipError_t launch_wide(int mode, const WideProblem* probs, int count, int operand, int split, int act,
-                       hipStream_t s) {
+                       hipStream_t s, int cfg) {
+  if (cfg < 0 || cfg >= wide_config_count(mode, split)) return hipErrorInvalidValue;
   for (int base = 0; base < count; base += WIDE_MAX_BATCH) {
     const int n = count - base < WIDE_MAX_BATCH ? count - base : WIDE_MAX_BATCH;
     hipError_t e;
-    if (operand == DT_F16) e = launch_phase<f16>(mode, probs + base, n, split, act, s);
-    else if (operand == DT_BF16) e = launch_phase<bf16>(mode, probs + base, n, split, act, s);
+    if (operand == DT_F16) e = launch_phase<f16>(mode, probs + base, n, split, act, cfg, s);
+    else if (operand == DT_BF16) e = launch_phase<bf16>(mode, probs + base, n, split, act, cfg, s);
     else return hipErrorInvalidValue;
     if (e != hipSuccess) return e;
   }
@@ -276,14 +282,21 @@ hipError_t launch_wide_reduce(const WideReduce& r, int operand, hipStream_t s) {
   return hipGetLastError();
 }
 
-void wide_pred_tile(int split, int* bm, int* bn) {
-  if (split == 2) {
-    *bm = PredCfg2<bf16, 0>::BM_;
-    *bn = PredCfg2<bf16, 0>::BN_;
-  } else {
-    *bm = PredCfg1<bf16, 0>::BM_;
-    *bn = PredCfg1<bf16, 0>::BN_;
+int wide_config_count(int mode, int split) {
+  switch (mode) {
+    case WIDE_PRED: return split == 2 ? kPred2Cfgs : kPred1Cfgs;
+    case WIDE_INFER: return kInferCfgs;
+    case WIDE_WEIGHT: return kWeightCfgs;
+    default: return 1;
   }
+}
+
+#define IPC_TILE_XY(BM_, BN_, S_, WM_, WN_) if (cfg == i++) { *bm = BM_; *bn = BN_; return; }
+void wide_pred_tile(int split, int cfg, int* bm, int* bn) {
+  int i = 0;
+  if (split == 2) { WIDE_PRED2_CFGS(IPC_TILE_XY) }
+  else { WIDE_PRED1_CFGS(IPC_TILE_XY) }
+  *bm = *bn = 0;
 }
 
 hipError_t launch_wide_copy(const WideCopy* copies, int count, int operand, hipStream_t s) {

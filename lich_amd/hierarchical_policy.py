@@ -150,6 +150,17 @@ class HierarchicalPolicy:
     def selected_recompute_activation(self, *, default: bool, **kw) -> bool:
         return bool(self._best(**kw).get("recompute_activation", default))
 
+    def selected_wide_config(self, *, default, **kw):
+        """The entry's wide-path tile configuration ``(pred, infer, weight,
+        ksplit)`` (written by ``lich_amd.autotune``), else ``default``."""
+        wc = self._best(**kw).get("wide_config")
+        if not isinstance(wc, dict):
+            return default
+        try:
+            return tuple(int(wc.get(k, -1)) for k in ("pred", "infer", "weight", "ksplit"))
+        except (TypeError, ValueError):
+            return default
+
     def selected_use_graph(self, *, default: bool, **kw) -> bool:
         return bool(self._best(**kw).get("use_cuda_graph", default))
 

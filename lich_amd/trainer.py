@@ -76,6 +76,9 @@ class IPCConfig:
     # latency-bound whole-step kernel, where the extra MFMAs are free) and 2
     # otherwise (the MFMA-bound wide path).
     pred_split: int | None = None
+    # Wide path tile configuration (pred, infer, weight, ksplit), -1 = default
+    # (ipc_plan_set_wide_config); a policy file's tuned choice takes precedence.
+    wide_config: tuple[int, int, int, int] | None = None
     # Kernel path: "auto" (the layer-resident whole-step kernel when eligible,
     # else the column-block whole-step kernel for narrow nets, else the wide
     # GEMM path when eligible, else phased), "resident", "narrow" / "on",
@@ -176,6 +179,7 @@ class HipIPC:
             except (OSError, ValueError):
                 self._hierarchical_policy = None
         self._runtime_recompute: bool = bool(cfg.recompute_activation)
+        self.wide_config = cfg.wide_config
         self.grid_z_cap: int = max(0, int(cfg.grid_z_max_layers))
         self.layer_groups = self._groups_for(self.grid_z_cap)
         self._signature_cache: dict[int, str] = {}
@@ -239,11 +243,13 @@ class HipIPC:
         ``trainer.py:158-177`` and ``:273-300``): the hierarchical policy
         first, then for grid.z the grid.z policy file keyed by this device."""
         self._runtime_recompute = bool(self.cfg.recompute_activation)
+        self.wide_config = self.cfg.wide_config
         cap = None
         pol = self._hierarchical_policy
         if pol is not None:
             kw = self._policy_kw(B)
             self._runtime_recompute = pol.selected_recompute_activation(default=self._runtime_recompute, **kw)
+            self.wide_config = pol.selected_wide_config(default=self.wide_config, **kw)
             if self.cfg.use_grid_z and self.cfg.grid_z_auto:
                 cap = pol.selected_grid_z(default=None, **kw)
         if cap is None and self.cfg.use_grid_z and self.cfg.grid_z_auto:
@@ -302,6 +308,8 @@ class HipIPC:
             self._fused))
         self._plan = handle
         nat.check(nat.lib().ipc_plan_set_tiles(handle, *self.phase_tiles(B)))
+        if self.wide_config is not None and int(nat.lib().ipc_plan_path(handle)) == nat.PATH_WIDE:
+            nat.check(nat.lib().ipc_plan_set_wide_config(handle, *[int(v) for v in self.wide_config]))
         nbytes = int(nat.lib().ipc_plan_workspace_bytes(handle))
         # zero-initialised (the wide path relies on zero padding); torch's
         # allocations are 256-byte aligned as the plan requires

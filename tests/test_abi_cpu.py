@@ -473,3 +473,32 @@ def test_noalloc_entry_point_validates_on_the_host():
     assert "scratch" in nat.last_error()
     # zero steps of an acceptable net: validated, nothing enqueued
     assert lib.ipc_steps_noalloc(*args, 0, None) == nat.IPC_OK
+
+
+def test_wide_tile_configurations_are_selectable_before_bind():
+    lib = _lib()
+    assert lib.ipc_plan_wide_config_count(0, nat.SPLIT_W) == 2 and lib.ipc_plan_wide_config_count(0, 1) == 2
+    assert lib.ipc_plan_wide_config_count(1, 1) == 2 and lib.ipc_plan_wide_config_count(2, 1) == 3
+    assert lib.ipc_plan_wide_config_count(0, nat.SPLIT_WX) == 0 and lib.ipc_plan_wide_config_count(7, 1) == 0
+    assert lib.ipc_plan_set_wide_config(None, 0, 0, 0, -1) == nat.ERR_NULL
+    dims = (ctypes.c_int * 4)(10, 64, 64, 784)
+    h = ctypes.c_void_p()
+    assert lib.ipc_plan_create(ctypes.byref(h), 3, dims, 128, 0, 0, 1, 2, 1e-4, 0.5, 1, 0, -1) == nat.IPC_OK
+    try:  # not a wide plan
+        assert lib.ipc_plan_set_wide_config(h, 0, 0, 0, -1) == nat.ERR_CONFIG
+    finally:
+        lib.ipc_plan_destroy(h)
+    wide = (ctypes.c_int * 4)(1000, 4096, 4096, 4096)
+    assert lib.ipc_plan_create(ctypes.byref(h), 3, wide, 1024, 0, 2, 2, 2, 1e-4, 0.5, 1, 0, nat.PATH_WIDE) == nat.IPC_OK
+    try:
+        base = lib.ipc_plan_workspace_bytes(h)
+        assert lib.ipc_plan_set_wide_config(h, 2, 0, 0, -1) == nat.ERR_CONFIG   # split-2 prediction has 0..1
+        assert lib.ipc_plan_set_wide_config(h, 0, 0, 3, -1) == nat.ERR_CONFIG   # weight has 0..2
+        assert lib.ipc_plan_set_wide_config(h, 0, 0, 0, 3) == nat.ERR_CONFIG    # not a power of two
+        assert lib.ipc_plan_set_wide_config(h, -1, 1, 2, 8) == nat.IPC_OK
+        assert lib.ipc_plan_workspace_bytes(h) == base                          # same prediction tile
+        # the 128 x 128 prediction tile: twice the output tiles of layer 0, half the slices
+        assert lib.ipc_plan_set_wide_config(h, 1, 0, 0, -1) == nat.IPC_OK
+        assert lib.ipc_plan_workspace_bytes(h) < base
+    finally:
+        lib.ipc_plan_destroy(h)

@@ -87,3 +87,14 @@ def test_build_targets_gfx950_only():
     text = (PKG / "build.py").read_text()
     assert 'ARCH = "gfx950"' in text and "--offload-arch" in text
     assert "-packed-fp32-ops" in text
+
+
+def test_only_the_cli_uses_the_cpu_reference_api():
+    """lich_amd.reference (the reference's pure-PyTorch API) serves the CLI's
+    reference command and the tuner's correctness probe; no training or
+    kernel module calls it."""
+    for path in PY_FILES:
+        if path.name in ("reference.py", "cli.py", "autotune.py"):
+            continue
+        text = path.read_text()
+        assert "from .reference" not in text and "lich_amd.reference" not in text, path
