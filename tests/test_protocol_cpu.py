@@ -1,0 +1,46 @@
+"""Exhaustive interleaving checks of the whole-step kernels' synchronisation
+schedules (tests/protocol_model.py): every read of an exchange slot sees the
+step it must see, no schedule deadlocks, the column kernel's counters are
+clear for the next launch, and each planted mistake (a dropped wait, a
+counter left uncleared, one buffer too few next to the top layer, a missing
+peer) is caught."""
+import pytest
+
+from protocol_model import Violation, column_kernel, resident_kernel
+
+
+@pytest.mark.parametrize("nblocks,ntile,steps", [(3, 3, 3), (2, 3, 2), (1, 2, 3), (3, 2, 2)])
+def test_column_kernel_barriers(nblocks, ntile, steps):
+    assert column_kernel(nblocks, ntile, steps, launches=2).explore() > 1
+
+
+def test_column_kernel_without_the_first_wait_reads_stale_eps():
+    with pytest.raises(Violation, match="read"):
+        column_kernel(2, 2, 2, launches=1, drop_barrier=True).explore()
+
+
+@pytest.mark.parametrize("clears", [("bar1",), ("bar0",)])
+def test_column_kernel_exit_must_clear_both_counters(clears):
+    with pytest.raises(Violation):
+        column_kernel(2, 2, 2, launches=2, exit_clears=clears).explore()
+
+
+@pytest.mark.parametrize("hidden,chunks,halves,steps", [
+    (1, 2, 1, 4), (2, 2, 1, 3), (3, 1, 1, 4), (2, 1, 2, 3), (1, 1, 2, 4), (1, 3, 1, 3), (2, 2, 2, 3)])
+def test_resident_kernel_exchange(hidden, chunks, halves, steps):
+    assert resident_kernel(hidden, chunks, halves, steps).explore() > 1
+
+
+@pytest.mark.parametrize("mistake", [
+    dict(g_buffers_top=2),            # W^T eps next to the top layer double- instead of triple-buffered
+    dict(top_waits_l2=False),         # top chunks do not wait for workgroup L-2
+    dict(chunk0_waits_siblings=False),  # chunk 0 sums partials its siblings have not published
+])
+def test_resident_kernel_planted_mistakes_next_to_the_top(mistake):
+    with pytest.raises(Violation):
+        resident_kernel(1, 2, 1, 4, **mistake).explore()
+
+
+def test_resident_kernel_planted_mistake_between_hidden_layers():
+    with pytest.raises(Violation):
+        resident_kernel(3, 1, 1, 3, hidden_waits_up=False).explore()
