@@ -521,6 +521,50 @@ __device__ __forceinline__ void setup(const Resident<OT, SPLIT, ACT>& k, const R
   __syncthreads();
 }
 
+// The states a hidden workgroup leaves after the last step: eps[l]; x[l]
+// (l >= 1); f(x[l+1]) from the values staged for the weight update (workgroup
+// l + 1 holds the same x[l+1], so each f(x) is written once and no activation
+// is evaluated again); and, next to the top layer, x[L-1], whose last update
+// the top workgroups leave to this one (they apply each step's update one step
+// late).
+template <typename OT, int SPLIT, int ACT>
+__device__ __forceinline__ void write_states(Resident<OT, SPLIT, ACT>& k, const ResidentArgs& p,
+                                             const f32x4* ea, const f32x4* xa, const f32x4* xb, const f32x4* fb) {
+  const int l = k.l, B = k.B, wave = k.wave;
+  float* E = p.e[l];
+  float* X = l >= 1 ? p.x[l] : nullptr;
+  float* XU = l + 1 == k.L - 1 ? p.x[l + 1] : nullptr;
+  float* FU = p.fx[l + 1];
+#pragma unroll
+  for (int i = 0; i < MAXT; ++i) {
+    const int t = wave + NWV * i;
+    if (t < k.n_pred) {
+      const int b = k.tcol(t);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = k.trow(t, q);
+        if (r < k.M && b < B) {
+          const long long o = (long long)r * B + b;
+          gbl(E)[o] = ea[i][q];
+          if (X) gbl(X)[o] = xa[i][q];
+        }
+      }
+    }
+    if (t < k.n_inf) {
+      const int b = k.tcol(t);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = k.trow(t, q);
+        if (r < k.K && b < B) {
+          const long long o = (long long)r * B + b;
+          if (FU) gbl(FU)[o] = fb[i][q];
+          if (XU) gbl(XU)[o] = xb[i][q];
+        }
+      }
+    }
+  }
+}
+
 // Hidden layer l (0 <= l <= L-2): W[l] at the update tiles, x[l] at the
 // prediction tiles, x[l+1] at the inference tiles, all resident for the launch.
 template <typename OT, int SPLIT, int ACT>
@@ -654,6 +698,7 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
         fb[i] = k.stage_f4(k.trow(t, 0), k.tcol(t), xb[i]);
       }
     }
+    if (s + 1 == p.steps) write_states(k, p, ea, xa, xb, fb);  // overlaps the last weight update
     __syncthreads();
     // ---- 4. W[l] += alpha eps[l] f(x_new[l+1])^T
 #pragma unroll
@@ -675,27 +720,7 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
     __syncthreads();
   }
 
-  // ---- results: eps[l] of the last step, x[l] and f(x[l]) (l >= 1), W[l]
-  float* E = p.e[l];
-  float* X = l >= 1 ? p.x[l] : nullptr;
-  float* FX = l >= 1 ? p.fx[l] : nullptr;
-#pragma unroll
-  for (int i = 0; i < MAXT; ++i) {
-    const int t = wave + NWV * i;
-    if (t < npr) {
-      const int b = k.tcol(t);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int r = k.trow(t, q);
-        if (r < k.M && b < B) {
-          const long long o = (long long)r * B + b;
-          gbl(E)[o] = ea[i][q];
-          if (X) gbl(X)[o] = xa[i][q];
-          if (FX) gbl(FX)[o] = act_t<ACT>(xa[i][q]);
-        }
-      }
-    }
-  }
+  // ---- results: W[l] (the states went out before the last weight update)
 #pragma unroll
   for (int i = 0; i < MU; ++i) {
     const int t = wave + NWV * i;
@@ -705,28 +730,6 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
       for (int q = 0; q < 4; ++q) {
         const int r = k.urt(t) * 16 + 4 * lg + q;
         if (r < k.M && c < k.K) gbl(p.w[l])[(long long)r * k.ldw_g + c] = wr[i][q];
-      }
-    }
-  }
-  if (from_top) {
-    // x[L-1] after the last step: the top workgroups apply each step's update
-    // one step late, so the final one is written here, from this workgroup's copy
-    float* XU = p.x[l + 1];
-    float* FXU = p.fx[l + 1];
-#pragma unroll
-    for (int i = 0; i < MAXT; ++i) {
-      const int t = wave + NWV * i;
-      if (t < ninf) {
-        const int b = k.tcol(t);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int r = k.trow(t, q);
-          if (r < k.K && b < B) {
-            const long long o = (long long)r * B + b;
-            gbl(XU)[o] = xb[i][q];
-            if (FXU) gbl(FXU)[o] = act_t<ACT>(xb[i][q]);
-          }
-        }
       }
     }
   }
@@ -953,21 +956,25 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
 }
 
 // XCD-aware placement.  Blocks are dealt to the eight XCDs round-robin by
-// block index, so the top workgroups of row block h take blocks h, h + 8,
-// h + 16, ... (one XCD per row block: each of them reads all its siblings'
-// partial products every step, and those reads then share one L2) and the
-// hidden workgroups the other XCDs' blocks; the spare blocks of the grid exit
-// at once.  Placement only affects speed: every exchange is ordered at agent
-// scope wherever the workgroups run.
+// block index, so the top workgroups of row block h take blocks 7 - h,
+// 15 - h, 23 - h, ... (one XCD per row block: each of them reads all its
+// siblings' partial products every step, and those reads then share one L2)
+// and the hidden workgroups the blocks of the other XCDs, the lower ones
+// first: the XCDs start their first blocks in index order, and the hidden
+// chain sets the pace while the top chunks may run a step ahead.  The spare
+// blocks of the grid exit at once.  Placement only affects speed: every
+// exchange is ordered at agent scope wherever the workgroups run.
 __host__ __device__ inline int resident_role(int bid, int hidden, int chunks, int halves) {
-  const int x = bid & 7, i = bid >> 3;
+  const int x = 7 - (bid & 7), i = bid >> 3;  // x: XCD counted from the last
   if (x < halves) return i < chunks ? hidden + x * chunks + i : -1;
   const int l = i * (8 - halves) + (x - halves);
   return l < hidden ? l : -1;
 }
 inline int resident_grid(int hidden, int chunks, int halves) {
-  const int top = 8 * (chunks - 1) + halves;
-  const int low = hidden > 0 ? 8 * ((hidden - 1) / (8 - halves)) + halves + (hidden - 1) % (8 - halves) + 1 : 0;
+  // the top chunks' blocks end at 8 * chunks - 1; the hidden workgroups fill
+  // XCDs 0 .. 7 - halves row by row of eight blocks
+  const int top = 8 * chunks;
+  const int low = hidden > 0 ? 8 * ((hidden - 1) / (8 - halves)) + 8 : 0;
   return top > low ? top : low;
 }
 
@@ -993,7 +1000,10 @@ __global__ void __launch_bounds__(NT) resident_kernel(const ResidentArgs args) {
   // last workgroup out clears the flags and the exit counter for the next launch
   __syncthreads();
   if (threadIdx.x == 0) {
-    const unsigned prev = __hip_atomic_fetch_add(&p.bar[1], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    // relaxed: a workgroup counts itself out after its last flag poll has
+    // returned (its value decided the loop), so the clearing below cannot be
+    // seen by a poll; the results' visibility is the kernel boundary's
+    const unsigned prev = __hip_atomic_fetch_add(&p.bar[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (prev == (unsigned)p.nwg - 1) {
       for (int w = 0; w < p.nwg + p.halves; ++w)
         __hip_atomic_store(&p.flags[w], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
