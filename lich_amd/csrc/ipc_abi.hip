@@ -610,11 +610,15 @@ bool narrow_outer(int B, int wmode) {
 }
 
 // Layer-resident kernel eligibility; fills `ra` and returns its workspace bytes, or -1.
+// fp32 operands run it with either weight update (the rank-B one as the column
+// kernel computes it); 16-bit operands with the GEMM update only.
 long long resident_eligible(int L, const int* dims, int B, int operand, int split, int wmode, bool narrow,
                             ResidentArgs& ra) {
-  if (!narrow || operand == IPC_DT_F32 || narrow_outer(B, wmode)) return -1;
-  if (split != IPC_SPLIT_NONE && split != IPC_SPLIT_WX) return -1;
-  return resident_plan(dims, L, B, split == IPC_SPLIT_WX ? 3 : 1, ra);
+  if (!narrow) return -1;
+  const bool outer = narrow_outer(B, wmode);
+  if (operand == IPC_DT_F32) return split == IPC_SPLIT_NONE ? resident_plan(dims, L, B, 1, 4, outer, ra) : -1;
+  if (outer || (split != IPC_SPLIT_NONE && split != IPC_SPLIT_WX)) return -1;
+  return resident_plan(dims, L, B, split == IPC_SPLIT_WX ? 3 : 1, 2, false, ra);
 }
 
 int launch_narrow_mode(ipc_plan* plan, int mode, int steps, hipStream_t s) {
@@ -730,8 +734,9 @@ int ipc_plan_create(ipc_plan** out, int L, const int* dims, int B, int storage, 
   long long res_bytes = resident_eligible(L, dims, B, operand, esplit, weight_mode, eligible, ra);
   if (path == IPC_PATH_RESIDENT && res_bytes < 0)
     return fail(IPC_ERR_CONFIG,
-                "the layer-resident kernel needs a narrow net with fp16/bf16 operands, split 1 or 3, L >= 2, "
-                "widths d_0..d_{L-1} <= %d, B <= %d and the GEMM weight update", RES_MAX_WIDTH, RES_MAX_B);
+                "the layer-resident kernel needs a narrow net with L >= 2, widths d_0..d_{L-1} <= %d, B <= %d, "
+                "operand blocks that fit the LDS, and fp16/bf16 operands with split 1 or 3 and the GEMM weight "
+                "update, or fp32 operands", RES_MAX_WIDTH, RES_MAX_B);
   // Every workgroup of a layer-resident launch waits for others, so all of
   // them must be able to run at once on this device (a compute-partitioned
   // device, or a smaller part, may hold fewer); otherwise an AUTO plan takes

@@ -87,11 +87,13 @@ __host__ __device__ inline void narrow_lds_layout(const int* dims, int L, int KS
 }
 
 // ---------------------------------------------------------------- layer-resident kernel
-// Multi-step launches of 16-bit-operand plans whose hidden widths are <= 64
-// and whose batch is <= 128 run a second whole-step kernel in which every
-// workgroup owns one layer's W for all steps (the top layer's W, with its
-// long input-width contraction, is split into column chunks owned by one
-// workgroup each) and exchanges only eps and W^T eps with its neighbours.
+// Multi-step launches of nets whose hidden widths are <= 64 run a second
+// whole-step kernel in which every workgroup owns one layer's W for all steps
+// (the top layer's W, with its long input-width contraction, is split into
+// column chunks owned by one workgroup each) and exchanges only eps and
+// W^T eps with its neighbours: 16-bit operands with the GEMM weight update
+// (B <= 128), and fp32 operands with either weight update while the operand
+// blocks fit the LDS (B <= 64 at width 64).
 constexpr int RES_MAX_WIDTH = 64;   // d_0 .. d_{L-1}
 constexpr int RES_MAX_B = 128;
 constexpr int RES_MAX_WG = 63;      // word 63 of the flag area is the input-image flag
@@ -101,6 +103,7 @@ constexpr int RES_TOP_ROWS = 32;    // rows of W[L-1] per top workgroup (a 64-ro
 struct ResidentArgs {
   int L, B, steps, nwg, chunks, kc, spin_limit, lds_bytes;
   int halves;                   // top-layer row blocks of RES_TOP_ROWS (one workgroup per chunk and block)
+  int outer;                    // weight update as a rank-B outer product on the VALU (fp32 operands, B <= 16)
   float alpha, gamma;
   int dims[NARROW_MAX_L + 1];
   float* x[NARROW_MAX_L + 1];
@@ -119,16 +122,17 @@ struct ResidentArgs {
   unsigned* bar;                // [1] exit counter, [2] wait timeout flag (shared with the column kernel)
 };
 
-// LDS layout of one workgroup (element offsets, 16-bit elements).  M x K is
-// the workgroup's block of W; `hidden` workgroups also hold W^T and eps in
-// the inference operand layout.  Contraction extents are padded to 32 and
-// output extents to 16; every row is padded by 8 elements.
-//   wh, wl  [M16][K32+8]   W hi / lo          (prediction A)
-//   wt      [K16][M32+8]   W^T hi             (inference A, hidden only)
-//   fh, fl  [B16][K32+8]   f(x upper) hi / lo (prediction B)
-//   ft      [K16][B32+8]   f(x upper) hi      (weight-update B)
-//   eb      [B16][M32+8]   eps                (inference B, hidden only)
-//   ea      [M16][B32+8]   eps                (weight-update A)
+// LDS layout of one workgroup (element offsets, in operand elements of
+// `esize` bytes).  M x K is the workgroup's block of W; `hidden` workgroups
+// also hold W^T and eps in the inference operand layout.  Contraction extents
+// are padded to the MFMA k-step (KP: 32 for 16-bit operands, 16 for fp32) and
+// output extents to 16; every row is padded by KP / 4 elements (16 bytes).
+//   wh, wl  [M16][KkP+pad]  W hi / lo          (prediction A)
+//   wt      [K16][MkP+pad]  W^T hi             (inference A, hidden only)
+//   fh, fl  [B16][KkP+pad]  f(x upper) hi / lo (prediction B)
+//   ft      [K16][BkP+pad]  f(x upper) hi      (weight-update B)
+//   eb      [B16][MkP+pad]  eps                (inference B, hidden only)
+//   ea      [M16][BkP+pad]  eps                (weight-update A)
 struct ResidentLds {
   int ldw, ldwt, ldf, ldft, lde, lda;
   int wh, wl, wt, fh, fl, ft, eb, ea, bytes;
@@ -136,10 +140,12 @@ struct ResidentLds {
 
 __host__ __device__ inline int res_round(int v, int m) { return (v + m - 1) / m * m; }
 
-__host__ __device__ inline void resident_lds_layout(int M, int K, int B, bool hidden, bool split3, ResidentLds& o) {
-  const int M16 = res_round(M, 16), M32 = res_round(M, 32), K16 = res_round(K, 16), K32 = res_round(K, 32);
-  const int B16 = res_round(B, 16), B32 = res_round(B, 32);
-  o.ldw = K32 + 8; o.ldwt = M32 + 8; o.ldf = K32 + 8; o.ldft = B32 + 8; o.lde = M32 + 8; o.lda = B32 + 8;
+__host__ __device__ inline void resident_lds_layout(int M, int K, int B, bool hidden, bool split3, int esize,
+                                                    ResidentLds& o) {
+  const int KP = esize == 4 ? 16 : 32, pad = KP / 4;
+  const int M16 = res_round(M, 16), MP = res_round(M, KP), K16 = res_round(K, 16), KK = res_round(K, KP);
+  const int B16 = res_round(B, 16), BP = res_round(B, KP);
+  o.ldw = KK + pad; o.ldwt = MP + pad; o.ldf = KK + pad; o.ldft = BP + pad; o.lde = MP + pad; o.lda = BP + pad;
   int at = 0;
   o.wh = at; at += M16 * o.ldw;
   o.wl = at; if (split3) at += M16 * o.ldw;
@@ -149,17 +155,19 @@ __host__ __device__ inline void resident_lds_layout(int M, int K, int B, bool hi
   o.ft = at; at += K16 * o.ldft;
   o.eb = at; if (hidden) at += B16 * o.lde;
   o.ea = at; at += M16 * o.lda;
-  o.bytes = at * 2;
+  o.bytes = at * esize;
 }
 
 // Exchanged 16x16 tiles of a [d][B] matrix.
 inline int resident_tiles(int d, int B) { return ((d + 15) / 16) * ((B + 15) / 16); }
 
-// Plan of the layer-resident kernel for dims / B (16-bit operands, split 1
-// or 3): fills chunks (NARROW_KCHUNK columns of the top layer each), kc, nwg
-// and lds_bytes of `a` and returns the workspace bytes its flags and
-// exchange buffers need, or -1 when the net is not eligible.
-long long resident_plan(const int* dims, int L, int B, int split, ResidentArgs& a);
+// Plan of the layer-resident kernel for dims / B (operands of `esize` bytes:
+// 2 with split 1 or 3, 4 with split 1; `outer`: the rank-B weight update,
+// fp32 operands and B <= NARROW_OUTER_MAX_B only): fills chunks
+// (NARROW_KCHUNK columns of the top layer each), kc, nwg, outer and
+// lds_bytes of `a` and returns the workspace bytes its flags and exchange
+// buffers need, or -1 when the net is not eligible.
+long long resident_plan(const int* dims, int L, int B, int split, int esize, bool outer, ResidentArgs& a);
 
 // Lays the flags, exchange buffers and input images out in `ws` (resident_plan's bytes).
 void resident_bind(ResidentArgs& a, char* ws);

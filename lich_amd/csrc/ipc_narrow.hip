@@ -428,7 +428,9 @@ struct Narrow {
         const int m = m0 + r, n = n0 + c;
         if (m < M && n < N) {
           float s = 0.0f;
-          for (int b = 0; b < B; ++b) s += so_e[r * (NC + 1) + b] * so_x[c * (NC + 1) + b];
+          // fused multiply-adds from zero in batch order (the layer-resident
+          // kernel's rank-B update computes the same sums)
+          for (int b = 0; b < B; ++b) s = __builtin_fmaf(so_e[r * (NC + 1) + b], so_x[c * (NC + 1) + b], s);
           {
 #pragma clang fp contract(off)
             const long long o = (long long)m * N + n;

@@ -51,19 +51,40 @@ constexpr int NT = 1024;  // threads per workgroup (16 waves)
 constexpr int NWV = NT / 64;
 constexpr int MAXT = 2;  // output tiles per wave and phase (32 tiles at most)
 
-template <typename OT> struct Vec8;
-template <> struct Vec8<f16> { typedef f16x8 T; };
-template <> struct Vec8<bf16> { typedef bf16x8 T; };
-template <typename OT> struct Vec4;
-template <> struct Vec4<f16> { typedef _Float16 T __attribute__((ext_vector_type(4))); };
-template <> struct Vec4<bf16> { typedef __bf16 T __attribute__((ext_vector_type(4))); };
-
-__device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
-__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
+// MFMA operands per operand type.  Per k-step of KSTEP, lane (r = lane % 16,
+// g = lane / 16) supplies the KL consecutive elements k = g * KL .. g * KL +
+// KL - 1 of its row (one fragment V); V4 holds four elements for staging.
+// 16-bit operands take one 16x16x32 MFMA per k-step.  fp32 operands take four
+// 16x16x4 MFMAs, instruction s taking k = 4 g + s from lane group g: the
+// order of the column kernel's fp32 products, so both kernels give the same
+// bits.
+template <typename OT> struct Op;
+template <> struct Op<f16> {
+  typedef f16x8 V;
+  typedef _Float16 V4 __attribute__((ext_vector_type(4)));
+  static constexpr int KSTEP = 32, KL = 8;
+  __device__ __forceinline__ static f32x4 mma(V a, V b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct Op<bf16> {
+  typedef bf16x8 V;
+  typedef __bf16 V4 __attribute__((ext_vector_type(4)));
+  static constexpr int KSTEP = 32, KL = 8;
+  __device__ __forceinline__ static f32x4 mma(V a, V b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct Op<float> {
+  typedef f32x4 V;
+  typedef f32x4 V4;
+  static constexpr int KSTEP = 16, KL = 4;
+  __device__ __forceinline__ static f32x4 mma(V a, V b, f32x4 c) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], b[s], c, 0, 0, 0);
+    return c;
+  }
+};
 
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.0f, 0.0f, 0.0f, 0.0f}; }
 
@@ -159,9 +180,10 @@ __device__ __forceinline__ f32x4 dact4_from(f32x4 x, f32x4 f) {
 
 template <typename OT, int SPLIT, int ACT>
 struct Resident {
-  typedef typename Vec8<OT>::T V8;
-  typedef typename Vec4<OT>::T V4;
+  typedef typename Op<OT>::V V8;
+  typedef typename Op<OT>::V4 V4;
   static constexpr bool S3 = SPLIT >= 3;
+  static constexpr int KSTEP = Op<OT>::KSTEP, KL = Op<OT>::KL;
 
   const ResidentArgs& p;
   OT* lds;
@@ -191,7 +213,7 @@ struct Resident {
     k0 = hidden ? 0 : j * p.kc;
     K = hidden ? p.dims[l + 1] : min(p.kc, p.dims[L] - k0);
     ldw_g = p.dims[l + 1];
-    resident_lds_layout(M, K, B, hidden, S3, lay);
+    resident_lds_layout(M, K, B, hidden, S3, (int)sizeof(OT), lay);
     nbt = (B + 15) / 16;
     const int mtl = (M + 15) / 16;
     ktl = (K + 15) / 16;
@@ -200,9 +222,9 @@ struct Resident {
     npr_full = ((p.dims[l] + 15) / 16) * nbt;
     n_inf = hidden ? ktl * nbt : 0;
     n_upd = mtl * ktl;
-    ks_k = (K + 31) / 32;
-    ks_m = (M + 31) / 32;
-    ks_b = (B + 31) / 32;
+    ks_k = (K + KSTEP - 1) / KSTEP;
+    ks_m = (M + KSTEP - 1) / KSTEP;
+    ks_b = (B + KSTEP - 1) / KSTEP;
     inv_nbt = 1.0f / (float)nbt;
     inv_ktl = 1.0f / (float)ktl;
     inv_B = 1.0f / (float)B;
@@ -332,18 +354,18 @@ struct Resident {
   // acc = W_block f(x upper) for prediction tile t
   __device__ __forceinline__ f32x4 pred_tile(int t) const {
     const int rt = qdiv(t, inv_nbt), ct = t - rt * nbt;
-    const int a0 = (rt * 16 + lr) * lay.ldw + lg * 8;
-    const int b0 = (ct * 16 + lr) * lay.ldf + lg * 8;
+    const int a0 = (rt * 16 + lr) * lay.ldw + lg * KL;
+    const int b0 = (ct * 16 + lr) * lay.ldf + lg * KL;
     f32x4 c = zero4();
     for (int ks = 0; ks < ks_k; ++ks) {
-      const V8 ah = ld8(lay.wh + a0 + ks * 32);
-      const V8 bh = ld8(lay.fh + b0 + ks * 32);
-      c = mfma16(ah, bh, c);
+      const V8 ah = ld8(lay.wh + a0 + ks * KSTEP);
+      const V8 bh = ld8(lay.fh + b0 + ks * KSTEP);
+      c = Op<OT>::mma(ah, bh, c);
       if (S3) {
-        const V8 al = ld8(lay.wl + a0 + ks * 32);
-        const V8 bl = ld8(lay.fl + b0 + ks * 32);
-        c = mfma16(al, bh, c);
-        c = mfma16(ah, bl, c);
+        const V8 al = ld8(lay.wl + a0 + ks * KSTEP);
+        const V8 bl = ld8(lay.fl + b0 + ks * KSTEP);
+        c = Op<OT>::mma(al, bh, c);
+        c = Op<OT>::mma(ah, bl, c);
       }
     }
     return c;
@@ -352,20 +374,37 @@ struct Resident {
   // acc = W^T eps for inference tile t (rows over K)
   __device__ __forceinline__ f32x4 infer_tile(int t) const {
     const int rt = qdiv(t, inv_nbt), ct = t - rt * nbt;
-    const int a0 = lay.wt + (rt * 16 + lr) * lay.ldwt + lg * 8;
-    const int b0 = lay.eb + (ct * 16 + lr) * lay.lde + lg * 8;
+    const int a0 = lay.wt + (rt * 16 + lr) * lay.ldwt + lg * KL;
+    const int b0 = lay.eb + (ct * 16 + lr) * lay.lde + lg * KL;
     f32x4 c = zero4();
-    for (int ks = 0; ks < ks_m; ++ks) c = mfma16(ld8(a0 + ks * 32), ld8(b0 + ks * 32), c);
+    for (int ks = 0; ks < ks_m; ++ks) c = Op<OT>::mma(ld8(a0 + ks * KSTEP), ld8(b0 + ks * KSTEP), c);
     return c;
+  }
+
+  // acc = eps f(x upper)^T over the batch as a rank-B outer product on the
+  // VALU (fp32 operands, B <= NARROW_OUTER_MAX_B): each of the lane's four
+  // sums runs over b = 0 .. B-1 with fused multiply-adds from zero, as the
+  // column kernel's rank-B update does.
+  __device__ __forceinline__ f32x4 outer_tile(int t) const {
+    const int c = uct(t) * 16 + lr, r0 = urt(t) * 16 + 4 * lg;
+    const OT* fr = lds + lay.ft + c * lay.ldft;
+    f32x4 acc = zero4();
+    for (int b = 0; b < B; ++b) {
+      const float f = to_f32(fr[b]);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[q] = __builtin_fmaf(to_f32(lds[lay.ea + (r0 + q) * lay.lda + b]), f, acc[q]);
+    }
+    return acc;
   }
 
   // acc = eps f(x upper)^T over the batch for update tile t (rows over M, columns over K)
   __device__ __forceinline__ f32x4 update_tile(int t) const {
+    if (p.outer) return outer_tile(t);
     const int rt = urt(t), ct = uct(t);
-    const int a0 = lay.ea + (rt * 16 + lr) * lay.lda + lg * 8;
-    const int b0 = lay.ft + (ct * 16 + lr) * lay.ldft + lg * 8;
+    const int a0 = lay.ea + (rt * 16 + lr) * lay.lda + lg * KL;
+    const int b0 = lay.ft + (ct * 16 + lr) * lay.ldft + lg * KL;
     f32x4 c = zero4();
-    for (int ks = 0; ks < ks_b; ++ks) c = mfma16(ld8(a0 + ks * 32), ld8(b0 + ks * 32), c);
+    for (int ks = 0; ks < ks_b; ++ks) c = Op<OT>::mma(ld8(a0 + ks * KSTEP), ld8(b0 + ks * KSTEP), c);
     return c;
   }
 
@@ -380,21 +419,21 @@ struct Resident {
     const int t0 = wave, t1 = wave + NWV;
     if (t1 < n && NWV % nbt == 0) {
       const int rt0 = qdiv(t0, inv_nbt), ct = t0 - rt0 * nbt, rt1 = rt0 + NWV / nbt;
-      const int a0 = (rt0 * 16 + lr) * lay.ldw + lg * 8, a1 = (rt1 * 16 + lr) * lay.ldw + lg * 8;
-      const int b0 = (ct * 16 + lr) * lay.ldf + lg * 8;
+      const int a0 = (rt0 * 16 + lr) * lay.ldw + lg * KL, a1 = (rt1 * 16 + lr) * lay.ldw + lg * KL;
+      const int b0 = (ct * 16 + lr) * lay.ldf + lg * KL;
       f32x4 c0 = zero4(), c1 = zero4();
       for (int ks = 0; ks < ks_k; ++ks) {
-        const V8 bh = ld8(lay.fh + b0 + ks * 32);
-        const V8 ah0 = ld8(lay.wh + a0 + ks * 32), ah1 = ld8(lay.wh + a1 + ks * 32);
-        c0 = mfma16(ah0, bh, c0);
-        c1 = mfma16(ah1, bh, c1);
+        const V8 bh = ld8(lay.fh + b0 + ks * KSTEP);
+        const V8 ah0 = ld8(lay.wh + a0 + ks * KSTEP), ah1 = ld8(lay.wh + a1 + ks * KSTEP);
+        c0 = Op<OT>::mma(ah0, bh, c0);
+        c1 = Op<OT>::mma(ah1, bh, c1);
         if (S3) {
-          const V8 bl = ld8(lay.fl + b0 + ks * 32);
-          const V8 al0 = ld8(lay.wl + a0 + ks * 32), al1 = ld8(lay.wl + a1 + ks * 32);
-          c0 = mfma16(al0, bh, c0);
-          c1 = mfma16(al1, bh, c1);
-          c0 = mfma16(ah0, bl, c0);
-          c1 = mfma16(ah1, bl, c1);
+          const V8 bl = ld8(lay.fl + b0 + ks * KSTEP);
+          const V8 al0 = ld8(lay.wl + a0 + ks * KSTEP), al1 = ld8(lay.wl + a1 + ks * KSTEP);
+          c0 = Op<OT>::mma(al0, bh, c0);
+          c1 = Op<OT>::mma(al1, bh, c1);
+          c0 = Op<OT>::mma(ah0, bl, c0);
+          c1 = Op<OT>::mma(ah1, bl, c1);
         }
       }
       c[0] = c0;
@@ -409,13 +448,13 @@ struct Resident {
     const int t0 = wave, t1 = wave + NWV;
     if (t1 < n && NWV % nbt == 0) {
       const int rt0 = qdiv(t0, inv_nbt), ct = t0 - rt0 * nbt, rt1 = rt0 + NWV / nbt;
-      const int a0 = lay.wt + (rt0 * 16 + lr) * lay.ldwt + lg * 8, a1 = lay.wt + (rt1 * 16 + lr) * lay.ldwt + lg * 8;
-      const int b0 = lay.eb + (ct * 16 + lr) * lay.lde + lg * 8;
+      const int a0 = lay.wt + (rt0 * 16 + lr) * lay.ldwt + lg * KL, a1 = lay.wt + (rt1 * 16 + lr) * lay.ldwt + lg * KL;
+      const int b0 = lay.eb + (ct * 16 + lr) * lay.lde + lg * KL;
       f32x4 c0 = zero4(), c1 = zero4();
       for (int ks = 0; ks < ks_m; ++ks) {
-        const V8 b = ld8(b0 + ks * 32);
-        c0 = mfma16(ld8(a0 + ks * 32), b, c0);
-        c1 = mfma16(ld8(a1 + ks * 32), b, c1);
+        const V8 b = ld8(b0 + ks * KSTEP);
+        c0 = Op<OT>::mma(ld8(a0 + ks * KSTEP), b, c0);
+        c1 = Op<OT>::mma(ld8(a1 + ks * KSTEP), b, c1);
       }
       c[0] = c0;
       c[1] = c1;
@@ -427,15 +466,15 @@ struct Resident {
 
   __device__ __forceinline__ void update_tiles(int n, f32x4 (&c)[MAXT]) const {
     const int t0 = wave, t1 = wave + NWV;
-    if (t1 < n && NWV % ktl == 0) {
+    if (!p.outer && t1 < n && NWV % ktl == 0) {
       const int rt0 = urt(t0), ct = t0 - rt0 * ktl, rt1 = rt0 + NWV / ktl;
-      const int a0 = lay.ea + (rt0 * 16 + lr) * lay.lda + lg * 8, a1 = lay.ea + (rt1 * 16 + lr) * lay.lda + lg * 8;
-      const int b0 = lay.ft + (ct * 16 + lr) * lay.ldft + lg * 8;
+      const int a0 = lay.ea + (rt0 * 16 + lr) * lay.lda + lg * KL, a1 = lay.ea + (rt1 * 16 + lr) * lay.lda + lg * KL;
+      const int b0 = lay.ft + (ct * 16 + lr) * lay.ldft + lg * KL;
       f32x4 c0 = zero4(), c1 = zero4();
       for (int ks = 0; ks < ks_b; ++ks) {
-        const V8 b = ld8(b0 + ks * 32);
-        c0 = mfma16(ld8(a0 + ks * 32), b, c0);
-        c1 = mfma16(ld8(a1 + ks * 32), b, c1);
+        const V8 b = ld8(b0 + ks * KSTEP);
+        c0 = Op<OT>::mma(ld8(a0 + ks * KSTEP), b, c0);
+        c1 = Op<OT>::mma(ld8(a1 + ks * KSTEP), b, c1);
       }
       c[0] = c0;
       c[1] = c1;
@@ -486,13 +525,13 @@ __device__ __forceinline__ void wait_peers(const ResidentArgs& p, const int* pee
 
 // Launch set-up, run while the workgroup's first state and weight loads are
 // in flight: the peer list, and zeros in the operand regions when the block
-// does not fill them (a dimension off the 32-element MFMA k-step or the
-// 16-row tile leaves padding that the MFMAs read); ends with a barrier, so
-// the staging writes that follow land after the zeros.
+// does not fill them (a dimension off the MFMA k-step or the 16-row tile
+// leaves padding that the MFMAs read); ends with a barrier, so the staging
+// writes that follow land after the zeros.
 template <typename OT, int SPLIT, int ACT>
 __device__ __forceinline__ void setup(const Resident<OT, SPLIT, ACT>& k, const ResidentArgs& p, int* peers,
                                       int& npeers) {
-  if ((k.M | k.K | k.B) & 31) {
+  if ((k.M | k.K | k.B) & (Resident<OT, SPLIT, ACT>::KSTEP - 1)) {
     uint4* z = reinterpret_cast<uint4*>(k.lds);
     for (int i = threadIdx.x; i < k.lay.bytes / 16; i += NT) z[i] = uint4{0u, 0u, 0u, 0u};
   }
@@ -771,7 +810,7 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
   // into LDS by the launches after it.
   char* image = p.image + (long long)j * p.image_stride;
   uint4* lds_image = reinterpret_cast<uint4*>(k.lds + k.lay.fh);
-  const int n16 = (k.lay.ea - k.lay.fh) * 2 / 16;
+  const int n16 = (k.lay.ea - k.lay.fh) * (int)sizeof(OT) / 16;
   const bool warm = *reinterpret_cast<const volatile unsigned*>(&p.flags[RES_MAX_WG]) == 1u;
   if (warm) {
     constexpr int CB = 8;  // 16-byte loads in flight per thread
@@ -1056,6 +1095,7 @@ hipError_t by_act(int act, bool prep, int bytes, const ResidentArgs* a, hipStrea
 // raise its LDS limit (prep), report its workgroups per CU (occ) or launch it.
 hipError_t dispatch(int operand, int split, int act, bool prep, int bytes, const ResidentArgs* a, hipStream_t s,
                     int* occ = nullptr) {
+  if (operand == DT_F32) return by_act<float, 1>(act, prep, bytes, a, s, occ);
   if (operand == DT_F16)
     return split >= 3 ? by_act<f16, 3>(act, prep, bytes, a, s, occ) : by_act<f16, 1>(act, prep, bytes, a, s, occ);
   if (operand == DT_BF16)
@@ -1065,8 +1105,10 @@ hipError_t dispatch(int operand, int split, int act, bool prep, int bytes, const
 
 }  // namespace
 
-long long resident_plan(const int* dims, int L, int B, int split, ResidentArgs& a) {
+long long resident_plan(const int* dims, int L, int B, int split, int esize, bool outer, ResidentArgs& a) {
   if (L < 2 || L > NARROW_MAX_L || B < 1 || B > RES_MAX_B) return -1;
+  if (esize == 4 ? split >= 2 : esize != 2) return -1;
+  if (outer && (esize != 4 || B > NARROW_OUTER_MAX_B)) return -1;
   for (int l = 0; l < L; ++l)
     if (dims[l] < 1 || dims[l] > RES_MAX_WIDTH) return -1;
   const bool s3 = split >= 3;
@@ -1074,7 +1116,7 @@ long long resident_plan(const int* dims, int L, int B, int split, ResidentArgs& 
   int need = 0;
   for (int l = 0; l + 1 < L; ++l) {
     ResidentLds o;
-    resident_lds_layout(dims[l], dims[l + 1], B, true, s3, o);
+    resident_lds_layout(dims[l], dims[l + 1], B, true, s3, esize, o);
     need = o.bytes > need ? o.bytes : need;
   }
   // top layer: one workgroup per NARROW_KCHUNK columns (the column kernel's
@@ -1084,7 +1126,8 @@ long long resident_plan(const int* dims, int L, int B, int split, ResidentArgs& 
   const int halves = (dims[L - 1] + RES_TOP_ROWS - 1) / RES_TOP_ROWS;
   if ((L - 1) + halves * C + halves > RES_MAX_WG) return -1;  // flags[nwg + h]: block h's eps flags
   ResidentLds o;
-  resident_lds_layout(dims[L - 1] < RES_TOP_ROWS ? dims[L - 1] : RES_TOP_ROWS, dL < kc ? dL : kc, B, false, s3, o);
+  resident_lds_layout(dims[L - 1] < RES_TOP_ROWS ? dims[L - 1] : RES_TOP_ROWS, dL < kc ? dL : kc, B, false, s3, esize,
+                      o);
   need = o.bytes > need ? o.bytes : need;
   if (need > limit) return -1;
   a.L = L;
@@ -1092,6 +1135,7 @@ long long resident_plan(const int* dims, int L, int B, int split, ResidentArgs& 
   a.chunks = C;
   a.kc = kc;
   a.halves = halves;
+  a.outer = outer ? 1 : 0;
   a.nwg = (L - 1) + halves * C;
   a.lds_bytes = res_round(need, 16);
   for (int l = 0; l <= L; ++l) a.dims[l] = dims[l];
@@ -1101,7 +1145,7 @@ long long resident_plan(const int* dims, int L, int B, int split, ResidentArgs& 
     bytes += (l + 2 == L ? 3LL : 2LL) * resident_tiles(dims[l + 1], B) * RES_TILE * 4;
   }
   bytes += 2LL * (C + 1) * resident_tiles(dims[L - 1], B) * RES_TILE * 4;
-  a.image_stride = res_round((o.ea - o.fh) * 2, 256);  // the fh .. ea region of the widest chunk
+  a.image_stride = res_round((o.ea - o.fh) * esize, 256);  // the fh .. ea region of the widest chunk
   bytes = res_round(bytes, 256) + C * a.image_stride;
   return bytes;
 }

@@ -214,10 +214,13 @@ def test_plan_path_selection_and_wide_workspace():
     finally:
         lib.ipc_plan_destroy(h)
     # a narrow net keeps a whole-step kernel under AUTO: the layer-resident one
-    # for 16-bit operands, the column-block one when asked for or for fp32
+    # for 16-bit operands and for fp32 operands whose blocks fit the LDS (B = 8
+    # here, with the rank-B update), the column-block one when asked for or
+    # for fp32 at B = 128
     narrow = (ctypes.c_int * 4)(10, 64, 64, 784)
-    for operand, path, want in ((1, -1, nat.PATH_RESIDENT), (1, 1, nat.PATH_NARROW), (0, -1, nat.PATH_NARROW)):
-        assert lib.ipc_plan_create(ctypes.byref(h), 3, narrow, 128, 0, operand, 3, 2, 1e-4, 0.5, 1, 0, path) == nat.IPC_OK
+    for operand, B, path, want in ((1, 128, -1, nat.PATH_RESIDENT), (1, 128, 1, nat.PATH_NARROW),
+                                   (0, 128, -1, nat.PATH_NARROW), (0, 8, -1, nat.PATH_RESIDENT)):
+        assert lib.ipc_plan_create(ctypes.byref(h), 3, narrow, B, 0, operand, 3, 2, 1e-4, 0.5, 1, 2, path) == nat.IPC_OK
         try:
             assert lib.ipc_plan_path(h) == want and lib.ipc_plan_fused(h) == 1
         finally:
@@ -225,7 +228,7 @@ def test_plan_path_selection_and_wide_workspace():
     assert lib.ipc_plan_path(None) == -1
 
 
-def _resident_ws_bytes(dims, B, recompute):
+def _resident_ws_bytes(dims, B, recompute, esize=2):
     """Restated workspace of a layer-resident plan: the column kernel's
     barrier words and f(x) buffers, then 256 bytes of step flags and the
     double-buffered exchange of 16x16 tiles (1 KiB each): eps[l] for
@@ -247,35 +250,42 @@ def _resident_ws_bytes(dims, B, recompute):
         n += (3 if l + 2 == L else 2) * tiles(dims[l + 1]) * 1024
     C = -(-dims[L] // 128)
     n += 2 * (C + 1) * tiles(dims[L - 1]) * 1024   # the partials and chunk 0's summed eps[L-1]
-    # then, per top chunk, its cached 16-bit f(x[L]) operands as laid out in
-    # LDS (split 3: hi and lo [B16][K32+8], hi [K16][B32+8]), 256-byte aligned
+    # then, per top chunk, its cached f(x[L]) operands as laid out in LDS
+    # (16-bit, split 3: hi and lo [B16][K32+8], hi [K16][B32+8]; fp32: [B16][K16+4]
+    # and [K16][B16+4]), 256-byte aligned
     r = lambda v, m: -(-v // m) * m  # noqa: E731
     K = min(dims[L], 128)
-    image = r((2 * r(B, 16) * (r(K, 32) + 8) + r(K, 16) * (r(B, 32) + 8)) * 2, 256)
+    if esize == 2:
+        image = r((2 * r(B, 16) * (r(K, 32) + 8) + r(K, 16) * (r(B, 32) + 8)) * 2, 256)
+    else:
+        image = r((r(B, 16) * (r(K, 16) + 4) + r(K, 16) * (r(B, 16) + 4)) * 4, 256)
     return r(n, 256) + C * image
 
 
-@pytest.mark.parametrize("dims,B,recompute", [
-    ((10, 64, 64, 64, 64, 64, 64, 784), 128, 1),
-    ((10, 64, 784), 128, 0),
-    ((7, 33, 48, 130), 40, 1),
-    ((3, 64, 100), 17, 1),
+@pytest.mark.parametrize("dims,B,recompute,operand", [
+    ((10, 64, 64, 64, 64, 64, 64, 784), 128, 1, 2),
+    ((10, 64, 784), 128, 0, 2),
+    ((7, 33, 48, 130), 40, 1, 2),
+    ((3, 64, 100), 17, 1, 2),
+    ((10, 64, 64, 64, 64, 784), 8, 1, 0),
+    ((7, 33, 48, 130), 40, 0, 0),
+    ((10, 64, 784), 64, 1, 0),
 ])
-def test_resident_plan_workspace(dims, B, recompute):
+def test_resident_plan_workspace(dims, B, recompute, operand):
     lib = _lib()
     h = ctypes.c_void_p()
     L = len(dims) - 1
     d = (ctypes.c_int * (L + 1))(*dims)
-    assert lib.ipc_plan_create(ctypes.byref(h), L, d, B, 0, 2, 3, 2, 1e-4, 0.5, recompute, 0, 3) == nat.IPC_OK
+    assert lib.ipc_plan_create(ctypes.byref(h), L, d, B, 0, operand, 3, 2, 1e-4, 0.5, recompute, 0, 3) == nat.IPC_OK
     try:
         assert lib.ipc_plan_path(h) == nat.PATH_RESIDENT
-        assert lib.ipc_plan_workspace_bytes(h) == _resident_ws_bytes(dims, B, recompute)
+        assert lib.ipc_plan_workspace_bytes(h) == _resident_ws_bytes(dims, B, recompute, 4 if operand == 0 else 2)
     finally:
         lib.ipc_plan_destroy(h)
 
 
 @pytest.mark.parametrize("dims,B,operand,split,wmode,why", [
-    ((10, 64, 64, 784), 128, 0, 1, 0, "fp32 operands"),
+    ((10, 64, 64, 784), 128, 0, 1, 0, "fp32 operand blocks beyond the LDS"),
     ((10, 64, 64, 784), 256, 1, 3, 0, "batch above 128"),
     ((10, 128, 64, 784), 128, 1, 3, 0, "hidden width above 64"),
     ((10, 784), 128, 1, 3, 0, "a single layer"),

@@ -1,4 +1,4 @@
-"""Layer-resident whole-step kernel (multi-step launches of narrow 16-bit-operand plans).
+"""Layer-resident whole-step kernel (multi-step launches of narrow plans).
 
 * Against the fp32 oracle after T steps: states <= 2e-2, weight deltas <= 5e-3
   (the 16-bit operand bars), on ragged shapes: widths and batches that are not
@@ -9,6 +9,10 @@
   MFMA chains and the same 128-column partial-sum order, so every state,
   error and weight must agree bit for bit.
 * Launch boundaries do not change bits, and no wait ever hits its spin limit.
+* fp32 operands (the small-batch configuration, B <= 64): bit-identical to the
+  column kernel with the rank-B and with the GEMM weight update, within the
+  fp32 bar (1e-5) of the oracle, and the forward initialisation leaves the
+  first errors exactly zero.
 """
 import numpy as np
 import pytest
@@ -20,7 +24,7 @@ from tests.helpers import DEV, report
 
 pytestmark = pytest.mark.gpu
 
-F16, BF16 = torch.float16, torch.bfloat16
+F16, BF16, F32 = torch.float16, torch.bfloat16, torch.float32
 
 SHAPES = [
     ((10, 64, 784), 128),
@@ -35,18 +39,19 @@ SHAPES = [
 ]
 
 
-def _model(dims, w0, act, op, path, split=None, recompute=True):
+def _model(dims, w0, act, op, path, split=None, recompute=True, wmode="gemm"):
     cfg = IPCConfig(dims=dims, activation=act, dtype=op, fused=path, pred_split=split,
-                    recompute_activation=recompute)
+                    recompute_activation=recompute, weight_update_mode=wmode)
     return HipIPC(cfg, device=DEV, weights=w0)
 
 
-def _run(dims, B, act, op, path, T, seed, split=None):
+def _run(dims, B, act, op, path, T, seed, split=None, wmode="gemm", launches=None):
     w0 = O.init_weights(dims, seed=seed, init="xavier_uniform")
     x_in, _labels, y = O.make_batch(dims, B, seed=seed)
-    m = _model(dims, w0, act, op, path, split)
+    m = _model(dims, w0, act, op, path, split, wmode=wmode)
     m.initialize_batch(x_in.to(DEV), y.to(DEV))
-    m.run_steps(T)
+    for n in launches or (T,):
+        m.run_steps(n)
     torch.cuda.synchronize()
     return m, w0, x_in, y
 
@@ -193,3 +198,62 @@ def test_cached_input_images_follow_new_batches_and_direct_writes():
     for a, b in zip(res.w + res.x + res.e[:-1], col.w + col.x + col.e[:-1]):
         assert torch.equal(a, b)
     assert res.barrier_timeouts() == 0
+
+
+# fp32 operands: the small-batch configuration and ragged nets, B <= 64
+SMALL = [
+    ((10, 64, 64, 64, 784), 1),
+    ((10, 64, 64, 64, 784), 8),
+    ((7, 33, 48, 130), 13),
+    ((10, 48, 64, 40, 300), 5),
+    ((10,) + (64,) * 6 + (784,), 16),
+]
+
+
+@pytest.mark.parametrize("act", ["tanh", "relu", "sigmoid", "gelu", "silu"])
+@pytest.mark.parametrize("wmode", ["outer", "gemm"])
+@pytest.mark.parametrize("dims,B", SMALL + [((10, 64, 64, 784), 64), ((7, 33, 48, 130), 40)])
+def test_fp32_resident_equals_column_kernel_bitwise(dims, B, wmode, act):
+    if wmode == "outer" and B > 16:
+        pytest.skip("the rank-B update covers B <= 16")
+    report("resident-fp32-vs-column", dims=dims, B=B, wmode=wmode, act=act)
+    ms = [_run(dims, B, act, F32, path, 6, seed=21, wmode=wmode, launches=(4, 2))[0] for path in ("resident", "narrow")]
+    assert [m.path for m in ms] == ["resident", "narrow"]
+    res, col = ms
+    for name, a, b in (("x", res.x, col.x), ("e", res.e[:-1], col.e[:-1]), ("w", res.w, col.w)):
+        for l, (u, v) in enumerate(zip(a, b)):
+            assert torch.equal(u, v), (name, l, float((u - v).abs().max()))
+    assert res.barrier_timeouts() == 0
+
+
+@pytest.mark.parametrize("wmode", ["outer", "gemm"])
+@pytest.mark.parametrize("dims,B", SMALL)
+def test_fp32_resident_matches_oracle(dims, B, wmode):
+    T, act = 8, "tanh"
+    report("resident-fp32-oracle", dims=dims, B=B, wmode=wmode)
+    m, w0, x_in, y = _run(dims, B, act, F32, "auto", T, seed=22, wmode=wmode)
+    assert m.path == "resident" and m.barrier_timeouts() == 0
+    x = O.forward_init(x_in, y, w0, act)
+    x_t, w_t, _e = O.run_steps(x, w0, T, act=act, alpha=1e-4, gamma=0.5)
+    s_err = O.global_rel_err(m.x, x_t)
+    w_err = O.global_rel_err(m.w, w_t)
+    print(f"resident fp32 {dims} B={B} {wmode}: state_err={s_err:.3e} w_err={w_err:.3e}")
+    assert s_err <= 1e-5 and w_err <= 1e-5
+
+
+def test_fp32_resident_forward_init_leaves_errors_exactly_zero():
+    dims, B, T = (10,) + (64,) * 4 + (784,), 8, 3
+    report("resident-fp32-wavefront", dims=dims, B=B)
+    w0 = O.init_weights(dims, seed=23, init="xavier_uniform")
+    x_in, _labels, y = O.make_batch(dims, B, seed=23)
+    m = _model(dims, w0, "tanh", F32, "resident", wmode="outer")
+    m.initialize_batch(x_in.to(DEV), y.to(DEV))
+    m.run_steps(1)
+    torch.cuda.synchronize()
+    for l in range(1, len(w0)):
+        assert torch.count_nonzero(m.e[l]) == 0, l
+    m.run_steps(T - 1)
+    torch.cuda.synchronize()
+    for l in range(len(w0)):
+        nz = torch.count_nonzero(m.w[l].cpu() - w0[l])
+        assert (nz == 0) if l >= T else (nz > 0), l

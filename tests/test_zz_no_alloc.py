@@ -30,14 +30,15 @@ def _noalloc(dims, B, x, e, w, operand, split, act, wmode, steps):
                                        1e-4, 0.5, wmode, steps, nat.current_stream_handle(DEV))
 
 
-@pytest.mark.parametrize("dims,dtype,wmode,path,batches", [
-    (D6, torch.float16, "gemm", "resident", (128, 64)),
-    (D6, torch.bfloat16, "gemm", "resident", (96, 40)),
-    ((10, 64, 64, 64, 784), torch.float32, "gemm", "narrow", (128, 48)),
-    ((10, 64, 64, 64, 64, 784), torch.float32, "auto", "narrow", (8, 4)),
+@pytest.mark.parametrize("dims,dtype,wmode,paths,batches", [
+    (D6, torch.float16, "gemm", ("resident", "resident"), (128, 64)),
+    (D6, torch.bfloat16, "gemm", ("resident", "resident"), (96, 40)),
+    (D6, torch.float16, "auto", ("narrow", "narrow"), (16, 8)),
+    ((10, 64, 64, 64, 784), torch.float32, "gemm", ("narrow", "resident"), (128, 48)),
+    ((10, 64, 64, 64, 64, 784), torch.float32, "auto", ("resident", "resident"), (8, 4)),
 ])
-def test_noalloc_steps_equal_the_plan_path(dims, dtype, wmode, path, batches):
-    for B in batches:
+def test_noalloc_steps_equal_the_plan_path(dims, dtype, wmode, paths, batches):
+    for B, path in zip(batches, paths):
         report("noalloc", dims=len(dims) - 1, dtype=str(dtype), B=B, path=path)
         w0 = O.init_weights(dims, seed=B, init="xavier_uniform")
         x_in, _l, y = O.make_batch(dims, B, seed=B)
