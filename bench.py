@@ -34,17 +34,18 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 METRIC = "iPC train samples/sec (L=6,h=64,B=128); fused-GEMM TFLOP/s vs MFMA peak"
-# HBM bytes that one launch of the dominant kernel moved in an earlier
-# profiling pass (not measured by this run): rocprofv3 --pmc FETCH_SIZE and
-# WRITE_SIZE passes (one counter per pass) over `bench.py --no-cpu --no-wide`,
-# each scaled by the same counter's reading for a plain device copy of known
-# size (`bench.py --copy-calibration`: FETCH_SIZE x 2.0, WRITE_SIZE x 1.0).
-# Keyed by kernel, with the profile summary that records the pass.
+# HBM bytes that one launch of the dominant kernel moved in a profiling pass
+# (not measured by this run): rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes
+# (one counter per pass) over `bench.py --no-cpu --no-wide`, each scaled by
+# the same counter's reading for a plain device copy of known size
+# (`bench.py --copy-calibration`: FETCH_SIZE x 2.0, WRITE_SIZE x 1.0).  Keyed
+# by kernel: (bytes, the profile summary that records the pass, the commit of
+# the kernel source it measured).
 MEASURED_TRAFFIC = {
     "layer-resident whole-step kernel, 4 steps per launch":
-        (4_320_896 + 3_374_720, "profiles/resident_whole_step_d6_h64_B128.md"),
+        (4_319_104 + 3_374_720, "profiles/resident_whole_step_d6_h64_B128.md", "65c76e5"),
     "whole-step kernel, 4 steps per launch":
-        (13_065_152 + 3_926_848, "profiles/narrow_whole_step_d6_h64_B128.md"),
+        (13_065_152 + 3_926_848, "profiles/narrow_whole_step_d6_h64_B128.md", "8dc03d3"),
 }
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0  # dense, no sparsity
@@ -458,10 +459,11 @@ def main() -> int:
         kernel = f"{dom} phase"
         launch_bytes, launch_flops = bf[dom]
     achieved = launch_bytes / (launch_us * 1e-6) / 1e9
-    traffic, traffic_src = MEASURED_TRAFFIC.get(kernel, (None, None))
+    traffic, traffic_src, traffic_commit = MEASURED_TRAFFIC.get(kernel, (None, None, None))
     roofline = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": traffic, "kernel": kernel,
-                "traffic_source": f"earlier rocprofv3 --pmc pass, {traffic_src}" if traffic_src else None,
+                "traffic_source": (f"rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes, {traffic_src}, kernel source "
+                                   f"at commit {traffic_commit}") if traffic_src else None,
                 "algorithmic_bytes_per_launch": launch_bytes,
                 "algorithmic_bytes_rule": f"{per_step_bytes} B per step (storage s=4: 2S + 2 sum_hidden d B + "
                                           f"(d_0+d_L) B) x {T if pmodel.fused else 1} steps per launch",
