@@ -122,6 +122,7 @@ def test_c2_relu_fp16_operands(depth, seed):
     model, _ = _gpu_run(dims, w0, x_in, y, "relu", T, torch.float16)
     s_err, dw_err = _errors(model, w0, x_t, w_t)
     frac = _gate_fraction(model.x[1:-1], x_t[1:-1])
+    # state_err is the max-norm error (global_rel_err); measured 3e-5 to 1.4e-2 over these cases
     print(f"c2 relu d={depth} seed={seed}: state_err={s_err:.3e} gate_frac={frac:.2e} dW_err={dw_err:.3e}")
     assert dw_err <= 5e-3 and frac <= 0.01
 
