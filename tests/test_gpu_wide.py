@@ -108,7 +108,7 @@ def test_wide_k_split_prediction(op, split):
     the plan cuts layer 0's prediction tiles into k-slices that fill the CUs
     left idle by the whole tiles, and a fourth launch adds the slices' partial
     products (ragged: M = 999 and B = 1000 end inside a tile), for both
-    prediction tile configurations (split 2: 128 x 128, split 1: 256 x 128).
+    default prediction tile configurations (split 2: 128 x 256, split 1: 256 x 128).
 
     The first step's prediction sees the same operands on both paths, so its
     eps[0] differs from the unsplit phased path only by the fp32 summation
