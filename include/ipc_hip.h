@@ -355,6 +355,23 @@ int ipc_steps_noalloc(int L, const int* dims, int B, void* const* x, void* const
  * without one); 0 restores the device query.  Not thread-safe. */
 int ipc_set_coresident_limit(int blocks);
 
+/* Tuning hook of the standalone 16-bit-storage calls (ipc_pred_err,
+ * ipc_forward, ipc_weight_update with recompute) on the LDS-DMA kernel: their
+ * B operand f(X_upper) is either activated in the loader of every row tile
+ * (0) or evaluated once by an elementwise pass into a buffer from a
+ * library-owned stream-ordered pool and then read like the other operands
+ * (1); -1 (the default) pre-activates by the rule of ipc_s16_preactivates
+ * when the stream is not being captured.  Both give the same bits.  No counterpart in the reference
+ * (TileLang fuses the activation into its loader).  Not thread-safe. */
+int ipc_set_s16_preactivate(int mode);
+
+/* Whether such a call of M rows, contraction K and batch B pre-activates under
+ * the current mode (kind: IPC_PHASE_PRED for ipc_pred_err / ipc_forward,
+ * IPC_PHASE_WEIGHT for a recomputing ipc_weight_update; 0 for any other), not
+ * counting graph capture.  The automatic rule: exp-based activations from
+ * M >= 1024 and K * B >= 2^20, relu from M >= 4096 and K * B >= 2^22. */
+int ipc_s16_preactivates(int kind, int act, int M, int K, int B);
+
 void ipc_plan_destroy(ipc_plan* plan);
 
 #ifdef __cplusplus

@@ -92,6 +92,8 @@ def _declare(lib):
         "ipc_plan_wide_config_count": ([i, i], i),
         "ipc_plan_set_wide_config": ([vp, i, i, i, i], i),
         "ipc_set_coresident_limit": ([i], i),
+        "ipc_set_s16_preactivate": ([i], i),
+        "ipc_s16_preactivates": ([i, i, i, i, i], i),
         "ipc_plan_graph_capture": ([vp, i], i),
         "ipc_plan_graph_launch": ([vp, i, vp], i),
         "ipc_plan_graph_steps": ([vp], i),

@@ -230,10 +230,81 @@ std::vector<WideProblem> s16_groups(const WideProblem& q, int groups, long long 
   return v;
 }
 
+// Pre-activation of a standalone call's B operand (ipc_set_s16_preactivate):
+// -1 automatic, 0 never, 1 always.
+int g_s16_preact = -1;
+
+// The library's stream-ordered pool of one device for the pre-activated
+// operands: a call allocates its buffer on its own stream and frees it there,
+// so calls on different streams never share one, and freed blocks stay in the
+// pool for the next call (release threshold: unlimited).
+hipMemPool_t s16_pool(int dev) {
+  static std::mutex mu;
+  static hipMemPool_t pools[64] = {};
+  if (dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!pools[dev]) {
+    hipMemPoolProps props{};
+    props.allocType = hipMemAllocationTypePinned;
+    props.location.type = hipMemLocationTypeDevice;
+    props.location.id = dev;
+    hipMemPool_t pool = nullptr;
+    if (hipMemPoolCreate(&pool, &props) != hipSuccess) return nullptr;
+    uint64_t keep = ~0ull;
+    hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+    pools[dev] = pool;
+  }
+  return pools[dev];
+}
+
+// Whether a call evaluates its B operand f(X_upper) once instead of in the
+// loader of every row tile (the same bits: f of the stored value, one
+// rounding; then the GEMM reads the result through LDS DMA like every other
+// operand).  The automatic rule, from the per-kernel sweep on MI355X: the
+// exponential activations pay for the extra pass from 4 row tiles of 256
+// (M >= 1024) and a 2^20-element operand; relu, cheap in the loader, from 16
+// row tiles and 2^22 elements.
+bool s16_preact_rule(int mode, int act, int M, long long kb) {
+  if (act == IPC_ACT_IDENTITY || mode == S16_INFER || g_s16_preact == 0) return false;
+  if (g_s16_preact > 0) return true;
+  if (act == IPC_ACT_RELU) return M >= 4096 && kb >= (1LL << 22);
+  return M >= 1024 && kb >= (1LL << 20);
+}
+
+// The rule, and not while the stream is being captured into a graph (then the
+// register path runs, as it does when the pool cannot supply the buffer).
+bool s16_preactivates(int mode, int act, int M, long long kb, hipStream_t s) {
+  if (!s16_preact_rule(mode, act, M, kb)) return false;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) {
+    (void)hipGetLastError();
+    return false;
+  }
+  return true;
+}
+
 int run_s16(int mode, const WideProblem& q, int groups, long long a_gs, long long b_gs, long long o_gs,
             long long x_gs, long long o2_gs, int operand, int act, void* stream, const char* what) {
+  hipStream_t s = (hipStream_t)stream;
+  if (s16_preactivates(mode, act, q.M, b_gs, s)) {
+    int dev = 0;
+    hipMemPool_t pool = hipGetDevice(&dev) == hipSuccess ? s16_pool(dev) : nullptr;
+    const long long n = (long long)groups * b_gs;  // the groups' B operands are contiguous, b_gs apart
+    void* buf = nullptr;
+    if (pool && hipMallocFromPoolAsync(&buf, (size_t)n * 2, pool, s) == hipSuccess) {
+      WideProblem qa = q;
+      qa.b = buf;
+      const std::vector<WideProblem> v = s16_groups(qa, groups, a_gs, b_gs, o_gs, x_gs, o2_gs);
+      hipError_t e = launch_s16_activate(q.b, buf, n, operand, act, s);
+      if (e == hipSuccess) e = launch_s16(mode, v.data(), groups, operand, IPC_ACT_IDENTITY, s);
+      const hipError_t ef = hipFreeAsync(buf, s);
+      if (e == hipSuccess) e = ef;
+      return launch_rc(e, what);
+    }
+    (void)hipGetLastError();
+  }
   const std::vector<WideProblem> v = s16_groups(q, groups, a_gs, b_gs, o_gs, x_gs, o2_gs);
-  return launch_rc(launch_s16(mode, v.data(), groups, operand, act, (hipStream_t)stream), what);
+  return launch_rc(launch_s16(mode, v.data(), groups, operand, act, s), what);
 }
 
 }  // namespace
@@ -1307,6 +1378,17 @@ int ipc_steps_noalloc(int L, const int* dims, int B, void* const* x, void* const
 int ipc_set_coresident_limit(int blocks) {
   if (blocks < 0) return fail(IPC_ERR_CONFIG, "the co-resident limit must be >= 0 (got %d)", blocks);
   g_coresident_limit = blocks;
+  return ok();
+}
+
+int ipc_s16_preactivates(int kind, int act, int M, int K, int B) {
+  const int mode = kind == IPC_PHASE_PRED ? S16_PRED : kind == IPC_PHASE_WEIGHT ? S16_WEIGHT : S16_INFER;
+  return s16_preact_rule(mode, act, M, (long long)K * B) ? 1 : 0;
+}
+
+int ipc_set_s16_preactivate(int mode) {
+  if (mode < -1 || mode > 1) return fail(IPC_ERR_CONFIG, "pre-activation mode must be -1, 0 or 1 (got %d)", mode);
+  g_s16_preact = mode;
   return ok();
 }
 

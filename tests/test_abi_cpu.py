@@ -512,3 +512,30 @@ def test_wide_tile_configurations_are_selectable_before_bind():
         assert lib.ipc_plan_workspace_bytes(h) < base
     finally:
         lib.ipc_plan_destroy(h)
+
+
+def test_s16_preactivate_hook_validates_its_mode():
+    lib = _lib()
+    assert lib.ipc_set_s16_preactivate(2) == nat.ERR_CONFIG and "pre-activation" in nat.last_error()
+    assert lib.ipc_set_s16_preactivate(-2) == nat.ERR_CONFIG
+    for mode in (0, 1, -1):
+        assert lib.ipc_set_s16_preactivate(mode) == nat.IPC_OK
+
+
+def test_s16_preactivation_rule():
+    """The automatic rule: exp-based activations from M >= 1024 and K*B >= 2^20,
+    relu from M >= 4096 and K*B >= 2^22, never for the inference update or
+    identity; mode 0 turns it off, mode 1 on."""
+    lib = _lib()
+    tanh, relu, ident = nat.act_code("tanh"), nat.act_code("relu"), nat.act_code("identity")
+    q = lib.ipc_s16_preactivates
+    assert q(0, tanh, 1024, 1024, 1024) == 1 and q(2, tanh, 1024, 1024, 1024) == 1
+    assert q(0, tanh, 1023, 1024, 1024) == 0 and q(0, tanh, 1024, 1024, 512) == 0
+    assert q(0, relu, 4096, 4096, 1024) == 1 and q(0, relu, 2048, 4096, 2048) == 0
+    assert q(0, relu, 4096, 1024, 2048) == 0
+    assert q(1, tanh, 8192, 8192, 8192) == 0 and q(0, ident, 8192, 8192, 8192) == 0
+    try:
+        assert lib.ipc_set_s16_preactivate(0) == nat.IPC_OK and q(0, tanh, 8192, 8192, 8192) == 0
+        assert lib.ipc_set_s16_preactivate(1) == nat.IPC_OK and q(0, relu, 8, 64, 8) == 1
+    finally:
+        lib.ipc_set_s16_preactivate(-1)

@@ -155,3 +155,76 @@ def test_dma_tile_refused_when_ineligible():
     with pytest.raises(ValueError, match="LDS-DMA"):
         k(torch.zeros((64, 128), device=DEV), torch.zeros((64, 64), device=DEV),
           torch.zeros((64, 128), device=DEV), torch.zeros((64, 128), device=DEV))
+
+
+def _preact(mode):
+    from lich_amd import _native as nat
+    assert nat.lib().ipc_set_s16_preactivate(mode) == 0
+
+
+@pytest.mark.parametrize("op", ["f16", "bf16"])
+@pytest.mark.parametrize("act", ACTS)
+@pytest.mark.parametrize("M,K,B,G", [(1024, 128, 256, 1), (1088, 1088, 192, 2), (300, 192, 128, 1)])
+def test_preactivated_operand_gives_the_register_path_bits(M, K, B, G, act, op):
+    """f(X_upper) evaluated once into a pooled buffer (ipc_set_s16_preactivate(1))
+    against the loader's register path (0): prediction, forward and the
+    recomputing weight update agree bit for bit, grouped (square layers) or
+    not, above and below the automatic threshold (M >= 1024)."""
+    report("dma16-preact", M=M, K=K, B=B, G=G, act=act, op=op)
+    dt = OPS[op]
+    g = gen(13 * M + K + B + G)
+    xu, w, xl = randn((G, K, B), g), randn((G, M, K), g, 1 / math.sqrt(K)), randn((G, M, B), g)
+    wk, e = randn((G, M, K), g, 1 / math.sqrt(K)), randn((G, M, B), g)
+    res = {}
+    try:
+        for mode in (0, 1):
+            _preact(mode)
+            ep = torch.empty((G, M, B), device=DEV, dtype=dt)
+            fp = torch.empty((G, M, B), device=DEV, dtype=dt)
+            wd = _t(wk, dt)
+            if G == 1:
+                build_prediction_error(M, K, B, act, dt, DMA)(_t(xu[0], dt), _t(w[0], dt), _t(xl[0], dt), ep[0])
+                build_forward(M, K, B, act, dt, DMA)(_t(xu[0], dt), _t(w[0], dt), fp[0])
+                build_weight_update(M, K, B, act, dt, DMA, 0.01, True)(wd[0], _t(e[0], dt), _t(xu[0], dt))
+            else:
+                build_prediction_error_batched(M, K, B, G, act, dt, DMA)(_t(xu, dt), _t(w, dt), _t(xl, dt), ep)
+                build_weight_update_batched(M, K, B, G, act, dt, DMA, 0.01, True)(wd, _t(e, dt), _t(xu, dt))
+            res[mode] = (ep, wd) + ((fp,) if G == 1 else ())  # forward has no grouped form
+        torch.cuda.synchronize()
+    finally:
+        _preact(-1)
+    for a, b in zip(res[0], res[1]):
+        assert torch.equal(a, b)
+
+
+def test_preactivation_is_skipped_under_graph_capture():
+    """A captured standalone call keeps the register path (no pool allocation
+    inside the capture); its replays match the direct call bit for bit."""
+    report("dma16-preact-graph")
+    dt = torch.bfloat16
+    M, K, B = 1024, 128, 256
+    g = gen(17)
+    xu, w, xl = _t(randn((K, B), g), dt), _t(randn((M, K), g, 1 / math.sqrt(K)), dt), _t(randn((M, B), g), dt)
+    fn = build_prediction_error(M, K, B, "tanh", dt, DMA)
+    direct = torch.empty((M, B), device=DEV, dtype=dt)
+    captured = torch.empty((M, B), device=DEV, dtype=dt)
+    try:
+        _preact(1)
+        fn(xu, w, xl, direct)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            fn(xu, w, xl, captured)  # warm-up outside the capture
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph):
+            fn(xu, w, xl, captured)
+        for _ in range(3):
+            captured.zero_()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(captured, direct)
+    finally:
+        _preact(-1)
