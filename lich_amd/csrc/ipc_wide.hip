@@ -18,13 +18,15 @@ using dma::Cfg;
 //   split-2 prediction: 128 x 256 (2 stages, waves 2 x 4): 281 us per launch on the wide
 //       configuration against 317 us for 128 x 128 (3 stages, 4 x 2), the alternative;
 //       256 x 128 (2 stages) measured 349 us
-//   inference: 128 x 256 (3, 2 x 4): 177 us against 183 us for 256 x 128 (3, 4 x 2)
-//   weight update: 128 x 256 (3, 2 x 4): 330 us against 353 us for 256 x 128 (3, 4 x 2)
-//       and 128 x 128 (4 stages, 4 x 2)
+//   inference: 128 x 256 (3 stages, 16 waves 4 x 4: 32 x 64 per wave, four waves per SIMD
+//       to hide the LDS and barrier latency): 180 us against 188 us for 128 x 256 with
+//       waves 2 x 4 and 183-188 us for 256 x 128 (3, 4 x 2)
+//   weight update: 128 x 256 (3, 4 x 4): 325 us against 337 us for 128 x 256 (3, 2 x 4),
+//       353 us for 256 x 128 (3, 4 x 2) and more for 128 x 128 (4 stages, 4 x 2)
 #define WIDE_PRED1_CFGS(X) X(256, 128, 3, 4, 2) X(128, 256, 3, 2, 4)
 #define WIDE_PRED2_CFGS(X) X(128, 256, 2, 2, 4) X(128, 128, 3, 4, 2)
-#define WIDE_INFER_CFGS(X) X(128, 256, 3, 2, 4) X(256, 128, 3, 4, 2)
-#define WIDE_WEIGHT_CFGS(X) X(128, 256, 3, 2, 4) X(256, 128, 3, 4, 2) X(128, 128, 4, 4, 2)
+#define WIDE_INFER_CFGS(X) X(128, 256, 3, 4, 4) X(128, 256, 3, 2, 4) X(256, 128, 3, 4, 2)
+#define WIDE_WEIGHT_CFGS(X) X(128, 256, 3, 4, 4) X(128, 256, 3, 2, 4) X(256, 128, 3, 4, 2) X(128, 128, 4, 4, 2)
 #define IPC_COUNT1(...) +1
 constexpr int kPred1Cfgs = 0 WIDE_PRED1_CFGS(IPC_COUNT1), kPred2Cfgs = 0 WIDE_PRED2_CFGS(IPC_COUNT1);
 constexpr int kInferCfgs = 0 WIDE_INFER_CFGS(IPC_COUNT1), kWeightCfgs = 0 WIDE_WEIGHT_CFGS(IPC_COUNT1);

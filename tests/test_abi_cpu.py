@@ -488,7 +488,7 @@ def test_noalloc_entry_point_validates_on_the_host():
 def test_wide_tile_configurations_are_selectable_before_bind():
     lib = _lib()
     assert lib.ipc_plan_wide_config_count(0, nat.SPLIT_W) == 2 and lib.ipc_plan_wide_config_count(0, 1) == 2
-    assert lib.ipc_plan_wide_config_count(1, 1) == 2 and lib.ipc_plan_wide_config_count(2, 1) == 3
+    assert lib.ipc_plan_wide_config_count(1, 1) == 3 and lib.ipc_plan_wide_config_count(2, 1) == 4
     assert lib.ipc_plan_wide_config_count(0, nat.SPLIT_WX) == 0 and lib.ipc_plan_wide_config_count(7, 1) == 0
     assert lib.ipc_plan_set_wide_config(None, 0, 0, 0, -1) == nat.ERR_NULL
     dims = (ctypes.c_int * 4)(10, 64, 64, 784)
@@ -503,7 +503,7 @@ def test_wide_tile_configurations_are_selectable_before_bind():
     try:
         base = lib.ipc_plan_workspace_bytes(h)
         assert lib.ipc_plan_set_wide_config(h, 2, 0, 0, -1) == nat.ERR_CONFIG   # split-2 prediction has 0..1
-        assert lib.ipc_plan_set_wide_config(h, 0, 0, 3, -1) == nat.ERR_CONFIG   # weight has 0..2
+        assert lib.ipc_plan_set_wide_config(h, 0, 0, 4, -1) == nat.ERR_CONFIG   # weight has 0..3
         assert lib.ipc_plan_set_wide_config(h, 0, 0, 0, 3) == nat.ERR_CONFIG    # not a power of two
         assert lib.ipc_plan_set_wide_config(h, -1, 1, 2, 8) == nat.IPC_OK
         assert lib.ipc_plan_workspace_bytes(h) == base                          # same prediction tile
