@@ -72,8 +72,10 @@ class IPCConfig:
     init: str = "kaiming_a_sqrt5"
     # Prediction-phase operand split for 16-bit operands over fp32 master
     # data: 1 plain, 2 = W as hi + lo terms, 3 = W and f(x) both split.  None
-    # picks 3 for narrow nets (every output width <= 128, L <= 16: the
-    # latency-bound whole-step kernel, where the extra MFMAs are free) and 2
+    # picks, for narrow nets (every output width <= 128, L <= 16: the
+    # whole-step kernels), 1 with fp16 operands (their rounding alone stays
+    # about 10x inside the bars, and the split costs ~6 % of the step) and 3
+    # with bf16 (split 1 misses the 5e-3 weight-delta bar on some seeds); 2
     # otherwise (the MFMA-bound wide path).
     pred_split: int | None = None
     # Wide path tile configuration (pred, infer, weight, ksplit), -1 = default
@@ -144,7 +146,10 @@ class HipIPC:
             self.pred_split = int(cfg.pred_split)
         elif self._storage == nat.DT_F32 and self._operand != nat.DT_F32:
             narrow = len(cfg.dims) - 1 <= 16 and max(int(d) for d in cfg.dims[:-1]) <= 128
-            self.pred_split = 3 if narrow else 2
+            if narrow:
+                self.pred_split = 1 if self._operand == nat.DT_F16 else 3
+            else:
+                self.pred_split = 2
         else:
             self.pred_split = 1
         mode = str(cfg.weight_update_mode).lower()

@@ -127,5 +127,7 @@ def test_autotune_writes_tables_the_trainer_reads(tmp_path):
 def test_execution_tuning_times_every_eligible_path():
     report("autotune-exec")
     best, trials = AT.tune_execution([10, 64, 64, 784], 128, "tanh", torch.float16, steps=4, replays=5)
-    assert {t["path"] for t in trials} == {"resident", "narrow", "phased"}
-    assert len(trials) == 12 and best in trials and best["step_ms"] == min(t["step_ms"] for t in trials)
+    # fp16 operands default to split 1 on narrow nets, which the wide path also runs
+    assert {t["path"] for t in trials} == {"resident", "narrow", "phased", "wide"}
+    assert len(trials) == 16 and best in trials and best["step_ms"] == min(t["step_ms"] for t in trials)
+    assert best["path"] == "resident"

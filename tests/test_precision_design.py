@@ -33,9 +33,13 @@ def _run(dims, B, seed, op, split, act="tanh", T=4):
 @pytest.mark.parametrize("op", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("depth", [3, 6])
 def test_paper_profile_design_meets_bars(depth, op, seed):
-    # the trainer's default for narrow nets: split 3
-    s, d = _run((10,) + (64,) * depth + (784,), 128, seed, op, split=3)
+    # the trainer's defaults for narrow nets: split 1 with fp16 operands, 3 with bf16
+    split = 1 if op == torch.float16 else 3
+    s, d = _run((10,) + (64,) * depth + (784,), 128, seed, op, split=split)
     assert s <= 2e-2 and d <= 5e-3, (s, d)
+    if split == 1:
+        # with a wide margin: fp16's rounding alone stays ~10x inside the bars
+        assert s <= 2e-3 and d <= 1.5e-3, (s, d)
 
 
 def test_split_reduces_the_prediction_error():
