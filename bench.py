@@ -40,10 +40,11 @@ METRIC = "iPC train samples/sec (L=6,h=64,B=128); fused-GEMM TFLOP/s vs MFMA pea
 # the same counter's reading for a plain device copy of known size
 # (`bench.py --copy-calibration`: FETCH_SIZE x 2.0, WRITE_SIZE x 1.0).  Keyed
 # by kernel: (bytes, the profile summary that records the pass, the commit of
-# the kernel source it measured).
+# the source it measured; the resident figure is the fp16 unsplit-operand
+# build that the trainer runs by default).
 MEASURED_TRAFFIC = {
     "layer-resident whole-step kernel, 4 steps per launch":
-        (4_319_104 + 3_374_720, "profiles/resident_whole_step_d6_h64_B128.md", "65c76e5"),
+        (3_877_248 + 3_374_720, "profiles/resident_whole_step_d6_h64_B128.md", "2ac391d"),
     "whole-step kernel, 4 steps per launch":
         (13_065_152 + 3_926_848, "profiles/narrow_whole_step_d6_h64_B128.md", "8dc03d3"),
 }
