@@ -147,7 +147,9 @@ class HipIPC:
         elif self._storage == nat.DT_F32 and self._operand != nat.DT_F32:
             narrow = len(cfg.dims) - 1 <= 16 and max(int(d) for d in cfg.dims[:-1]) <= 128
             if narrow:
-                self.pred_split = 1 if self._operand == nat.DT_F16 else 3
+                # fp16 operands need no split with a smooth activation; relu's step-shaped f'
+                # turns operand rounding into flipped derivatives and keeps split 3
+                self.pred_split = 1 if self._operand == nat.DT_F16 and self.act_name != "relu" else 3
             else:
                 self.pred_split = 2
         else:
