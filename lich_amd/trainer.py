@@ -73,10 +73,11 @@ class IPCConfig:
     # Prediction-phase operand split for 16-bit operands over fp32 master
     # data: 1 plain, 2 = W as hi + lo terms, 3 = W and f(x) both split.  None
     # picks, for narrow nets (every output width <= 128, L <= 16: the
-    # whole-step kernels), 1 with fp16 operands (their rounding alone stays
-    # about 10x inside the bars, and the split costs ~6 % of the step) and 3
-    # with bf16 (split 1 misses the 5e-3 weight-delta bar on some seeds); 2
-    # otherwise (the MFMA-bound wide path).
+    # whole-step kernels), 1 with fp16 operands and a smooth activation (their
+    # rounding alone stays about 10x inside the bars, and the split costs ~6 %
+    # of the step), 3 with bf16 (split 1 misses the 5e-3 weight-delta bar on
+    # some seeds) or relu (unsplit operands flip f' near 0); 2 otherwise (the
+    # MFMA-bound wide path).
     pred_split: int | None = None
     # Wide path tile configuration (pred, infer, weight, ksplit), -1 = default
     # (ipc_plan_set_wide_config); a policy file's tuned choice takes precedence.

@@ -30,6 +30,14 @@ def _split(t: torch.Tensor, op: torch.dtype):
     return hi, _r(t - hi, op)
 
 
+def weight_pair(w: torch.Tensor, op: torch.dtype) -> torch.Tensor:
+    """W as a wide plan with weight pairs stores it: float(hi) + float(lo) with
+    hi = cvt(W), lo = cvt(W - hi) (about 17 significant bits; the fp32 sum
+    rounds once more where lo lies far below hi).  The value is its own pair."""
+    hi, lo = _split(w, op)
+    return hi + lo
+
+
 def pred_matmul(w: torch.Tensor, a: torch.Tensor, op: torch.dtype, split: int = 1) -> torch.Tensor:
     """``w @ a`` with 16-bit operands: split 1 rounds both operands once;
     split 2 carries ``w`` as hi + lo terms; split 3 carries both operands as
@@ -57,16 +65,21 @@ def forward_init_operand16(x_input, y_target, w, *, act: str, op: torch.dtype, s
 
 
 def step_operand16(x: Sequence[torch.Tensor], w: Sequence[torch.Tensor], *, act: str, alpha: float,
-                   gamma: float, op: torch.dtype, split: int = 1):
+                   gamma: float, op: torch.dtype, split: int = 1, w_pairs: bool = False):
     """fp32 master x/eps/W; GEMM operands rounded to ``op`` (the prediction
-    optionally split, see ``pred_matmul``); fp32 accumulate."""
+    optionally split, see ``pred_matmul``); fp32 accumulate.  ``w_pairs``: W is
+    stored as its hi + lo pair (``weight_pair``) before and after the update."""
     L = len(w)
+    if w_pairs:
+        w = [weight_pair(v, op) for v in w]
     e = [x[l] - pred_matmul(w[l], act_forward(act, x[l + 1]), op, split) for l in range(L)]
     new_x = [v.clone() for v in x]
     for l in range(1, L):
         sig = _r(w[l - 1], op).T @ _r(e[l - 1], op)
         new_x[l] = x[l] + gamma * (-e[l] + act_derivative(act, x[l]) * sig)
     new_w = [w[l] + alpha * (_r(e[l], op) @ _r(act_forward(act, new_x[l + 1]), op).T) for l in range(L)]
+    if w_pairs:
+        new_w = [weight_pair(v, op) for v in new_w]
     return new_x, new_w, e
 
 
