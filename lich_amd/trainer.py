@@ -73,11 +73,12 @@ class IPCConfig:
     # Prediction-phase operand split for 16-bit operands over fp32 master
     # data: 1 plain, 2 = W as hi + lo terms, 3 = W and f(x) both split.  None
     # picks, for narrow nets (every output width <= 128, L <= 16: the
-    # whole-step kernels), 1 with fp16 operands and a smooth activation (their
-    # rounding alone stays about 10x inside the bars, and the split costs ~6 %
+    # whole-step kernels), 1 with fp16 operands and tanh or sigmoid (their
+    # rounding alone stays 6x or more inside the bars, and the split costs ~6 %
     # of the step), 3 with bf16 (split 1 misses the 5e-3 weight-delta bar on
-    # some seeds) or relu (unsplit operands flip f' near 0); 2 otherwise (the
-    # MFMA-bound wide path).
+    # some seeds) or relu, silu, gelu (f' steps or crosses zero: unsplit
+    # operands reach 0.5x the bar or beyond); 2 otherwise (the MFMA-bound
+    # wide path).
     pred_split: int | None = None
     # Wide path tile configuration (pred, infer, weight, ksplit), -1 = default
     # (ipc_plan_set_wide_config); a policy file's tuned choice takes precedence.
@@ -148,9 +149,11 @@ class HipIPC:
         elif self._storage == nat.DT_F32 and self._operand != nat.DT_F32:
             narrow = len(cfg.dims) - 1 <= 16 and max(int(d) for d in cfg.dims[:-1]) <= 128
             if narrow:
-                # fp16 operands need no split with a smooth activation; relu's step-shaped f'
-                # turns operand rounding into flipped derivatives and keeps split 3
-                self.pred_split = 1 if self._operand == nat.DT_F16 and self.act_name != "relu" else 3
+                # fp16 operands need no split with a monotone smooth activation; relu's
+                # step and the zero crossings of silu's and gelu's f' make operand
+                # rounding flip or swing derivatives, so those keep split 3
+                monotone = self.act_name in ("tanh", "sigmoid")
+                self.pred_split = 1 if self._operand == nat.DT_F16 and monotone else 3
             else:
                 self.pred_split = 2
         else:

@@ -54,6 +54,20 @@ def test_relu_keeps_the_split_with_fp16_operands(seed):
     assert s1 > 10 * s3 and d1 > 5 * d3, (s1, s3, d1, d3)
 
 
+@pytest.mark.parametrize("act", ["silu", "gelu"])
+def test_zero_crossing_derivatives_keep_the_split_with_fp16_operands(act):
+    # silu's and gelu's f' cross zero: unsplit fp16 operands take the weight-delta error
+    # to 2.1-2.4e-3 at d = 3 (about half the bar) against ~1.3e-4 with split 3; tanh and
+    # sigmoid stay at or below 8.4e-4 unsplit, so only they default to split 1
+    dims = (10,) + (64,) * 3 + (784,)
+    r1 = [_run(dims, 128, seed, torch.float16, split=1, act=act) for seed in range(5)]
+    r3 = [_run(dims, 128, seed, torch.float16, split=3, act=act) for seed in range(5)]
+    d1, d3 = max(d for _s, d in r1), max(d for _s, d in r3)
+    assert d1 > 1.5e-3 and d3 <= 2e-4, (d1, d3)
+    for smooth in ("tanh", "sigmoid"):
+        assert max(_run(dims, 128, seed, torch.float16, split=1, act=smooth)[1] for seed in range(5)) <= 1e-3
+
+
 def test_split_reduces_the_prediction_error():
     dims = (10,) + (64,) * 4 + (784,)
     errs = {k: _run(dims, 128, 0, torch.bfloat16, split=k)[1] for k in (1, 2, 3)}
