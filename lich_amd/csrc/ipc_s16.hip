@@ -12,8 +12,17 @@ namespace {
 
 using dma::Cfg;
 
+// Tile configurations (BM, BN, stages, waves along M, waves along N): the
+// prediction, forward and inference kernels run 256 x 128 tiles with 16 waves
+// (64 x 32 per wave, four per SIMD to hide the LDS reads and barriers), 1-10 %
+// faster than 8 waves at M = K >= 4096, B >= 2048; the weight update keeps 8
+// waves (64 x 64 each), within +-3 % of 16.  The k order, and so every result
+// bit, does not depend on the wave layout.
 #ifndef S16_CFG
-#define S16_CFG 256, 128, 3, 4, 2
+#define S16_CFG 256, 128, 3, 4, 4
+#endif
+#ifndef S16_WCFG
+#define S16_WCFG 256, 128, 3, 4, 2
 #endif
 
 template <typename OT>
@@ -26,7 +35,7 @@ struct S16 {
         case S16_PRED: return Cfg<OT, S16_PRED, 1, ACT, R, S16_CFG>::launch(probs, count, s);
         case S16_FWD: return Cfg<OT, S16_FWD, 1, ACT, R, S16_CFG>::launch(probs, count, s);
         case S16_INFER: return Cfg<OT, S16_INFER, 1, ACT, false, S16_CFG>::launch(probs, count, s);
-        default: return Cfg<OT, S16_WEIGHT, 1, ACT, R, S16_CFG>::launch(probs, count, s);
+        default: return Cfg<OT, S16_WEIGHT, 1, ACT, R, S16_WCFG>::launch(probs, count, s);
       }
     }
   };
