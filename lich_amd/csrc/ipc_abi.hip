@@ -487,6 +487,7 @@ struct ipc_plan {
   long long res_ws_off = 0;
   // wide GEMM path
   bool wide = false;
+  bool wdirect = false;  // wide, split 2: the prediction reads W itself (no Wh / Wl copies)
   std::vector<WideProblem> wpred, winfer, wweight, wfwd;  // wfwd: l = L-1 .. 1
   int pred_ksplit = 1;                                    // > 1: layer 0's prediction is k-split (last in wpred)
   int wcfg[3] = {0, 0, 0};                                // tile configuration of the pred / infer / weight launches
@@ -614,11 +615,19 @@ struct WideLayout {
     total += wide_pad(b.rows * b.ld * 2, 256);
     return b;
   }
-  WideLayout(const std::vector<int>& d, int L, int B, bool split2, int pred_cfg) {
+  // direct: the split-2 prediction reads the fp32 W (ld = d_{l+1}, a multiple
+  // of WIDE_BK) in place of Wh / Wl, which then get no storage (their ld and
+  // rows still give the contraction lengths and row counts)
+  WideLayout(const std::vector<int>& d, int L, int B, bool split2, int pred_cfg, bool direct = false) {
     wh.resize(L); wl.resize(L); wt.resize(L); f.resize(L + 1); ft.resize(L + 1); e.resize(L); et.resize(L);
     for (int l = 0; l < L; ++l) {
-      wh[l] = add(d[l], d[l + 1]);                  // [d_l][d_{l+1}]  pred A
-      if (split2) wl[l] = add(d[l], d[l + 1]);      //                 pred A_lo
+      if (direct) {
+        wh[l].ld = d[l + 1];
+        wh[l].rows = d[l];
+      } else {
+        wh[l] = add(d[l], d[l + 1]);                // [d_l][d_{l+1}]  pred A
+        if (split2) wl[l] = add(d[l], d[l + 1]);    //                 pred A_lo
+      }
       if (l <= L - 2) wt[l] = add(d[l + 1], d[l]);  // [d_{l+1}][d_l]  infer A (layer l+1)
     }
     for (int l = 1; l <= L; ++l) {
@@ -859,7 +868,12 @@ int ipc_plan_create(ipc_plan** out, int L, const int* dims, int B, int storage, 
     p->res_ws_off = (p->ws_bytes + 255) / 256 * 256;
     p->ws_bytes = p->res_ws_off + res_bytes;
   }
-  if (p->wide) p->ws_bytes = WideLayout(p->dims, L, B, p->split == IPC_SPLIT_W, 0).total;
+  if (p->wide) {
+    // the split-2 prediction reads W itself when every contraction is whole k-steps
+    p->wdirect = p->split == IPC_SPLIT_W;
+    for (int l = 0; l < L; ++l) p->wdirect = p->wdirect && dims[l + 1] % WIDE_BK == 0;
+    p->ws_bytes = WideLayout(p->dims, L, B, p->split == IPC_SPLIT_W, 0, p->wdirect).total;
+  }
   *out = p;
   return ok();
 }
@@ -942,7 +956,11 @@ int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w
     plan->launches = 1;
   }
   if (plan->wide) {
-    const WideLayout lay(d, L, B, plan->split == IPC_SPLIT_W, plan->wcfg[0]);
+    const WideLayout lay(d, L, B, plan->split == IPC_SPLIT_W, plan->wcfg[0], plan->wdirect);
+    if (plan->wdirect)
+      for (int l = 0; l < L; ++l)
+        if (reinterpret_cast<uintptr_t>(w[l]) % 16 != 0)
+          return fail(IPC_ERR_ALIGN, "W[%d] must be 16-byte aligned: the wide prediction reads it directly", l);
     char* ws = static_cast<char*>(workspace);
     auto buf = [&](const WideLayout::Buf& b) -> void* { return b.off < 0 ? nullptr : ws + b.off; };
     auto a16 = [](const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
@@ -952,6 +970,7 @@ int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w
       WideProblem q{};
       q.M = d[l]; q.N = B; q.K = (int)lay.wh[l].ld;
       q.a = buf(lay.wh[l]); q.a_lo = buf(lay.wl[l]); q.lda = lay.wh[l].ld; q.a_lim = (int)lay.wh[l].rows;
+      if (plan->wdirect) { q.a = w[l]; q.a_lo = nullptr; q.lda = d[l + 1]; q.a_lim = d[l]; }
       q.b = buf(lay.ft[l + 1]); q.ldb = lay.ft[l + 1].ld; q.b_lim = (int)lay.ft[l + 1].rows;
       q.out = e[l]; q.ldo = B;
       q.aux = x[l]; q.ldx = B;
@@ -1013,7 +1032,7 @@ int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w
       q.a = buf(lay.e[l]); q.lda = lay.e[l].ld; q.a_lim = (int)lay.e[l].rows;
       q.b = buf(lay.f[l + 1]); q.ldb = lay.f[l + 1].ld; q.b_lim = (int)lay.f[l + 1].rows;
       q.out = w[l]; q.ldo = d[l + 1];
-      q.h = buf(lay.wh[l]); q.ldh = lay.wh[l].ld;
+      q.h = buf(lay.wh[l]); q.ldh = lay.wh[l].ld;  // null with wdirect: only W and WT are stored
       q.hl = buf(lay.wl[l]); q.ldhl = lay.wl[l].ld;
       q.t = buf(lay.wt[l]); q.ldt = lay.wt[l].ld;
       q.scal = plan->alpha;
@@ -1067,7 +1086,7 @@ int run_phase(ipc_plan* plan, int phase, hipStream_t s) {
     switch (phase) {
       case IPC_PHASE_PRED:
         TRY(launch_rc(launch_wide(WIDE_PRED, plan->wpred.data(), (int)plan->wpred.size(), plan->operand,
-                                  plan->split == IPC_SPLIT_W ? 2 : 1, plan->act, s, plan->wcfg[0]),
+                                  plan->split == IPC_SPLIT_W ? 2 : 1, plan->act, s, plan->wcfg[0], plan->wdirect),
                       "wide prediction phase"));
         if (plan->pred_ksplit > 1)
           return launch_rc(launch_wide_reduce(plan->wreduce, plan->operand, s), "wide prediction reduce");
@@ -1142,7 +1161,8 @@ int ipc_plan_forward_init(ipc_plan* plan, void* stream) {
     TRY(launch_rc(launch_wide_copy(plan->wsync_init.data(), (int)plan->wsync_init.size(), plan->operand, s),
                   "wide operand copies"));
     for (auto& q : plan->wfwd)
-      TRY(launch_rc(launch_wide(WIDE_FWD, &q, 1, plan->operand, plan->split == IPC_SPLIT_W ? 2 : 1, plan->act, s),
+      TRY(launch_rc(launch_wide(WIDE_FWD, &q, 1, plan->operand, plan->split == IPC_SPLIT_W ? 2 : 1, plan->act, s, 0,
+                                plan->wdirect),
                     "wide forward init"));
     return ok();
   }
@@ -1203,7 +1223,8 @@ int ipc_plan_set_wide_config(ipc_plan* plan, int pred_cfg, int infer_cfg, int we
   for (int ph = 0; ph < 3; ++ph) plan->wcfg[ph] = c[ph] < 0 ? 0 : c[ph];
   plan->ksplit_request = ksplit < 0 ? 0 : ksplit;
   // the prediction tile sets how many k-split slices the workspace holds
-  plan->ws_bytes = WideLayout(plan->dims, plan->L, plan->B, plan->split == IPC_SPLIT_W, plan->wcfg[0]).total;
+  plan->ws_bytes =
+      WideLayout(plan->dims, plan->L, plan->B, plan->split == IPC_SPLIT_W, plan->wcfg[0], plan->wdirect).total;
   return ok();
 }
 

@@ -25,6 +25,10 @@
 //     the stage everybody has finished with;
 //   * fragments of the next 16-k slice are read while the current slice's
 //     MFMAs run; split 2 adds the A_lo B products (error compensation);
+//   * A32 (split-2 wide prediction and forward): A is the fp32 W itself, 64
+//     k-values per 256-byte LDS row (chunk c of row r at c ^ (r & 15)), split
+//     into its hi and lo 16-bit fragments as it is read (the values the
+//     separate hi / lo copies would hold, in the same bytes per stage);
 //   * workgroups are renumbered so that the tiles one XCD runs are consecutive
 //     (the tiles sharing rows of A share that XCD's L2);
 //   * a k-split prediction problem (last in its launch) runs each tile as
@@ -82,6 +86,15 @@ __device__ __forceinline__ int mn_swz(int r, int c) { return c ^ ((r & 3) << 2);
 // Global source of LDS slot `slot` (16 bytes) of an operand block.
 //   KC: rows e0 .. e0+EDGE-1 (clamped to lim-1), k0 .. k0+63
 //   MN: k-rows k0 .. k0+63, columns e0 .. e0+EDGE-1 (chunk starts clamped to lim-8)
+// Global source of LDS slot `slot` (16 bytes = 4 floats) of an fp32
+// k-contiguous block: rows e0 .. e0+EDGE-1 (clamped to lim-1), k0 .. k0+63.
+template <int EDGE>
+__device__ __forceinline__ const float* slot_src32(const float* g, long long ld, int e0, int lim, int k0, int slot) {
+  const int r = slot >> 4, c = (slot & 15) ^ (r & 15);
+  const int row = e0 + r < lim ? e0 + r : lim - 1;
+  return g + (long long)row * ld + k0 + c * 4;
+}
+
 template <typename OT, bool MN, int EDGE>
 __device__ __forceinline__ const OT* slot_src(const OT* g, long long ld, int e0, int lim, int k0, int slot) {
   if (!MN) {
@@ -95,6 +108,18 @@ __device__ __forceinline__ const OT* slot_src(const OT* g, long long ld, int e0,
     return g + (long long)(k0 + r) * ld + col;
   }
 }
+
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+
+// The fp32 values of 8 packed 16-bit operands (bf16: each half of a packed
+// word shifted into place, so that no value is converted a second time).
+__device__ __forceinline__ f32x8 widen8(bf16x8 h) {
+  const uint4 u = __builtin_bit_cast(uint4, h);
+  auto lo = [](unsigned w) { return __builtin_bit_cast(float, w << 16); };
+  auto hi = [](unsigned w) { return __builtin_bit_cast(float, w & 0xffff0000u); };
+  return f32x8{lo(u.x), hi(u.x), lo(u.y), hi(u.y), lo(u.z), hi(u.z), lo(u.w), hi(u.w)};
+}
+__device__ __forceinline__ f32x8 widen8(f16x8 h) { return __builtin_convertvector(h, f32x8); }
 
 template <typename OT>
 __device__ __forceinline__ unsigned pack2(OT a, OT b) {
@@ -112,6 +137,7 @@ __device__ __forceinline__ float hi16(unsigned v) {
 
 // Dynamic LDS of a configuration: the pipeline stages, reused by the fp32
 // epilogue tile (BM rows of BN + 1 floats).
+// (LO: the A_lo block, or A stored as fp32 rows of twice the bytes.)
 constexpr int smem_bytes(int BM, int BN, int S, bool LO) {
   return S * (BM * 128 * (LO ? 2 : 1) + BN * 128) > BM * (BN + 1) * 4 ? S * (BM * 128 * (LO ? 2 : 1) + BN * 128)
                                                                      : BM * (BN + 1) * 4;
@@ -145,16 +171,21 @@ struct Batch {
 // ACT: the epilogue activation (WIDE_INFER, WIDE_FWD, S16_INFER) or the
 // activation of the register-path B operand (BREG: S16_PRED, S16_FWD,
 // S16_WEIGHT recompute); ACT_IDENTITY otherwise.
-template <typename OT, int MODE, int SPLIT, int ACT, bool BREG, int BM, int BN, int S, int WGM, int WGN>
+template <typename OT, int MODE, int SPLIT, int ACT, bool BREG, int BM, int BN, int S, int WGM, int WGN,
+          bool A32 = false>
 __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr bool LO = SPLIT == 2;
   constexpr bool AMN = a_mn(MODE), BMN = b_mn(MODE), S16 = is_s16(MODE);
+  static_assert(!A32 || (LO && !AMN && !S16 && !BREG), "fp32 A: the split-2 wide prediction and forward");
   constexpr int NW = WGM * WGN, NT = NW * 64;
-  constexpr int A_BYTES = BM * 128, B_BYTES = BN * 128;
-  constexpr int STAGE = A_BYTES * (LO ? 2 : 1) + B_BYTES;
+  // A: one 16-bit block of 128-byte rows (and its A_lo block), or one fp32
+  // block of 256-byte rows (A32): the same bytes per stage
+  constexpr int A_BYTES = BM * (A32 ? 256 : 128), B_BYTES = BN * 128;
+  constexpr int A_BLOCKS = LO && !A32 ? 2 : 1;
+  constexpr int STAGE = A_BYTES * A_BLOCKS + B_BYTES;
   constexpr int IA = A_BYTES / 1024 / NW, IB = B_BYTES / 1024 / NW;  // DMA instructions per wave and stage
-  constexpr int LPS = IA * (LO ? 2 : 1) + (BREG ? 0 : IB);
+  constexpr int LPS = IA * A_BLOCKS + (BREG ? 0 : IB);
   constexpr int RB = B_BYTES / 16 / NT;                               // register-path chunks per thread
   constexpr int WTM = BM / WGM, WTN = BN / WGN, RM = WTM / 32, RN = WTN / 32;
   using MF = Mfma32<OT>;
@@ -189,6 +220,7 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int wm = w / WGN, wn = w % WGN;
   const OT* A = reinterpret_cast<const OT*>(p.a);
+  const float* A32p = reinterpret_cast<const float*>(p.a);  // A32: the fp32 W
   const OT* Al = reinterpret_cast<const OT*>(p.a_lo);
   const OT* Bg = reinterpret_cast<const OT*>(p.b);
   const long long lda = p.lda, ldb = p.ldb;
@@ -201,11 +233,16 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
 #pragma unroll
     for (int q = 0; q < IA; ++q) {
       const int blk = q * NW + w;
-      const OT* src = slot_src<OT, AMN, BM>(A, lda, m0, alim, k0, blk * 64 + lane);
-      __builtin_amdgcn_global_load_lds((glb_void*)src, (lds_void*)(st + blk * 1024), 16, 0, 0);
-      if (LO) {
-        const OT* srl = slot_src<OT, AMN, BM>(Al, lda, m0, alim, k0, blk * 64 + lane);
-        __builtin_amdgcn_global_load_lds((glb_void*)srl, (lds_void*)(st + A_BYTES + blk * 1024), 16, 0, 0);
+      if constexpr (A32) {
+        const float* src = slot_src32<BM>(A32p, lda, m0, alim, k0, blk * 64 + lane);
+        __builtin_amdgcn_global_load_lds((glb_void*)src, (lds_void*)(st + blk * 1024), 16, 0, 0);
+      } else {
+        const OT* src = slot_src<OT, AMN, BM>(A, lda, m0, alim, k0, blk * 64 + lane);
+        __builtin_amdgcn_global_load_lds((glb_void*)src, (lds_void*)(st + blk * 1024), 16, 0, 0);
+        if (LO) {
+          const OT* srl = slot_src<OT, AMN, BM>(Al, lda, m0, alim, k0, blk * 64 + lane);
+          __builtin_amdgcn_global_load_lds((glb_void*)srl, (lds_void*)(st + A_BYTES + blk * 1024), 16, 0, 0);
+        }
       }
     }
     if (!BREG) {
@@ -213,7 +250,7 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
       for (int q = 0; q < IB; ++q) {
         const int blk = q * NW + w;
         const OT* src = slot_src<OT, BMN, BN>(Bg, ldb, n0, blim, k0, blk * 64 + lane);
-        __builtin_amdgcn_global_load_lds((glb_void*)src, (lds_void*)(st + A_BYTES * (LO ? 2 : 1) + blk * 1024),
+        __builtin_amdgcn_global_load_lds((glb_void*)src, (lds_void*)(st + A_BYTES * A_BLOCKS + blk * 1024),
                                          16, 0, 0);
       }
     }
@@ -230,7 +267,7 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
   };
   auto store_breg = [&](int stage) {
     if (BREG) {
-      unsigned char* sb = smem + stage * STAGE + A_BYTES * (LO ? 2 : 1);
+      unsigned char* sb = smem + stage * STAGE + A_BYTES * A_BLOCKS;
 #pragma unroll
       for (int i = 0; i < RB; ++i) {
         const unsigned in[4] = {breg[i].x, breg[i].y, breg[i].z, breg[i].w};
@@ -328,6 +365,19 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
     if (AMN) return frag_mn(blk, BM * 2, wm * WTM + i * 32, kk);
     return frag_kc(blk, wm * WTM + i * 32, kk);
   };
+  // A32: the 8 fp32 k-values of the lane (two 16-byte chunks of its row)
+  // split into hi = cvt(w) and lo = cvt(w - hi), converted as a vector (packed
+  // round-to-nearest-even conversions, the same bits as cvt of each value: the
+  // values come from LDS, with no product the compiler could fold in)
+  auto frag_a32 = [&](const unsigned char* blk, int i, int kk, V& hi, V& lo) {
+    const unsigned char* rb = blk + (wm * WTM + i * 32 + lr) * 256;
+    const int c0 = kk * 4 + lk * 2, sw = lr & 15;
+    const f32x4 w0 = *reinterpret_cast<const f32x4*>(rb + ((c0 ^ sw) << 4));
+    const f32x4 w1 = *reinterpret_cast<const f32x4*>(rb + (((c0 + 1) ^ sw) << 4));
+    const f32x8 wv = __builtin_shufflevector(w0, w1, 0, 1, 2, 3, 4, 5, 6, 7);
+    hi = __builtin_convertvector(wv, V);
+    lo = __builtin_convertvector(wv - widen8(hi), V);  // w - hi is exact
+  };
   auto frag_b = [&](const unsigned char* blk, int j, int kk) -> V {
     if (BMN) return frag_mn(blk, BN * 2, wn * WTN + j * 32, kk);
     return frag_kc(blk, wn * WTN + j * 32, kk);
@@ -348,7 +398,7 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
 
     const unsigned char* sa = smem + stage * STAGE;
     const unsigned char* sal = sa + A_BYTES;
-    const unsigned char* sb = sa + A_BYTES * (LO ? 2 : 1);
+    const unsigned char* sb = sa + A_BYTES * A_BLOCKS;
     V af[2][RM], bf[2][RN], alf[2][LO ? RM : 1];
     // Software pipeline over the 16-k slices of the stage: the reads of
     // slice kk+1 go out while slice kk's MFMAs run.  A scheduling barrier
@@ -358,8 +408,12 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
     for (int j = 0; j < RN; ++j) bf[0][j] = frag_b(sb, j, 0);
 #pragma unroll
     for (int i = 0; i < RM; ++i) {
-      af[0][i] = frag_a(sa, i, 0);
-      if (LO) alf[0][i] = frag_a(sal, i, 0);
+      if constexpr (A32) {
+        frag_a32(sa, i, 0, af[0][i], alf[0][LO ? i : 0]);
+      } else {
+        af[0][i] = frag_a(sa, i, 0);
+        if (LO) alf[0][i] = frag_a(sal, i, 0);
+      }
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -370,8 +424,12 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
         for (int j = 0; j < RN; ++j) bf[nxt][j] = frag_b(sb, j, kk + 1);
 #pragma unroll
         for (int i = 0; i < RM; ++i) {
-          af[nxt][i] = frag_a(sa, i, kk + 1);
-          if (LO) alf[nxt][i] = frag_a(sal, i, kk + 1);
+          if constexpr (A32) {
+            frag_a32(sa, i, kk + 1, af[nxt][i], alf[nxt][LO ? i : 0]);
+          } else {
+            af[nxt][i] = frag_a(sa, i, kk + 1);
+            if (LO) alf[nxt][i] = frag_a(sal, i, kk + 1);
+          }
         }
       }
 #pragma unroll
@@ -499,7 +557,7 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
         if (vec && nv == 4) {
           *reinterpret_cast<float4*>(op) = make_float4(v[0], v[1], v[2], v[3]);
           uint2 hh; hh.x = pack2(hv[0], hv[1]); hh.y = pack2(hv[2], hv[3]);
-          *reinterpret_cast<uint2*>(hp) = hh;
+          if (MODE != WIDE_WEIGHT || p.h) *reinterpret_cast<uint2*>(hp) = hh;
           if (MODE == WIDE_WEIGHT && p.hl) {
             uint2 ll; ll.x = pack2(lv[0], lv[1]); ll.y = pack2(lv[2], lv[3]);
             *reinterpret_cast<uint2*>(reinterpret_cast<OT*>(p.hl) + (long long)m * p.ldhl + n) = ll;
@@ -510,7 +568,7 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
         } else {
           for (int q = 0; q < nv; ++q) {
             op[q] = v[q];
-            hp[q] = hv[q];
+            if (MODE != WIDE_WEIGHT || p.h) hp[q] = hv[q];
             if (MODE == WIDE_WEIGHT && p.hl) reinterpret_cast<OT*>(p.hl)[(long long)m * p.ldhl + n + q] = lv[q];
             if (MODE == WIDE_INFER && p.out2) reinterpret_cast<float*>(p.out2)[(long long)m * p.ld2 + n + q] = fv[q];
           }
@@ -552,12 +610,13 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
 
 // One kernel configuration: LDS limit set once per process, launch over a
 // ragged batch of up to WIDE_MAX_BATCH problems.
-template <typename OT, int MODE, int SPLIT, int ACT, bool BREG, int BM, int BN, int S, int WGM, int WGN>
+template <typename OT, int MODE, int SPLIT, int ACT, bool BREG, int BM, int BN, int S, int WGM, int WGN,
+          bool A32 = false>
 struct Cfg {
   static constexpr int smem = smem_bytes(BM, BN, S, SPLIT == 2);
   static constexpr int BM_ = BM, BN_ = BN;
   static const void* fn() {
-    return reinterpret_cast<const void*>(&dma_gemm_kernel<OT, MODE, SPLIT, ACT, BREG, BM, BN, S, WGM, WGN>);
+    return reinterpret_cast<const void*>(&dma_gemm_kernel<OT, MODE, SPLIT, ACT, BREG, BM, BN, S, WGM, WGN, A32>);
   }
   static hipError_t prepare() {
     static const hipError_t e = hipFuncSetAttribute(fn(), hipFuncAttributeMaxDynamicSharedMemorySize, smem);
@@ -571,7 +630,7 @@ struct Cfg {
     bt.tail = count;
     int total = 0;
     for (int i = 0; i < count; ++i) {
-      if (SPLIT == 2 && MODE == WIDE_PRED && !probs[i].a_lo) return hipErrorInvalidValue;
+      if (SPLIT == 2 && MODE == WIDE_PRED && !A32 && !probs[i].a_lo) return hipErrorInvalidValue;
       const int ks = MODE == WIDE_PRED && probs[i].ksplit > 1 ? probs[i].ksplit : 1;
       if (ks > 1) {
         if (probs[i].K % (ks * WIDE_BK) != 0) return hipErrorInvalidValue;

@@ -60,12 +60,13 @@ inline long long wide_pad(long long v, long long m) { return (v + m - 1) / m * m
 // tiles that reach past M or N clamp their loads there and mask their stores.
 struct WideProblem {
   int M, N, K;
-  const void* a; const void* a_lo; long long lda; int a_lim;  // a_lo: split-2 term (pred) or nullptr
+  const void* a; const void* a_lo; long long lda; int a_lim;  // a_lo: split-2 term (pred) or nullptr;
+                                                              // a fp32 (a_lo unused) in launch_wide's a32 mode
   const void* b; long long ldb; int b_lim;
   void* out; long long ldo;        // WIDE: pred eps[l], fwd x[l] (written); infer x[l], weight W[l] (updated), fp32
                                    // S16:  pred E, fwd OUT (written); infer X, weight W (updated), 16-bit
   const void* aux; long long ldx;  // WIDE pred: x[l], infer: eps[l] (fp32); S16 pred: X_lower, infer: E (16-bit)
-  void* h; long long ldh;          // WIDE: 16-bit copy [M][ldh]: pred E, infer/fwd F, weight Wh
+  void* h; long long ldh;          // WIDE: 16-bit copy [M][ldh]: pred E, infer/fwd F, weight Wh (or null)
   void* hl; long long ldhl;        // WIDE weight: Wl [M][ldhl]
   void* t; long long ldt;          // WIDE: transposed 16-bit copy [N][ldt] (pred ET, infer/fwd FT, weight WT), or null
   void* out2; long long ld2;       // infer, save mode: f(x_new) (fp32 for WIDE, 16-bit for S16), or null
@@ -104,9 +105,11 @@ void wide_pred_tile(int split, int cfg, int* bm, int* bn);
 // Launches one phase of the wide path over `count` layers (one launch per
 // WIDE_MAX_BATCH layers) on tile configuration `cfg`.  `operand` is DT_F16
 // or DT_BF16, `split` 1 or 2 (pred and fwd), `act` the activation of the
-// infer / fwd epilogues.
+// infer / fwd epilogues.  `a32` (split-2 pred and fwd): each problem's `a`
+// is the fp32 W itself (a_lo unused, K a multiple of WIDE_BK, rows 16-byte
+// aligned), split into its hi and lo operands as the kernel reads it.
 hipError_t launch_wide(int mode, const WideProblem* probs, int count, int operand, int split, int act,
-                       hipStream_t s, int cfg = 0);
+                       hipStream_t s, int cfg = 0, bool a32 = false);
 
 // Raises the dynamic-LDS limit of every wide-path kernel instantiation.
 hipError_t wide_prepare();
@@ -122,7 +125,7 @@ hipError_t launch_s16_activate(const void* in, void* out, long long n, int opera
 
 // Refresh of the 16-bit copies from the fp32 masters (after the masters were
 // written outside a step):
-//   dst[r][c] = cvt(f(src[r][c]))      (and dst_lo = cvt(v - hi) when given)
+//   dst[r][c] = cvt(f(src[r][c]))      (when given; dst_lo = cvt(v - hi) when given)
 //   dst_t[c][r] = the same hi value    (when given)
 // for r < rows, c < cols; f is the activation `act` (ACT_IDENTITY for W).
 struct WideCopy {

@@ -25,46 +25,55 @@ using dma::Cfg;
 //       353 us for 256 x 128 (3, 4 x 2) and more for 128 x 128 (4 stages, 4 x 2)
 #define WIDE_PRED1_CFGS(X) X(256, 128, 3, 4, 2) X(128, 256, 3, 2, 4)
 #define WIDE_PRED2_CFGS(X) X(128, 256, 2, 2, 4) X(128, 128, 3, 4, 2)
+// the split-2 prediction reading the fp32 W (a32): waves 4 x 2, so that each
+// wave splits its 32-row A fragment for 4 column blocks (two waves share it)
+#define WIDE_PRED2A_CFGS(X) X(128, 256, 2, 4, 2) X(128, 128, 3, 4, 2)
 #define WIDE_INFER_CFGS(X) X(128, 256, 3, 4, 4) X(128, 256, 3, 2, 4) X(256, 128, 3, 4, 2)
 #define WIDE_WEIGHT_CFGS(X) X(128, 256, 3, 4, 4) X(128, 256, 3, 2, 4) X(256, 128, 3, 4, 2) X(128, 128, 4, 4, 2)
 #define IPC_COUNT1(...) +1
 constexpr int kPred1Cfgs = 0 WIDE_PRED1_CFGS(IPC_COUNT1), kPred2Cfgs = 0 WIDE_PRED2_CFGS(IPC_COUNT1);
 constexpr int kInferCfgs = 0 WIDE_INFER_CFGS(IPC_COUNT1), kWeightCfgs = 0 WIDE_WEIGHT_CFGS(IPC_COUNT1);
+static_assert(0 WIDE_PRED2A_CFGS(IPC_COUNT1) == kPred2Cfgs, "one a32 configuration per split-2 prediction one");
 
 // forward initialisation: the split-1 prediction tiles; split 2 keeps 128 x 128
 // (one layer per launch: its tiles fill all CUs once per 4096-row layer, 82 us
 // per layer against 120 us on the prediction's 128 x 256 tiles; the sums per
 // element do not depend on the tile, so the first prediction errors stay exactly 0)
 template <typename OT, int ACT> using FwdCfg1 = Cfg<OT, WIDE_FWD, 1, ACT, false, 256, 128, 3, 4, 2>;
-template <typename OT, int ACT> using FwdCfg2 = Cfg<OT, WIDE_FWD, 2, ACT, false, 128, 128, 3, 4, 2>;
+template <typename OT, int ACT, bool A32> using FwdCfg2 = Cfg<OT, WIDE_FWD, 2, ACT, false, 128, 128, 3, 4, 2, A32>;
 
 // Launches (or prepares) configuration `cfg` of a list: the i-th X(...) entry.
-#define IPC_CFG_CASE(MODE_, SPLIT_, ACT_, BM_, BN_, S_, WM_, WN_)                                     \
-  if (cfg == i++) return prep ? Cfg<OT, MODE_, SPLIT_, ACT_, false, BM_, BN_, S_, WM_, WN_>::prepare()   \
-                              : Cfg<OT, MODE_, SPLIT_, ACT_, false, BM_, BN_, S_, WM_, WN_>::launch(probs, count, s);
-#define IPC_P1(BM_, BN_, S_, WM_, WN_) IPC_CFG_CASE(WIDE_PRED, 1, ACT_IDENTITY, BM_, BN_, S_, WM_, WN_)
-#define IPC_P2(BM_, BN_, S_, WM_, WN_) IPC_CFG_CASE(WIDE_PRED, 2, ACT_IDENTITY, BM_, BN_, S_, WM_, WN_)
-#define IPC_IN(BM_, BN_, S_, WM_, WN_) IPC_CFG_CASE(WIDE_INFER, 1, ACT, BM_, BN_, S_, WM_, WN_)
-#define IPC_WT(BM_, BN_, S_, WM_, WN_) IPC_CFG_CASE(WIDE_WEIGHT, 1, ACT_IDENTITY, BM_, BN_, S_, WM_, WN_)
+#define IPC_CFG_CASE(MODE_, SPLIT_, ACT_, A32_, BM_, BN_, S_, WM_, WN_)                                   \
+  if (cfg == i++) return prep ? Cfg<OT, MODE_, SPLIT_, ACT_, false, BM_, BN_, S_, WM_, WN_, A32_>::prepare()  \
+                              : Cfg<OT, MODE_, SPLIT_, ACT_, false, BM_, BN_, S_, WM_, WN_, A32_>::launch(    \
+                                    probs, count, s);
+#define IPC_P1(BM_, BN_, S_, WM_, WN_) IPC_CFG_CASE(WIDE_PRED, 1, ACT_IDENTITY, false, BM_, BN_, S_, WM_, WN_)
+#define IPC_P2(BM_, BN_, S_, WM_, WN_) IPC_CFG_CASE(WIDE_PRED, 2, ACT_IDENTITY, false, BM_, BN_, S_, WM_, WN_)
+#define IPC_P2A(BM_, BN_, S_, WM_, WN_) IPC_CFG_CASE(WIDE_PRED, 2, ACT_IDENTITY, true, BM_, BN_, S_, WM_, WN_)
+#define IPC_IN(BM_, BN_, S_, WM_, WN_) IPC_CFG_CASE(WIDE_INFER, 1, ACT, false, BM_, BN_, S_, WM_, WN_)
+#define IPC_WT(BM_, BN_, S_, WM_, WN_) IPC_CFG_CASE(WIDE_WEIGHT, 1, ACT_IDENTITY, false, BM_, BN_, S_, WM_, WN_)
 
 template <typename OT>
 struct Phase {
   template <int ACT>
   struct Run {
-    // prep: raise the LDS limit of configuration `cfg` instead of launching it
+    // prep: raise the LDS limit of configuration `cfg` instead of launching it;
+    // a32: the split-2 prediction / forward read the fp32 W (problems' a) itself
     static hipError_t run(int mode, int split, int cfg, bool prep, const WideProblem* probs, int count,
-                          hipStream_t s) {
+                          hipStream_t s, bool a32) {
       int i = 0;
       switch (mode) {
         case WIDE_PRED:
-          if (split == 2) { WIDE_PRED2_CFGS(IPC_P2) }
+          if (split == 2 && a32) { WIDE_PRED2A_CFGS(IPC_P2A) }
+          else if (split == 2) { WIDE_PRED2_CFGS(IPC_P2) }
           else { WIDE_PRED1_CFGS(IPC_P1) }
           return hipErrorInvalidValue;
         case WIDE_INFER: { WIDE_INFER_CFGS(IPC_IN) } return hipErrorInvalidValue;
         case WIDE_WEIGHT: { WIDE_WEIGHT_CFGS(IPC_WT) } return hipErrorInvalidValue;
         default:  // WIDE_FWD
-          if (prep) return split == 2 ? FwdCfg2<OT, ACT>::prepare() : FwdCfg1<OT, ACT>::prepare();
-          return split == 2 ? FwdCfg2<OT, ACT>::launch(probs, count, s) : FwdCfg1<OT, ACT>::launch(probs, count, s);
+          if (split != 2) return prep ? FwdCfg1<OT, ACT>::prepare() : FwdCfg1<OT, ACT>::launch(probs, count, s);
+          if (a32) return prep ? FwdCfg2<OT, ACT, true>::prepare() : FwdCfg2<OT, ACT, true>::launch(probs, count, s);
+          return prep ? FwdCfg2<OT, ACT, false>::prepare() : FwdCfg2<OT, ACT, false>::launch(probs, count, s);
       }
     }
   };
@@ -72,16 +81,19 @@ struct Phase {
     hipError_t e;
     for (int act = 0; act < 6; ++act) {
       for (int c = 0; c < kInferCfgs; ++c)
-        if ((e = dma::by_act<Run>(act, WIDE_INFER, 1, c, true, nullptr, 0, nullptr)) != hipSuccess) return e;
+        if ((e = dma::by_act<Run>(act, WIDE_INFER, 1, c, true, nullptr, 0, nullptr, false)) != hipSuccess) return e;
       for (int sp = 1; sp <= 2; ++sp)
-        if ((e = dma::by_act<Run>(act, WIDE_FWD, sp, 0, true, nullptr, 0, nullptr)) != hipSuccess) return e;
+        for (int a32 = 0; a32 <= (sp == 2 ? 1 : 0); ++a32)
+          if ((e = dma::by_act<Run>(act, WIDE_FWD, sp, 0, true, nullptr, 0, nullptr, a32 != 0)) != hipSuccess)
+            return e;
     }
     for (int c = 0; c < kPred1Cfgs; ++c)
-      if ((e = Run<0>::run(WIDE_PRED, 1, c, true, nullptr, 0, nullptr)) != hipSuccess) return e;
+      if ((e = Run<0>::run(WIDE_PRED, 1, c, true, nullptr, 0, nullptr, false)) != hipSuccess) return e;
     for (int c = 0; c < kPred2Cfgs; ++c)
-      if ((e = Run<0>::run(WIDE_PRED, 2, c, true, nullptr, 0, nullptr)) != hipSuccess) return e;
+      for (int a32 = 0; a32 <= 1; ++a32)
+        if ((e = Run<0>::run(WIDE_PRED, 2, c, true, nullptr, 0, nullptr, a32 != 0)) != hipSuccess) return e;
     for (int c = 0; c < kWeightCfgs; ++c)
-      if ((e = Run<0>::run(WIDE_WEIGHT, 1, c, true, nullptr, 0, nullptr)) != hipSuccess) return e;
+      if ((e = Run<0>::run(WIDE_WEIGHT, 1, c, true, nullptr, 0, nullptr, false)) != hipSuccess) return e;
     return hipSuccess;
   }
 };
@@ -118,7 +130,7 @@ __global__ void __launch_bounds__(256) wide_copy_kernel(const WideCopyBatch cb) 
     if (r < c.rows && col < c.cols) {
       v = act_f(c.act, c.src[(long long)r * c.lds + col]);
       const OT hi = cvt<OT>(v);
-      dst[(long long)r * c.ldd + col] = hi;
+      if (dst) dst[(long long)r * c.ldd + col] = hi;
       if (lo) lo[(long long)r * c.ldl + col] = cvt<OT>(v - to_f32(hi));
       v = to_f32(hi);
     }
@@ -246,8 +258,9 @@ __global__ void __launch_bounds__(256) wide_reduce_kernel(const WideReduce r) {
 }
 
 template <typename OT>
-hipError_t launch_phase(int mode, const WideProblem* probs, int count, int split, int act, int cfg, hipStream_t s) {
-  return dma::by_act<Phase<OT>::template Run>(act, mode, split, cfg, false, probs, count, s);
+hipError_t launch_phase(int mode, const WideProblem* probs, int count, int split, int act, int cfg, hipStream_t s,
+                        bool a32) {
+  return dma::by_act<Phase<OT>::template Run>(act, mode, split, cfg, false, probs, count, s, a32);
 }
 
 }  // namespace
@@ -259,13 +272,14 @@ hipError_t wide_prepare() {
 }
 
 hipError_t launch_wide(int mode, const WideProblem* probs, int count, int operand, int split, int act,
-                       hipStream_t s, int cfg) {
+                       hipStream_t s, int cfg, bool a32) {
   if (cfg < 0 || cfg >= wide_config_count(mode, split)) return hipErrorInvalidValue;
+  if (a32 && (split != 2 || (mode != WIDE_PRED && mode != WIDE_FWD))) return hipErrorInvalidValue;
   for (int base = 0; base < count; base += WIDE_MAX_BATCH) {
     const int n = count - base < WIDE_MAX_BATCH ? count - base : WIDE_MAX_BATCH;
     hipError_t e;
-    if (operand == DT_F16) e = launch_phase<f16>(mode, probs + base, n, split, act, cfg, s);
-    else if (operand == DT_BF16) e = launch_phase<bf16>(mode, probs + base, n, split, act, cfg, s);
+    if (operand == DT_F16) e = launch_phase<f16>(mode, probs + base, n, split, act, cfg, s, a32);
+    else if (operand == DT_BF16) e = launch_phase<bf16>(mode, probs + base, n, split, act, cfg, s, a32);
     else return hipErrorInvalidValue;
     if (e != hipSuccess) return e;
   }

@@ -142,9 +142,12 @@ def _wide_layout_bytes(dims, B, split2):
     aligned 16-bit buffer per operand copy, rows and columns padded to 64:
     W hi [and lo] and its transpose (for l < L-1), f(x[l]) and its transpose
     for l = 1..L, eps[l] for l < L and its transpose for l < L-1, then the
-    partial products of a k-split prediction of layer 0."""
+    partial products of a k-split prediction of layer 0.  A split-2 net whose
+    every contraction d_{l+1} is a multiple of 64 keeps no W hi / lo copies:
+    its prediction reads the fp32 W itself."""
     pad = lambda v, m: (v + m - 1) // m * m  # noqa: E731
     L = len(dims) - 1
+    direct = split2 and all(d % 64 == 0 for d in dims[1:])
     total = 256
 
     def add(rows, cols):
@@ -152,9 +155,10 @@ def _wide_layout_bytes(dims, B, split2):
         total += pad(pad(rows, 64) * pad(cols, 64) * 2, 256)
 
     for l in range(L):
-        add(dims[l], dims[l + 1])
-        if split2:
+        if not direct:
             add(dims[l], dims[l + 1])
+            if split2:
+                add(dims[l], dims[l + 1])
         if l <= L - 2:
             add(dims[l + 1], dims[l])
     for l in range(1, L + 1):
@@ -190,6 +194,19 @@ def test_plan_path_selection_and_wide_workspace():
         assert lib.ipc_plan_bind(h, arr, arr, arr, None, None) == nat.ERR_NULL
         assert "workspace" in nat.last_error()
         assert lib.ipc_plan_bind(h, arr, arr, arr, None, P + 16) == nat.ERR_ALIGN
+        # every contraction is whole 64-k steps: the prediction reads W itself (16-byte rows)
+        wmis = (ctypes.c_void_p * 4)(P, P + 4, P, P)
+        assert lib.ipc_plan_bind(h, arr, arr, wmis, None, P) == nat.ERR_ALIGN
+        assert "W[1]" in nat.last_error()
+    finally:
+        lib.ipc_plan_destroy(h)
+    # a split-2 net with a contraction off the 64-k grid keeps the W hi / lo copies
+    ragged2 = (10, 300, 200, 784)
+    r2 = (ctypes.c_int * 4)(*ragged2)
+    assert lib.ipc_plan_create(ctypes.byref(h), 3, r2, 128, 0, 2, 2, 2, 1e-4, 0.5, 1, 0, 2) == nat.IPC_OK
+    try:
+        assert lib.ipc_plan_workspace_bytes(h) == _wide_layout_bytes(ragged2, 128, True)
+        assert _wide_layout_bytes(ragged2, 128, True) > _wide_layout_bytes(ragged2, 128, False)
     finally:
         lib.ipc_plan_destroy(h)
     # split 1 drops the W_lo copies; ragged sizes pad rows and columns to 64
