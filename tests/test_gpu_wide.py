@@ -38,6 +38,8 @@ CASES = [
     ((10, 784), 64, "sigmoid", F16, 2, True, "uniform"),           # L = 1: no inference phase
     ((7, 130, 65, 257), 37, "tanh", F16, 2, True, "uniform"),       # ragged: no tile/vector alignment
     ((10,) + (300,) * 17 + (784,), 64, "tanh", BF16, 2, True, "uniform"),  # 18 layers: chunked launches
+    # every contraction a multiple of 64: the split-2 prediction reads the fp32 W itself
+    ((10, 256, 192, 768), 128, "tanh", BF16, 2, True, "uniform"),
 ]
 
 
@@ -79,7 +81,7 @@ def test_wide_relu_gate():
     assert dw_err <= 5e-3 and frac <= 0.01
 
 
-@pytest.mark.parametrize("case", [CASES[0], CASES[2], CASES[5]], ids=_id)
+@pytest.mark.parametrize("case", [CASES[0], CASES[2], CASES[5], CASES[7]], ids=_id)
 def test_wide_equals_phased_path(case):
     """Same 16-bit operands, different fp32 summation order: states and weights
     agree to the fp32 bar, errors and weight deltas (small differences of
