@@ -33,7 +33,18 @@ using dma::Cfg;
 #define IPC_COUNT1(...) +1
 constexpr int kPred1Cfgs = 0 WIDE_PRED1_CFGS(IPC_COUNT1), kPred2Cfgs = 0 WIDE_PRED2_CFGS(IPC_COUNT1);
 constexpr int kInferCfgs = 0 WIDE_INFER_CFGS(IPC_COUNT1), kWeightCfgs = 0 WIDE_WEIGHT_CFGS(IPC_COUNT1);
-static_assert(0 WIDE_PRED2A_CFGS(IPC_COUNT1) == kPred2Cfgs, "one a32 configuration per split-2 prediction one");
+// the a32 list mirrors the split-2 one tile for tile (the plan sizes the
+// k-split and the workspace from wide_pred_tile, which reads the latter)
+#define IPC_TILE_CODE(BM_, BN_, S_, WM_, WN_) BM_ * 4096 + BN_,
+constexpr int kPred2Tiles[] = {WIDE_PRED2_CFGS(IPC_TILE_CODE)};
+constexpr int kPred2ATiles[] = {WIDE_PRED2A_CFGS(IPC_TILE_CODE)};
+constexpr bool same_tiles() {
+  for (int i = 0; i < kPred2Cfgs; ++i)
+    if (kPred2Tiles[i] != kPred2ATiles[i]) return false;
+  return true;
+}
+static_assert(sizeof(kPred2ATiles) == sizeof(kPred2Tiles) && same_tiles(),
+              "one a32 configuration, of the same tile, per split-2 prediction one");
 
 // forward initialisation: the split-1 prediction tiles; split 2 keeps 128 x 128
 // (one layer per launch: its tiles fill all CUs once per 4096-row layer, 82 us
