@@ -802,21 +802,31 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
     }
     __builtin_amdgcn_sched_barrier(0);  // one batch of loads per tile (register pressure)
   }
-  setup(k, p, peers, npeers_lds);
-  const int npeers = npeers_lds;
   // f(x[L]) of the chunk: x[L] is clamped, so its 16-bit operand copies (the
   // LDS region fh .. ea) are cached in the workspace by the first launch after
   // the forward initialisation (which marks the cache stale) and copied back
-  // into LDS by the launches after it.
+  // into LDS by the launches after it.  The flag that says whether the cache is
+  // valid and the image's first CB * NT 16-byte pieces are loaded with the
+  // states, before the set-up barrier, so that the three latencies overlap (a
+  // launch with a stale cache drops the pieces; the image region always exists).
   char* image = p.image + (long long)j * p.image_stride;
   uint4* lds_image = reinterpret_cast<uint4*>(k.lds + k.lay.fh);
   const int n16 = (k.lay.ea - k.lay.fh) * (int)sizeof(OT) / 16;
   const bool warm = *reinterpret_cast<const volatile unsigned*>(&p.flags[RES_MAX_WG]) == 1u;
+  constexpr int CB = 8;  // 16-byte loads in flight per thread
+  const gu32x4* isrc = (const gu32x4*)image;
+  u32x4 img[CB];
+#pragma unroll
+  for (int u = 0; u < CB; ++u) img[u] = isrc[min((int)threadIdx.x + u * NT, n16 - 1)];
+  setup(k, p, peers, npeers_lds);
+  const int npeers = npeers_lds;
   if (warm) {
-    constexpr int CB = 8;  // 16-byte loads in flight per thread
-    const gu32x4* src = (const gu32x4*)image;
+    const gu32x4* src = isrc;
     u32x4* dst = reinterpret_cast<u32x4*>(lds_image);
-    for (int base = threadIdx.x; base < n16; base += CB * NT) {
+#pragma unroll
+    for (int u = 0; u < CB; ++u)
+      if ((int)threadIdx.x + u * NT < n16) dst[threadIdx.x + u * NT] = img[u];
+    for (int base = threadIdx.x + CB * NT; base < n16; base += CB * NT) {
       u32x4 v[CB];
 #pragma unroll
       for (int u = 0; u < CB; ++u) v[u] = src[min(base + u * NT, n16 - 1)];
