@@ -536,8 +536,11 @@ __device__ __forceinline__ void setup(const Resident<OT, SPLIT, ACT>& k, const R
     for (int i = threadIdx.x; i < k.lay.bytes / 16; i += NT) z[i] = uint4{0u, 0u, 0u, 0u};
   }
   if (threadIdx.x == 0) {
-    // the workgroups this one exchanges with, in both directions
-    const int L = k.L, C = p.chunks, top0 = L - 1;
+    // the workgroups this one exchanges with, in both directions (from the
+    // kernel arguments: the LDS copy of the block is published by the barrier
+    // below)
+    const ResidentArgs& a = k.p;
+    const int L = k.L, C = a.chunks, top0 = L - 1;
     int n = 0;
     if (k.hidden) {
       if (k.l >= 1) peers[n++] = k.l - 1;
@@ -547,7 +550,7 @@ __device__ __forceinline__ void setup(const Resident<OT, SPLIT, ACT>& k, const R
         // next to the top layer: each row block's chunk-0 eps[L-1] flag (published
         // only after the block's other chunks have published, so it also covers
         // their progress)
-        for (int hh = 0; hh < p.halves; ++hh) peers[n++] = p.nwg + hh;
+        for (int hh = 0; hh < a.halves; ++hh) peers[n++] = a.nwg + hh;
       }
     } else {
       // the siblings in the row block, then workgroup L-2 (waited for one step behind)
@@ -610,9 +613,10 @@ template <typename OT, int SPLIT, int ACT>
 __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const ResidentArgs& p, int* peers,
                                            int& npeers_lds) {
   constexpr int MU = 1;  // update tiles per wave: d_l x d_{l+1} <= 64 x 64 is at most 16 tiles
-  const int L = k.L, B = k.B, C = p.chunks, l = k.l, wave = k.wave, lg = k.lg, lr = k.lr;
+  // (scalars from the kernel arguments: the LDS copy p is published by setup)
+  const int L = k.L, B = k.B, C = k.p.chunks, l = k.l, wave = k.wave, lg = k.lg, lr = k.lr;
   const int npr = k.n_pred, ninf = k.n_inf;
-  const float gamma = p.gamma, alpha = p.alpha;
+  const float gamma = k.p.gamma, alpha = k.p.alpha;
   // fb: f(x[l+1]) as staged for the MFMAs, reused for the next step's f'(x[l+1])
   f32x4 xa[MAXT], ea[MAXT], xb[MAXT], gb[MAXT], fb[MAXT], wr[MU];
   // (a tile index past the tile count maps to rows past the matrix, so the
@@ -622,8 +626,8 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
     const int t = wave + NWV * i;
     ea[i] = zero4(); gb[i] = zero4(); fb[i] = zero4();
     const int b = k.tcol(t);
-    const float* x0 = uniform(p.x[l]);
-    const float* x1 = uniform(p.x[l + 1]);
+    const float* x0 = uniform(k.p.x[l]);  // the kernel arguments (the LDS copy is not published yet)
+    const float* x1 = uniform(k.p.x[l + 1]);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int r = k.trow(t, q);
@@ -636,7 +640,7 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
   for (int i = 0; i < MU; ++i) {
     const int t = wave + NWV * i;
     const int c = k.uct(t) * 16 + lr;
-    const float* w = uniform(p.w[l]);
+    const float* w = uniform(k.p.w[l]);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int r = k.urt(t) * 16 + 4 * lg + q;
@@ -780,11 +784,12 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
 template <typename OT, int SPLIT, int ACT>
 __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const ResidentArgs& p, int* peers,
                                         int& npeers_lds) {
-  const int L = k.L, B = k.B, C = p.chunks, l = k.l, j = k.j, wave = k.wave, lg = k.lg, lr = k.lr;
+  // (scalars from the kernel arguments: the LDS copy p is published by setup)
+  const int L = k.L, B = k.B, C = k.p.chunks, l = k.l, j = k.j, wave = k.wave, lg = k.lg, lr = k.lr;
   // npr: this row block's prediction tiles; nrec: the layer's, the size of every
   // exchange record of the top layer (the block's tiles start at tile k.toff)
   const int npr = k.n_pred, nrec = k.npr_full, r0 = k.row0;
-  const float gamma = p.gamma, alpha = p.alpha;
+  const float gamma = k.p.gamma, alpha = k.p.alpha;
   f32x4 xa[MAXT], wr[MAXT];
 #pragma unroll
   for (int i = 0; i < MAXT; ++i) {
@@ -792,8 +797,8 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
     // (tile indices past the counts map to rows past the matrix: the range
     // checks alone cover them, and every load is issued without a branch)
     const int b = k.tcol(t), c = k.uct(t) * 16 + lr;
-    const float* x0 = uniform(p.x[l]);
-    const float* w = uniform(p.w[l]);
+    const float* x0 = uniform(k.p.x[l]);  // the kernel arguments (the LDS copy is not published yet)
+    const float* w = uniform(k.p.w[l]);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int r = k.trow(t, q), ru = k.urt(t) * 16 + 4 * lg + q;
@@ -809,10 +814,10 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
   // valid and the image's first CB * NT 16-byte pieces are loaded with the
   // states, before the set-up barrier, so that the three latencies overlap (a
   // launch with a stale cache drops the pieces; the image region always exists).
-  char* image = p.image + (long long)j * p.image_stride;
+  char* image = k.p.image + (long long)j * k.p.image_stride;
   uint4* lds_image = reinterpret_cast<uint4*>(k.lds + k.lay.fh);
   const int n16 = (k.lay.ea - k.lay.fh) * (int)sizeof(OT) / 16;
-  const bool warm = *reinterpret_cast<const volatile unsigned*>(&p.flags[RES_MAX_WG]) == 1u;
+  const bool warm = *reinterpret_cast<const volatile unsigned*>(&k.p.flags[RES_MAX_WG]) == 1u;
   constexpr int CB = 8;  // 16-byte loads in flight per thread
   const gu32x4* isrc = (const gu32x4*)image;
   u32x4 img[CB];
@@ -1039,10 +1044,12 @@ __global__ void __launch_bounds__(NT) resident_kernel(const ResidentArgs args) {
   static_assert(sizeof(ResidentArgs) % 4 == 0, "argument block copy");
   const int role = resident_role(blockIdx.x, args.L - 1, args.chunks, args.halves);
   if (role < 0) return;  // a spare block of the XCD-aware grid
+  // The copy is published by the set-up barrier of run_hidden / run_top; until
+  // then the role and the prologue's loads are addressed from the kernel
+  // arguments (k.p), so that those loads are in flight while it is made.
   for (int i = threadIdx.x; i < (int)(sizeof(ResidentArgs) / 4); i += NT)
     reinterpret_cast<int*>(&p)[i] = reinterpret_cast<const int*>(&args)[i];
-  __syncthreads();
-  R k(p, lds_raw, role);
+  R k(args, lds_raw, role);
   if (k.hidden) run_hidden(k, p, peers, npeers);
   else run_top(k, p, peers, npeers);
 
