@@ -193,6 +193,10 @@ struct Resident {
   // top workgroups: row block h (rows row0 .. row0 + M - 1 of W[L-1]); toff: the
   // block's first tile in the layer's exchange records of npr_full tiles
   int h, row0, toff, npr_full;
+  // the prologue's operands in memory (from the kernel arguments): x[l],
+  // x[l + 1] (hidden workgroups), W[l], and a top chunk's input image
+  const float *x_g, *xu_g, *w_g;
+  char* image_g;
   bool hidden;
   int nbt, n_pred, n_inf, n_upd, ktl, ks_k, ks_m, ks_b;
   float inv_nbt, inv_ktl, inv_B;
@@ -205,21 +209,32 @@ struct Resident {
     B = p.B;
     hidden = wg < L - 1;
     l = hidden ? wg : L - 1;
+    // the layer's argument scalars in one batch of loads with one wait (loaded
+    // where first used, they would cost a memory round trip each)
+    const int dm = p.dims[l], dk = p.dims[l + 1], din = p.dims[L], kc = p.kc, nch = p.chunks;
+    const long long istride = p.image_stride;
+    x_g = p.x[l];
+    xu_g = p.x[l + 1];
+    w_g = p.w[l];
+    image_g = p.image;
+    asm volatile("" ::"s"(dm), "s"(dk), "s"(din), "s"(kc), "s"(nch), "s"(istride), "s"(x_g), "s"(xu_g), "s"(w_g),
+                 "s"(image_g), "s"(p.flags), "s"(p.gamma), "s"(p.alpha), "s"(p.steps));
     const int top = hidden ? 0 : wg - (L - 1);
-    j = hidden ? 0 : top % p.chunks;
-    h = hidden ? 0 : top / p.chunks;
+    j = hidden ? 0 : top % nch;
+    image_g += (long long)j * istride;
+    h = hidden ? 0 : top / nch;
     row0 = h * RES_TOP_ROWS;
-    M = hidden ? p.dims[l] : min(RES_TOP_ROWS, p.dims[l] - row0);
-    k0 = hidden ? 0 : j * p.kc;
-    K = hidden ? p.dims[l + 1] : min(p.kc, p.dims[L] - k0);
-    ldw_g = p.dims[l + 1];
+    M = hidden ? dm : min(RES_TOP_ROWS, dm - row0);
+    k0 = hidden ? 0 : j * kc;
+    K = hidden ? dk : min(kc, din - k0);
+    ldw_g = dk;
     resident_lds_layout(M, K, B, hidden, S3, (int)sizeof(OT), lay);
     nbt = (B + 15) / 16;
     const int mtl = (M + 15) / 16;
     ktl = (K + 15) / 16;
     n_pred = mtl * nbt;
     toff = (row0 / 16) * nbt;
-    npr_full = ((p.dims[l] + 15) / 16) * nbt;
+    npr_full = ((dm + 15) / 16) * nbt;
     n_inf = hidden ? ktl * nbt : 0;
     n_upd = mtl * ktl;
     ks_k = (K + KSTEP - 1) / KSTEP;
@@ -524,23 +539,32 @@ __device__ __forceinline__ void wait_peers(const ResidentArgs& p, const int* pee
 }
 
 // Launch set-up, run while the workgroup's first state and weight loads are
-// in flight: the peer list, and zeros in the operand regions when the block
-// does not fill them (a dimension off the MFMA k-step or the 16-row tile
-// leaves padding that the MFMAs read); ends with a barrier, so the staging
-// writes that follow land after the zeros.
+// in flight: zeros in the operand regions when the block does not fill them (a
+// dimension off the MFMA k-step or the 16-row tile leaves padding that the
+// MFMAs read), then a barrier, so the staging writes that follow land after
+// the zeros.
 template <typename OT, int SPLIT, int ACT>
-__device__ __forceinline__ void setup(const Resident<OT, SPLIT, ACT>& k, const ResidentArgs& p, int* peers,
-                                      int& npeers) {
+__device__ __forceinline__ void setup(const Resident<OT, SPLIT, ACT>& k) {
   if ((k.M | k.K | k.B) & (Resident<OT, SPLIT, ACT>::KSTEP - 1)) {
     uint4* z = reinterpret_cast<uint4*>(k.lds);
     for (int i = threadIdx.x; i < k.lay.bytes / 16; i += NT) z[i] = uint4{0u, 0u, 0u, 0u};
+    __syncthreads();
   }
+}
+
+// The end of the prologue, once the staging writes are issued: the LDS copy
+// of the argument block (its words were loaded at entry and have arrived with
+// the prologue's own loads), the barrier that publishes the copy and the
+// staged operands, and then the list of workgroups this one exchanges with, in
+// both directions, from the copy (thread 0; only wave 0 reads it, in
+// wait_peers, after the next publish's barrier).
+template <typename OT, int SPLIT, int ACT>
+__device__ __forceinline__ void end_prologue(const Resident<OT, SPLIT, ACT>& k, ResidentArgs& p, int aword, int* peers,
+                                             int& npeers) {
+  if (threadIdx.x < sizeof(ResidentArgs) / 4) reinterpret_cast<int*>(&p)[threadIdx.x] = aword;
+  __syncthreads();
   if (threadIdx.x == 0) {
-    // the workgroups this one exchanges with, in both directions (from the
-    // kernel arguments: the LDS copy of the block is published by the barrier
-    // below)
-    const ResidentArgs& a = k.p;
-    const int L = k.L, C = a.chunks, top0 = L - 1;
+    const int L = k.L, C = p.chunks, top0 = L - 1;
     int n = 0;
     if (k.hidden) {
       if (k.l >= 1) peers[n++] = k.l - 1;
@@ -550,7 +574,7 @@ __device__ __forceinline__ void setup(const Resident<OT, SPLIT, ACT>& k, const R
         // next to the top layer: each row block's chunk-0 eps[L-1] flag (published
         // only after the block's other chunks have published, so it also covers
         // their progress)
-        for (int hh = 0; hh < a.halves; ++hh) peers[n++] = a.nwg + hh;
+        for (int hh = 0; hh < p.halves; ++hh) peers[n++] = p.nwg + hh;
       }
     } else {
       // the siblings in the row block, then workgroup L-2 (waited for one step behind)
@@ -560,7 +584,6 @@ __device__ __forceinline__ void setup(const Resident<OT, SPLIT, ACT>& k, const R
     }
     npeers = n;
   }
-  __syncthreads();
 }
 
 // The states a hidden workgroup leaves after the last step: eps[l]; x[l]
@@ -610,8 +633,8 @@ __device__ __forceinline__ void write_states(Resident<OT, SPLIT, ACT>& k, const 
 // Hidden layer l (0 <= l <= L-2): W[l] at the update tiles, x[l] at the
 // prediction tiles, x[l+1] at the inference tiles, all resident for the launch.
 template <typename OT, int SPLIT, int ACT>
-__device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const ResidentArgs& p, int* peers,
-                                           int& npeers_lds) {
+__device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, ResidentArgs& p, int* peers,
+                                           int& npeers_lds, int aword) {
   constexpr int MU = 1;  // update tiles per wave: d_l x d_{l+1} <= 64 x 64 is at most 16 tiles
   // (scalars from the kernel arguments: the LDS copy p is published by setup)
   const int L = k.L, B = k.B, C = k.p.chunks, l = k.l, wave = k.wave, lg = k.lg, lr = k.lr;
@@ -626,8 +649,8 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
     const int t = wave + NWV * i;
     ea[i] = zero4(); gb[i] = zero4(); fb[i] = zero4();
     const int b = k.tcol(t);
-    const float* x0 = uniform(k.p.x[l]);  // the kernel arguments (the LDS copy is not published yet)
-    const float* x1 = uniform(k.p.x[l + 1]);
+    const float* x0 = uniform(k.x_g);
+    const float* x1 = uniform(k.xu_g);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int r = k.trow(t, q);
@@ -640,15 +663,14 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
   for (int i = 0; i < MU; ++i) {
     const int t = wave + NWV * i;
     const int c = k.uct(t) * 16 + lr;
-    const float* w = uniform(k.p.w[l]);
+    const float* w = uniform(k.w_g);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int r = k.urt(t) * 16 + 4 * lg + q;
       wr[i][q] = ld_at(w, r * k.ldw_g + c, r < k.M && c < k.K);
     }
   }
-  setup(k, p, peers, npeers_lds);
-  const int npeers = npeers_lds;
+  setup(k);
 #pragma unroll
   for (int i = 0; i < MAXT; ++i) {
     const int t = wave + NWV * i;
@@ -659,7 +681,7 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
     const int t = wave + NWV * i;
     if (t < k.n_upd) k.stage_w4(k.urt(t) * 16 + 4 * lg, k.uct(t) * 16 + lr, wr[i]);
   }
-  __syncthreads();
+  end_prologue(k, p, aword, peers, npeers_lds);
 
   const bool from_top = l + 1 == L - 1;
   for (int s = 0; s < p.steps; ++s) {
@@ -702,7 +724,7 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
       da[i] = l >= 1 ? dact4<ACT>(xa[i]) : zero4();
       db[i] = dact4_from<ACT>(xb[i], fb[i]);
     }
-    wait_peers(p, peers, npeers, (unsigned)(s + 1));
+    wait_peers(p, peers, npeers_lds, (unsigned)(s + 1));
     // ---- 3. x[l] with g[l] from workgroup l-1; x[l+1] with eps[l+1] from above
     // (every exchange load of the phase is issued before the first use)
     f32x4 gl[MAXT], eu[MAXT];
@@ -782,8 +804,8 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, const Re
 // [k0, k0 + K) of W[L-1] at the update tiles, the same rows of x[L-1] at the
 // prediction tiles, f(x[L]) of the chunk in LDS.
 template <typename OT, int SPLIT, int ACT>
-__device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const ResidentArgs& p, int* peers,
-                                        int& npeers_lds) {
+__device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, ResidentArgs& p, int* peers,
+                                        int& npeers_lds, int aword) {
   // (scalars from the kernel arguments: the LDS copy p is published by setup)
   const int L = k.L, B = k.B, C = k.p.chunks, l = k.l, j = k.j, wave = k.wave, lg = k.lg, lr = k.lr;
   // npr: this row block's prediction tiles; nrec: the layer's, the size of every
@@ -797,8 +819,8 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
     // (tile indices past the counts map to rows past the matrix: the range
     // checks alone cover them, and every load is issued without a branch)
     const int b = k.tcol(t), c = k.uct(t) * 16 + lr;
-    const float* x0 = uniform(k.p.x[l]);  // the kernel arguments (the LDS copy is not published yet)
-    const float* w = uniform(k.p.w[l]);
+    const float* x0 = uniform(k.x_g);
+    const float* w = uniform(k.w_g);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int r = k.trow(t, q), ru = k.urt(t) * 16 + 4 * lg + q;
@@ -814,17 +836,16 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
   // valid and the image's first CB * NT 16-byte pieces are loaded with the
   // states, before the set-up barrier, so that the three latencies overlap (a
   // launch with a stale cache drops the pieces; the image region always exists).
-  char* image = k.p.image + (long long)j * k.p.image_stride;
+  char* image = k.image_g;
   uint4* lds_image = reinterpret_cast<uint4*>(k.lds + k.lay.fh);
   const int n16 = (k.lay.ea - k.lay.fh) * (int)sizeof(OT) / 16;
-  const bool warm = *reinterpret_cast<const volatile unsigned*>(&k.p.flags[RES_MAX_WG]) == 1u;
+  const bool warm = __hip_atomic_load(&k.p.flags[RES_MAX_WG], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 1u;
   constexpr int CB = 8;  // 16-byte loads in flight per thread
   const gu32x4* isrc = (const gu32x4*)image;
   u32x4 img[CB];
 #pragma unroll
   for (int u = 0; u < CB; ++u) img[u] = isrc[min((int)threadIdx.x + u * NT, n16 - 1)];
-  setup(k, p, peers, npeers_lds);
-  const int npeers = npeers_lds;
+  setup(k);
   if (warm) {
     const gu32x4* src = isrc;
     u32x4* dst = reinterpret_cast<u32x4*>(lds_image);
@@ -842,8 +863,8 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
   } else {
     // evaluate f(x[L]) of the chunk; row block 0 also writes it to fx[L] and to
     // the image (the chunk's row blocks share one)
-    const float* XL = p.x[L];
-    float* FL = k.h == 0 ? p.fx[L] : nullptr;
+    const float* XL = k.p.x[L];
+    float* FL = k.h == 0 ? k.p.fx[L] : nullptr;
     constexpr int SB = 8;  // loads in flight per thread
     const int n = k.K * B;
     for (int base = threadIdx.x; base < n; base += SB * NT) {
@@ -882,7 +903,7 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
       }
     }
   }
-  __syncthreads();
+  end_prologue(k, p, aword, peers, npeers_lds);
 
   // The chunks apply each step's x[L-1] update one step late, just before the
   // next step's eps[L-1]: their own chain (partial product, partial sums,
@@ -914,7 +935,7 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, const Resid
     f32x4 da[MAXT];
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) da[i] = dact4<ACT>(xa[i]);
-    wait_peers(p, peers, npeers, (unsigned)(s + 1), 1);
+    wait_peers(p, peers, npeers_lds, (unsigned)(s + 1), 1);
     f32x4 g[MAXT];
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) g[i] = zero4();
@@ -1041,17 +1062,23 @@ __global__ void __launch_bounds__(NT) resident_kernel(const ResidentArgs args) {
   __shared__ ResidentArgs p;
   __shared__ int peers[RES_MAX_WG];
   __shared__ int npeers;
-  static_assert(sizeof(ResidentArgs) % 4 == 0, "argument block copy");
-  const int role = resident_role(blockIdx.x, args.L - 1, args.chunks, args.halves);
+  static_assert(sizeof(ResidentArgs) % 4 == 0 && sizeof(ResidentArgs) / 4 <= NT, "argument block copy");
+  // Each thread's word of the copy is loaded first and stored at the end of
+  // the prologue (end_prologue), whose barrier publishes it; until then the
+  // role and the prologue's loads are addressed from the kernel arguments
+  // (k.p).
+  constexpr int NARG = sizeof(ResidentArgs) / 4;
+  const int aword = reinterpret_cast<const int*>(&args)[min((int)threadIdx.x, NARG - 1)];  // (no branch)
+  // The argument scalars the prologue needs arrive in two batches of loads
+  // with one wait each (loaded where first used, they cost a memory round
+  // trip each): those that place the block, then those of its layer.
+  const int L = args.L, B = args.B, chunks = args.chunks, halves = args.halves;
+  asm volatile("" ::"s"(L), "s"(B), "s"(chunks), "s"(halves));
+  const int role = resident_role(blockIdx.x, L - 1, chunks, halves);
   if (role < 0) return;  // a spare block of the XCD-aware grid
-  // The copy is published by the set-up barrier of run_hidden / run_top; until
-  // then the role and the prologue's loads are addressed from the kernel
-  // arguments (k.p), so that those loads are in flight while it is made.
-  for (int i = threadIdx.x; i < (int)(sizeof(ResidentArgs) / 4); i += NT)
-    reinterpret_cast<int*>(&p)[i] = reinterpret_cast<const int*>(&args)[i];
-  R k(args, lds_raw, role);
-  if (k.hidden) run_hidden(k, p, peers, npeers);
-  else run_top(k, p, peers, npeers);
+  R k(args, lds_raw, role);  // (loads the layer's scalars in the second batch)
+  if (k.hidden) run_hidden(k, p, peers, npeers, aword);
+  else run_top(k, p, peers, npeers, aword);
 
   // last workgroup out clears the flags and the exit counter for the next launch
   __syncthreads();
