@@ -88,10 +88,11 @@ template <> struct Op<float> {
 
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.0f, 0.0f, 0.0f, 0.0f}; }
 
-// floor(n / d) for 0 <= n < 2^22 and inv = 1.0f / d: (n + 0.5) / d is never
-// an integer and lies at least 0.5 / d from one, more than the product's
-// rounding error, so the float quotient truncates to the exact result (a few
-// instructions instead of an integer-division sequence).
+// floor(n / d) for 0 <= n < 2^21 and inv = 1 / d within one ulp (the
+// hardware reciprocal): (n + 0.5) / d is never an integer and lies at least
+// 0.5 / d from one, more than the error of inv and of the product, so the
+// float quotient truncates to the exact result (a few instructions instead of
+// an integer-division sequence).
 __device__ __forceinline__ int qdiv(int n, float inv) { return (int)(((float)n + 0.5f) * inv); }
 
 // Global-memory (address space 1) views.  The state and workspace pointers
@@ -122,6 +123,23 @@ __device__ __forceinline__ const float* uniform(const float* p) {
 // Out-of-range values never reach an output: every use of one (staging,
 // errors, stores) checks the range again.
 __device__ __forceinline__ float ld_at(const float* m, int idx, bool in) { return gbl(m)[in ? idx : 0]; }
+
+// A block of memory read through a buffer resource (word 3 0x00020000: the
+// gfx9 descriptor's 32-bit data format): loads at byte offsets past `bytes`
+// return 0 by the hardware's range check, so a load needs neither a range
+// test nor a clamped 64-bit address, only a 32-bit offset.  The prologue's
+// loads use it: its per-wave instruction count, four waves to a SIMD, sets
+// when the last wave's loads leave.  Values outside the matrix's rows and
+// columns are never used (every use checks the range again).
+struct BufRead {
+  __amdgpu_buffer_rsrc_t r;
+  __device__ __forceinline__ BufRead(const void* base, unsigned bytes)
+      : r(__builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000)) {}
+  __device__ __forceinline__ float f32(unsigned off) const {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+  }
+  __device__ __forceinline__ u32x4 u128(unsigned off) const { return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0); }
+};
 
 // An exchange record is one 16x16 result tile stored as every lane's four
 // result registers (16 bytes per lane), so each access is one 16-byte load or
@@ -194,8 +212,9 @@ struct Resident {
   // block's first tile in the layer's exchange records of npr_full tiles
   int h, row0, toff, npr_full;
   // the prologue's operands in memory (from the kernel arguments): x[l],
-  // x[l + 1] (hidden workgroups), W[l], and a top chunk's input image
-  const float *x_g, *xu_g, *w_g;
+  // x[l + 1] and f(x[l + 1]) (hidden workgroups), W[l], and a top chunk's
+  // input image
+  const float *x_g, *xu_g, *fu_g, *w_g;
   char* image_g;
   bool hidden;
   int nbt, n_pred, n_inf, n_upd, ktl, ks_k, ks_m, ks_b;
@@ -215,10 +234,11 @@ struct Resident {
     const long long istride = p.image_stride;
     x_g = p.x[l];
     xu_g = p.x[l + 1];
+    fu_g = p.fx[l + 1];
     w_g = p.w[l];
     image_g = p.image;
-    asm volatile("" ::"s"(dm), "s"(dk), "s"(din), "s"(kc), "s"(nch), "s"(istride), "s"(x_g), "s"(xu_g), "s"(w_g),
-                 "s"(image_g), "s"(p.flags), "s"(p.gamma), "s"(p.alpha), "s"(p.steps));
+    asm volatile("" ::"s"(dm), "s"(dk), "s"(din), "s"(kc), "s"(nch), "s"(istride), "s"(x_g), "s"(xu_g), "s"(fu_g),
+                 "s"(w_g), "s"(image_g), "s"(p.flags));
     const int top = hidden ? 0 : wg - (L - 1);
     j = hidden ? 0 : top % nch;
     image_g += (long long)j * istride;
@@ -240,9 +260,9 @@ struct Resident {
     ks_k = (K + KSTEP - 1) / KSTEP;
     ks_m = (M + KSTEP - 1) / KSTEP;
     ks_b = (B + KSTEP - 1) / KSTEP;
-    inv_nbt = 1.0f / (float)nbt;
-    inv_ktl = 1.0f / (float)ktl;
-    inv_B = 1.0f / (float)B;
+    inv_nbt = __builtin_amdgcn_rcpf((float)nbt);
+    inv_ktl = __builtin_amdgcn_rcpf((float)ktl);
+    inv_B = __builtin_amdgcn_rcpf((float)B);
   }
 
   // Re-derives the lane indices from an opaque copy of the thread id: every
@@ -278,10 +298,16 @@ struct Resident {
   // block, written with one 8-byte store each when all four exist.
   __device__ __forceinline__ f32x4 stage_f4(int r0, int b, f32x4 v) {
     f32x4 f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) f[q] = act_t<ACT>(v[q]);
+    return stage_fv4(r0, b, f);
+  }
+
+  // The same with f(v) given (its operand terms only).
+  __device__ __forceinline__ f32x4 stage_fv4(int r0, int b, f32x4 f) {
     OT hi[4], lo[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      f[q] = act_t<ACT>(v[q]);
       hi[q] = cvt<OT>(f[q]);
       if (S3) lo[q] = cvt<OT>(f[q] - to_f32(hi[q]));
     }
@@ -554,17 +580,21 @@ __device__ __forceinline__ void setup(const Resident<OT, SPLIT, ACT>& k) {
 
 // The end of the prologue, once the staging writes are issued: the LDS copy
 // of the argument block (its words were loaded at entry and have arrived with
-// the prologue's own loads), the barrier that publishes the copy and the
-// staged operands, and then the list of workgroups this one exchanges with, in
-// both directions, from the copy (thread 0; only wave 0 reads it, in
-// wait_peers, after the next publish's barrier).
+// the prologue's own loads) and the list of workgroups this one exchanges
+// with, in both directions (thread 0, while the other waves finish staging),
+// then the barrier that publishes them and the staged operands.
 template <typename OT, int SPLIT, int ACT>
 __device__ __forceinline__ void end_prologue(const Resident<OT, SPLIT, ACT>& k, ResidentArgs& p, int aword, int* peers,
                                              int& npeers) {
   if (threadIdx.x < sizeof(ResidentArgs) / 4) reinterpret_cast<int*>(&p)[threadIdx.x] = aword;
-  __syncthreads();
+  static_assert(offsetof(ResidentArgs, halves) / 4 < 64, "wave 0 holds the scalars of the peer list");
+  // wave 0's lanes hold the argument block's first 64 words (their share of
+  // the copy): the scalars come from there instead of a memory load
+  const int C = __builtin_amdgcn_readlane(aword, offsetof(ResidentArgs, chunks) / 4);
+  const int halves = __builtin_amdgcn_readlane(aword, offsetof(ResidentArgs, halves) / 4);
+  const int nwg = __builtin_amdgcn_readlane(aword, offsetof(ResidentArgs, nwg) / 4);
   if (threadIdx.x == 0) {
-    const int L = k.L, C = p.chunks, top0 = L - 1;
+    const int L = k.L, top0 = L - 1;
     int n = 0;
     if (k.hidden) {
       if (k.l >= 1) peers[n++] = k.l - 1;
@@ -574,7 +604,7 @@ __device__ __forceinline__ void end_prologue(const Resident<OT, SPLIT, ACT>& k, 
         // next to the top layer: each row block's chunk-0 eps[L-1] flag (published
         // only after the block's other chunks have published, so it also covers
         // their progress)
-        for (int hh = 0; hh < p.halves; ++hh) peers[n++] = p.nwg + hh;
+        for (int hh = 0; hh < halves; ++hh) peers[n++] = nwg + hh;
       }
     } else {
       // the siblings in the row block, then workgroup L-2 (waited for one step behind)
@@ -584,6 +614,7 @@ __device__ __forceinline__ void end_prologue(const Resident<OT, SPLIT, ACT>& k, 
     }
     npeers = n;
   }
+  __syncthreads();
 }
 
 // The states a hidden workgroup leaves after the last step: eps[l]; x[l]
@@ -642,39 +673,57 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, Resident
   const float gamma = k.p.gamma, alpha = k.p.alpha;
   // fb: f(x[l+1]) as staged for the MFMAs, reused for the next step's f'(x[l+1])
   f32x4 xa[MAXT], ea[MAXT], xb[MAXT], gb[MAXT], fb[MAXT], wr[MU];
-  // (a tile index past the tile count maps to rows past the matrix, so the
-  // range checks alone cover it; every load is issued without a branch)
+  // f(x[l+1]) as the previous launch left it in fx[l+1] (the same bits as
+  // evaluating it again) is valid when the input images are (a flag set by the
+  // last workgroup out of a launch, cleared by the forward initialisation and
+  // ipc_plan_sync); it is loaded with the states either way
+  const bool warm = __hip_atomic_load(&k.p.flags[RES_MAX_WG], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 1u;
+  f32x4 fu[MAXT];
+  // (a tile index past the tile count maps to rows past the matrix, which
+  // the buffers' range checks return as zeros; rows 4 lg + q and column lr of
+  // a tile: one 32-bit offset per lane, the tile's corner and q uniform)
+  {
+    const BufRead bx0(k.x_g, k.M * B * 4), bx1(k.xu_g, k.K * B * 4), bf1(k.fu_g, k.K * B * 4);
+    const unsigned lane_x = (unsigned)(4 * lg * B + lr) * 4u;
 #pragma unroll
-  for (int i = 0; i < MAXT; ++i) {
-    const int t = wave + NWV * i;
-    ea[i] = zero4(); gb[i] = zero4(); fb[i] = zero4();
-    const int b = k.tcol(t);
-    const float* x0 = uniform(k.x_g);
-    const float* x1 = uniform(k.xu_g);
+    for (int i = 0; i < MAXT; ++i) {
+      const int t = wave + NWV * i;
+      ea[i] = zero4(); gb[i] = zero4(); fb[i] = zero4();
+      const int rt = __builtin_amdgcn_readfirstlane(qdiv(t, k.inv_nbt)), ct = t - rt * k.nbt;
+      const unsigned corner = (unsigned)(rt * 16 * B + ct * 16) * 4u;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int r = k.trow(t, q);
-      xa[i][q] = ld_at(x0, r * B + b, r < k.M && b < B);
-      xb[i][q] = ld_at(x1, r * B + b, r < k.K && b < B);
+      for (int q = 0; q < 4; ++q) {
+        const unsigned off = lane_x + corner + (unsigned)(q * B) * 4u;
+        xa[i][q] = bx0.f32(off);
+        xb[i][q] = bx1.f32(off);
+        fu[i][q] = bf1.f32(off);
+      }
+      __builtin_amdgcn_sched_barrier(0);  // one batch of loads per tile (register pressure)
     }
-    __builtin_amdgcn_sched_barrier(0);  // one batch of loads per tile (register pressure)
-  }
+    const BufRead bw(k.w_g, k.M * k.ldw_g * 4);
+    const unsigned lane_w = (unsigned)(4 * lg * k.ldw_g + lr) * 4u;
 #pragma unroll
-  for (int i = 0; i < MU; ++i) {
-    const int t = wave + NWV * i;
-    const int c = k.uct(t) * 16 + lr;
-    const float* w = uniform(k.w_g);
+    for (int i = 0; i < MU; ++i) {
+      const int t = wave + NWV * i;
+      const int ut = __builtin_amdgcn_readfirstlane(k.urt(t)), uc = t - ut * k.ktl;
+      const unsigned corner = (unsigned)(ut * 16 * k.ldw_g + uc * 16) * 4u;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int r = k.urt(t) * 16 + 4 * lg + q;
-      wr[i][q] = ld_at(w, r * k.ldw_g + c, r < k.M && c < k.K);
+      for (int q = 0; q < 4; ++q) wr[i][q] = bw.f32(lane_w + corner + (unsigned)(q * k.ldw_g) * 4u);
     }
   }
   setup(k);
+  if (warm) {
 #pragma unroll
-  for (int i = 0; i < MAXT; ++i) {
-    const int t = wave + NWV * i;
-    if (t < ninf) fb[i] = k.stage_f4(k.trow(t, 0), k.tcol(t), xb[i]);
+    for (int i = 0; i < MAXT; ++i) {
+      const int t = wave + NWV * i;
+      if (t < ninf) fb[i] = k.stage_fv4(k.trow(t, 0), k.tcol(t), fu[i]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < MAXT; ++i) {
+      const int t = wave + NWV * i;
+      if (t < ninf) fb[i] = k.stage_f4(k.trow(t, 0), k.tcol(t), xb[i]);
+    }
   }
 #pragma unroll
   for (int i = 0; i < MU; ++i) {
@@ -682,6 +731,7 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, Resident
     if (t < k.n_upd) k.stage_w4(k.urt(t) * 16 + 4 * lg, k.uct(t) * 16 + lr, wr[i]);
   }
   end_prologue(k, p, aword, peers, npeers_lds);
+  const int npeers = npeers_lds;
 
   const bool from_top = l + 1 == L - 1;
   for (int s = 0; s < p.steps; ++s) {
@@ -724,7 +774,7 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, Resident
       da[i] = l >= 1 ? dact4<ACT>(xa[i]) : zero4();
       db[i] = dact4_from<ACT>(xb[i], fb[i]);
     }
-    wait_peers(p, peers, npeers_lds, (unsigned)(s + 1));
+    wait_peers(p, peers, npeers, (unsigned)(s + 1));
     // ---- 3. x[l] with g[l] from workgroup l-1; x[l+1] with eps[l+1] from above
     // (every exchange load of the phase is issued before the first use)
     f32x4 gl[MAXT], eu[MAXT];
@@ -813,21 +863,28 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, ResidentArg
   const int npr = k.n_pred, nrec = k.npr_full, r0 = k.row0;
   const float gamma = k.p.gamma, alpha = k.p.alpha;
   f32x4 xa[MAXT], wr[MAXT];
+  {
+    // the block's rows of x[L-1] and its rows and columns of W[L-1] through
+    // buffers that end with the block (tile indices past the counts map to
+    // rows past it: zeros; rows 4 lg + q and column lr of a tile: one 32-bit
+    // offset per lane, the tile's corner and q uniform)
+    const int ldw = k.ldw_g;
+    const BufRead bx(k.x_g + (long long)r0 * B, k.M * B * 4);
+    const BufRead bw(k.w_g + (long long)r0 * ldw + k.k0, ((k.M - 1) * ldw + k.K) * 4);
+    const unsigned lane_x = (unsigned)(4 * lg * B + lr) * 4u, lane_w = (unsigned)(4 * lg * ldw + lr) * 4u;
 #pragma unroll
-  for (int i = 0; i < MAXT; ++i) {
-    const int t = wave + NWV * i;
-    // (tile indices past the counts map to rows past the matrix: the range
-    // checks alone cover them, and every load is issued without a branch)
-    const int b = k.tcol(t), c = k.uct(t) * 16 + lr;
-    const float* x0 = uniform(k.x_g);
-    const float* w = uniform(k.w_g);
+    for (int i = 0; i < MAXT; ++i) {
+      const int t = wave + NWV * i;
+      const int rt = __builtin_amdgcn_readfirstlane(qdiv(t, k.inv_nbt)), ct = t - rt * k.nbt;
+      const int ut = __builtin_amdgcn_readfirstlane(k.urt(t)), uc = t - ut * k.ktl;
+      const unsigned cx = (unsigned)(rt * 16 * B + ct * 16) * 4u, cw = (unsigned)(ut * 16 * ldw + uc * 16) * 4u;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int r = k.trow(t, q), ru = k.urt(t) * 16 + 4 * lg + q;
-      xa[i][q] = ld_at(x0, (r0 + r) * B + b, r < k.M && b < B);
-      wr[i][q] = ld_at(w, (r0 + ru) * k.ldw_g + k.k0 + c, ru < k.M && c < k.K);
+      for (int q = 0; q < 4; ++q) {
+        xa[i][q] = bx.f32(lane_x + cx + (unsigned)(q * B) * 4u);
+        wr[i][q] = bw.f32(lane_w + cw + (unsigned)(q * ldw) * 4u);
+      }
+      __builtin_amdgcn_sched_barrier(0);  // one batch of loads per tile (register pressure)
     }
-    __builtin_amdgcn_sched_barrier(0);  // one batch of loads per tile (register pressure)
   }
   // f(x[L]) of the chunk: x[L] is clamped, so its 16-bit operand copies (the
   // LDS region fh .. ea) are cached in the workspace by the first launch after
@@ -843,8 +900,11 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, ResidentArg
   constexpr int CB = 8;  // 16-byte loads in flight per thread
   const gu32x4* isrc = (const gu32x4*)image;
   u32x4 img[CB];
+  {
+    const BufRead bi(image, n16 * 16);  // pieces past the image read as zeros (and are not stored)
 #pragma unroll
-  for (int u = 0; u < CB; ++u) img[u] = isrc[min((int)threadIdx.x + u * NT, n16 - 1)];
+    for (int u = 0; u < CB; ++u) img[u] = bi.u128((threadIdx.x + u * NT) * 16u);
+  }
   setup(k);
   if (warm) {
     const gu32x4* src = isrc;
@@ -904,6 +964,7 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, ResidentArg
     }
   }
   end_prologue(k, p, aword, peers, npeers_lds);
+  const int npeers = npeers_lds;
 
   // The chunks apply each step's x[L-1] update one step late, just before the
   // next step's eps[L-1]: their own chain (partial product, partial sums,
@@ -935,7 +996,7 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, ResidentArg
     f32x4 da[MAXT];
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) da[i] = dact4<ACT>(xa[i]);
-    wait_peers(p, peers, npeers_lds, (unsigned)(s + 1), 1);
+    wait_peers(p, peers, npeers, (unsigned)(s + 1), 1);
     f32x4 g[MAXT];
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) g[i] = zero4();
