@@ -563,8 +563,8 @@ int scratch_address(char** out) {
 // Zeroes the column kernel's barrier words and, when given, the resident
 // kernel's flag words (64 words each) before a launch on the scratch.
 __global__ void scratch_clear_kernel(unsigned* bar, unsigned* flags) {
-  bar[threadIdx.x] = 0u;
-  if (flags) flags[threadIdx.x] = 0u;
+  if (threadIdx.x < 64) bar[threadIdx.x] = 0u;
+  if (flags) flags[threadIdx.x] = 0u;  // the layer-resident flag area, RES_FLAG_BYTES / 4 words
 }
 
 // Workgroups of a whole-step kernel instantiation that the current device
@@ -1384,9 +1384,10 @@ int ipc_steps_noalloc(int L, const int* dims, int B, void* const* x, void* const
                       gamma, narrow_outer(B, weight_mode), kNarrowSpinLimit, cap, ws, res_off));
   hipStream_t s = (hipStream_t)stream;
   // the scratch keeps the previous call's contents: the barrier words and the
-  // resident flags (their word RES_MAX_WG marks the cached input images
-  // valid) must start at zero; everything else is written before it is read
-  hipLaunchKernelGGL(scratch_clear_kernel, dim3(1), dim3(64), 0, s, reinterpret_cast<unsigned*>(ws),
+  // resident flag area (step flags, cache generation and the workgroups'
+  // cache slots: zeros mark every cache stale) must start at zero; everything
+  // else is written before it is read
+  hipLaunchKernelGGL(scratch_clear_kernel, dim3(1), dim3(RES_FLAG_BYTES / 4), 0, s, reinterpret_cast<unsigned*>(ws),
                      res_bytes >= 0 ? reinterpret_cast<unsigned*>(ws + res_off) : nullptr);
   TRY(launch_rc(hipGetLastError(), "scratch clear"));
   if (res_bytes >= 0) {

@@ -33,7 +33,7 @@ struct NarrowArgs {
   float* a[NARROW_MAX_L + 1];  // saved activations (save mode) or nullptr
   float* fx[NARROW_MAX_L + 1]; // f(x[l]) as read by phase B: a[l] in save mode, else workspace
   unsigned* bar;               // workspace: [0] arrivals, [1] exits, [2] barrier timeout flag
-  unsigned* res_image_flag;    // layer-resident plans: cleared by FORWARD (x[L] changed), else nullptr
+  unsigned* res_image_flag;    // layer-resident plans: the cache generation FORWARD bumps (x[L] changed), else nullptr
 };
 
 // Workspace bytes of a plan: 256 bytes of barrier counters, then (recompute
@@ -96,7 +96,8 @@ __host__ __device__ inline void narrow_lds_layout(const int* dims, int L, int KS
 // blocks fit the LDS (B <= 64 at width 64).
 constexpr int RES_MAX_WIDTH = 64;   // d_0 .. d_{L-1}
 constexpr int RES_MAX_B = 128;
-constexpr int RES_MAX_WG = 63;      // word 63 of the flag area is the input-image flag
+constexpr int RES_MAX_WG = 63;      // word 63 of the flag area is the cache generation
+constexpr int RES_FLAG_BYTES = 512;  // flag area: step flags, generation, per-workgroup cache slots
 constexpr int RES_TILE = 256;       // floats per exchanged 16x16 tile (64 lanes x 4)
 constexpr int RES_TOP_ROWS = 32;    // rows of W[L-1] per top workgroup (a 64-row layer takes two)
 
@@ -116,10 +117,11 @@ struct ResidentArgs {
   float* xs;                    // eps[L-1] as summed by each row block's chunk 0: [2][tiles(d_{L-1})][RES_TILE]
   char* image;                  // per top chunk: its f(x[L]) operand LDS image, image_stride bytes apart
   long long image_stride;
-  unsigned* flags;              // [nwg] last step each workgroup has published, [nwg + h] the last step
-                                // whose eps[L-1] rows top chunk 0 of row block h has published;
-                                // [RES_MAX_WG] image valid
-  unsigned* bar;                // [1] exit counter, [2] wait timeout flag (shared with the column kernel)
+  unsigned* flags;              // [nwg] steps each workgroup has published (counted across launches),
+                                // [nwg + h] those whose eps[L-1] rows top chunk 0 of row block h has
+                                // published; [RES_MAX_WG] cache generation, [RES_MAX_WG + 1 + w]
+                                // generation + 1 once workgroup w's cached operands are current
+  unsigned* bar;                // [2] wait timeout flag (shared with the column kernel)
 };
 
 // LDS layout of one workgroup (element offsets, in operand elements of

@@ -542,8 +542,9 @@ __global__ void __launch_bounds__(NT) narrow_kernel(const NarrowArgs p) {
   const int ntile = p.wtile_start[p.L];
   const int nb = gridDim.x;
   if (p.mode == NMODE_FORWARD) {
-    // x[L] may have changed: a layer-resident plan's cached input images are stale
-    if (p.res_image_flag && blockIdx.x == 0 && threadIdx.x == 0) *p.res_image_flag = 0u;
+    // x[L] may have changed: a layer-resident plan's cached input images (and
+    // f(x) copies) are stale; a new generation makes every cache slot stale
+    if (p.res_image_flag && blockIdx.x == 0 && threadIdx.x == 0) *p.res_image_flag += 1u;
     for (int cb = blockIdx.x; cb < ncb; cb += nb) k.forward(cb);
     return;
   }

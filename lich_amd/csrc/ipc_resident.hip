@@ -541,7 +541,8 @@ __device__ __forceinline__ void publish(unsigned* flag, unsigned value) {
 // Waits until every peer's flag reaches `value`, the last `n_prev` peers'
 // flags `value - 1` (one lane of wave 0 per peer, relaxed polls, then one
 // acquire fence, which invalidates L2, pairing with the publishers' release
-// fences).
+// fences).  The flags count steps across launches, so they are compared as a
+// difference, which stays right when the count wraps around.
 __device__ __forceinline__ void wait_peers(const ResidentArgs& p, const int* peers, int npeers, unsigned value,
                                            int n_prev = 0) {
   if (threadIdx.x < 64) {
@@ -551,7 +552,7 @@ __device__ __forceinline__ void wait_peers(const ResidentArgs& p, const int* pee
     int spins = 0;
     while (true) {
       bool ok = true;
-      if (f) ok = __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= want;
+      if (f) ok = (int)(__hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - want) >= 0;
       if (__all(ok)) break;
       __builtin_amdgcn_s_sleep(1);
       if (++spins > p.spin_limit) {
@@ -562,6 +563,33 @@ __device__ __forceinline__ void wait_peers(const ResidentArgs& p, const int* pee
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
   __syncthreads();
+}
+
+// The flags area across launches.  Step flags are never cleared: every
+// workgroup publishes once per step, so at the start of a launch they all
+// hold the same count, the workgroup's own flag gives it, and the launch
+// publishes and waits for base + s + 1.  Word RES_MAX_WG is a generation,
+// bumped when cached operands go stale (the forward initialisation, which may
+// change x[L], and ipc_plan_sync); word RES_MAX_WG + 1 + wg holds generation
+// + 1 once workgroup wg's cached operands (a top chunk's input image, a hidden
+// workgroup's f(x[l+1]) in fx[l+1]) belong to the current generation.  Each
+// workgroup reads and writes only its own slot, at its start and end, so no
+// workgroup has to know that it is the last one out.
+struct Epoch {
+  unsigned base, gen;
+  bool warm;
+};
+__device__ __forceinline__ Epoch load_epoch(const ResidentArgs& a, int wg) {
+  Epoch e;
+  e.base = __hip_atomic_load(&a.flags[wg], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  e.gen = __hip_atomic_load(&a.flags[RES_MAX_WG], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  e.warm = __hip_atomic_load(&a.flags[RES_MAX_WG + 1 + wg], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == e.gen + 1u;
+  return e;
+}
+// At the end of a launch (read by the next one, after the kernel boundary).
+__device__ __forceinline__ void mark_cached(const ResidentArgs& a, int wg, const Epoch& e) {
+  if (threadIdx.x == 0 && a.steps > 0)
+    __hip_atomic_store(&a.flags[RES_MAX_WG + 1 + wg], e.gen + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Launch set-up, run while the workgroup's first state and weight loads are
@@ -673,11 +701,11 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, Resident
   const float gamma = k.p.gamma, alpha = k.p.alpha;
   // fb: f(x[l+1]) as staged for the MFMAs, reused for the next step's f'(x[l+1])
   f32x4 xa[MAXT], ea[MAXT], xb[MAXT], gb[MAXT], fb[MAXT], wr[MU];
-  // f(x[l+1]) as the previous launch left it in fx[l+1] (the same bits as
-  // evaluating it again) is valid when the input images are (a flag set by the
-  // last workgroup out of a launch, cleared by the forward initialisation and
-  // ipc_plan_sync); it is loaded with the states either way
-  const bool warm = __hip_atomic_load(&k.p.flags[RES_MAX_WG], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 1u;
+  // f(x[l+1]) as this workgroup left it in fx[l+1] at the end of the previous
+  // launch (the same bits as evaluating it again) is used when that belongs to
+  // the current generation; it is loaded with the states either way
+  const Epoch ep = load_epoch(k.p, k.wg);
+  const bool warm = ep.warm;
   f32x4 fu[MAXT];
   // (a tile index past the tile count maps to rows past the matrix, which
   // the buffers' range checks return as zeros; rows 4 lg + q and column lr of
@@ -767,14 +795,14 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, Resident
       if (t < ninf) st_rec(xg + k.rec(t), gb[i]);
     }
     // ---- 2. exchange; f'(x[l]) and f'(x[l+1]) of the old states meanwhile
-    publish(&p.flags[k.wg], (unsigned)(s + 1));
+    publish(&p.flags[k.wg], ep.base + (unsigned)(s + 1));
     f32x4 da[MAXT], db[MAXT];
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) {
       da[i] = l >= 1 ? dact4<ACT>(xa[i]) : zero4();
       db[i] = dact4_from<ACT>(xb[i], fb[i]);
     }
-    wait_peers(p, peers, npeers, (unsigned)(s + 1));
+    wait_peers(p, peers, npeers, ep.base + (unsigned)(s + 1));
     // ---- 3. x[l] with g[l] from workgroup l-1; x[l+1] with eps[l+1] from above
     // (every exchange load of the phase is issued before the first use)
     f32x4 gl[MAXT], eu[MAXT];
@@ -848,6 +876,7 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, Resident
       }
     }
   }
+  mark_cached(p, k.wg, ep);  // fx[l+1] was written in the last step
 }
 
 // Top-layer chunk j, row block h: rows [row0, row0 + M) and columns
@@ -896,7 +925,8 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, ResidentArg
   char* image = k.image_g;
   uint4* lds_image = reinterpret_cast<uint4*>(k.lds + k.lay.fh);
   const int n16 = (k.lay.ea - k.lay.fh) * (int)sizeof(OT) / 16;
-  const bool warm = __hip_atomic_load(&k.p.flags[RES_MAX_WG], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 1u;
+  const Epoch ep = load_epoch(k.p, k.wg);
+  const bool warm = ep.warm;
   constexpr int CB = 8;  // 16-byte loads in flight per thread
   const gu32x4* isrc = (const gu32x4*)image;
   u32x4 img[CB];
@@ -992,11 +1022,11 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, ResidentArg
     // ---- 2. exchange: the siblings' partials of this step, workgroup L-2's g
     // of the previous one; f'(x[L-1]) of the state the late update starts from
     // meanwhile
-    publish(&p.flags[k.wg], (unsigned)(s + 1));
+    publish(&p.flags[k.wg], ep.base + (unsigned)(s + 1));
     f32x4 da[MAXT];
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) da[i] = dact4<ACT>(xa[i]);
-    wait_peers(p, peers, npeers, (unsigned)(s + 1), 1);
+    wait_peers(p, peers, npeers, ep.base + (unsigned)(s + 1), 1);
     f32x4 g[MAXT];
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) g[i] = zero4();
@@ -1035,7 +1065,7 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, ResidentArg
         const int t = wave + NWV * i;
         if (t < npr) st_rec(xs + k.rec(k.toff + t), ev4[i]);
       }
-      publish(&p.flags[p.nwg + k.h], (unsigned)(s + 1));
+      publish(&p.flags[p.nwg + k.h], ep.base + (unsigned)(s + 1));
     }
     // eps[L-1] into the weight-update A operand (and e[L-1] after the last step)
 #pragma unroll
@@ -1089,6 +1119,7 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, ResidentArg
       }
     }
   }
+  mark_cached(p, k.wg, ep);  // the chunk's image was written by row block 0 this launch or before
 }
 
 // XCD-aware placement.  Blocks are dealt to the eight XCDs round-robin by
@@ -1140,23 +1171,6 @@ __global__ void __launch_bounds__(NT) resident_kernel(const ResidentArgs args) {
   R k(args, lds_raw, role);  // (loads the layer's scalars in the second batch)
   if (k.hidden) run_hidden(k, p, peers, npeers, aword);
   else run_top(k, p, peers, npeers, aword);
-
-  // last workgroup out clears the flags and the exit counter for the next launch
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    // relaxed: a workgroup counts itself out after its last flag poll has
-    // returned (its value decided the loop), so the clearing below cannot be
-    // seen by a poll; the results' visibility is the kernel boundary's
-    const unsigned prev = __hip_atomic_fetch_add(&p.bar[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (prev == (unsigned)p.nwg - 1) {
-      for (int w = 0; w < p.nwg + p.halves; ++w)
-        __hip_atomic_store(&p.flags[w], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      // the top chunks' input images are now written (read by the next launch,
-      // after this kernel has completed)
-      __hip_atomic_store(&p.flags[RES_MAX_WG], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(&p.bar[1], 0u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
 }
 
 // ---------------------------------------------------------------- dispatch
@@ -1244,7 +1258,7 @@ long long resident_plan(const int* dims, int L, int B, int split, int esize, boo
   a.nwg = (L - 1) + halves * C;
   a.lds_bytes = res_round(need, 16);
   for (int l = 0; l <= L; ++l) a.dims[l] = dims[l];
-  long long bytes = 256;  // flags
+  long long bytes = RES_FLAG_BYTES;  // flags
   for (int l = 0; l + 1 < L; ++l) {
     if (l >= 1) bytes += 2LL * resident_tiles(dims[l], B) * RES_TILE * 4;
     bytes += (l + 2 == L ? 3LL : 2LL) * resident_tiles(dims[l + 1], B) * RES_TILE * 4;
@@ -1258,7 +1272,7 @@ long long resident_plan(const int* dims, int L, int B, int split, int esize, boo
 void resident_bind(ResidentArgs& a, char* ws) {
   const int L = a.L, B = a.B;
   a.flags = reinterpret_cast<unsigned*>(ws);
-  char* at = ws + 256;
+  char* at = ws + RES_FLAG_BYTES;
   for (int l = 0; l < NARROW_MAX_L; ++l) { a.xe[l] = nullptr; a.xg[l] = nullptr; }
   for (int l = 0; l + 1 < L; ++l) {
     if (l >= 1) {
@@ -1275,7 +1289,7 @@ void resident_bind(ResidentArgs& a, char* ws) {
   a.image = ws + res_round((long long)(at - ws), 256);
 }
 
-__global__ void resident_invalidate_kernel(unsigned* flag) { *flag = 0u; }
+__global__ void resident_invalidate_kernel(unsigned* gen) { *gen += 1u; }
 
 hipError_t resident_invalidate(const ResidentArgs& a, hipStream_t s) {
   hipLaunchKernelGGL(resident_invalidate_kernel, dim3(1), dim3(1), 0, s, a.flags + RES_MAX_WG);

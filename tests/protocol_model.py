@@ -11,11 +11,13 @@ kernels' own schedules:
   between steps, and the exit counter whose last arrival clears both counters
   for the next launch;
 * layer-resident kernel (lich_amd/csrc/ipc_resident.hip, ``run_hidden`` /
-  ``run_top`` / ``publish`` / ``wait_peers`` / ``setup``): hidden workgroup l
-  writes eps[l] and W[l]^T eps[l] records (double-buffered, triple next to
-  the top layer), the top chunks write partial products and chunk 0 of each
-  row block the summed eps[L-1], every workgroup raises its step flag and
-  waits for its peers (the top chunks for workgroup L-2 one step behind).
+  ``run_top`` / ``publish`` / ``wait_peers`` / ``load_epoch``): hidden
+  workgroup l writes eps[l] and W[l]^T eps[l] records (double-buffered,
+  triple next to the top layer), the top chunks write partial products and
+  chunk 0 of each row block the summed eps[L-1], every workgroup raises its
+  step flag and waits for its peers (the top chunks for workgroup L-2 one
+  step behind); the flags count steps across launches and are never
+  cleared.
 
 A slot remembers the step whose value it holds; every read names the step it
 must see, so a read before its write (a missing wait) and an overwrite before
@@ -175,59 +177,76 @@ def _with_launch_order(progs, nblocks, ntile, launches):
 
 
 # --------------------------------------------------------------------------- layer-resident kernel
-def resident_kernel(hidden: int, chunks: int, halves: int, steps: int, *, g_buffers_top: int = 3,
+def resident_kernel(hidden: int, chunks: int, halves: int, steps: int, *, launches: int = 1, g_buffers_top: int = 3,
                     top_waits_l2: bool = True, chunk0_waits_siblings: bool = True,
-                    hidden_waits_up: bool = True) -> Model:
-    """One launch of the layer-resident kernel: hidden workgroups 0..hidden-1
-    (hidden = L - 1; workgroup hidden-1 sits next to the top layer) and the
-    top chunks (h, j), h < halves, j < chunks.  The keyword switches plant the
-    mistakes the tests expect the model to catch."""
+                    hidden_waits_up: bool = True, reset_base: bool = False) -> Model:
+    """``launches`` launches of the layer-resident kernel: hidden workgroups
+    0..hidden-1 (hidden = L - 1; workgroup hidden-1 sits next to the top
+    layer) and the top chunks (h, j), h < halves, j < chunks.  The flags are
+    never cleared: every workgroup publishes once per step, so a launch starts
+    with every flag at the steps of the launches before it (``load_epoch``
+    reads the workgroup's own flag as that base) and publishes and waits for
+    base + s + 1.  Slots remember the step counted across launches; the
+    exchange buffers are chosen by the step within the launch, as in the
+    kernel.  Launch n + 1 starts once every workgroup of launch n has finished
+    (stream order).  The keyword switches plant the mistakes the tests expect
+    the model to catch (``reset_base``: a launch that counts from zero again
+    while the flags hold the previous launch's steps)."""
     L2 = hidden - 1
     progs = {}
-    for l in range(hidden):
-        from_top = l == L2
-        prog = []
-        peers = []  # setup(): the workgroups it exchanges with
-        if l >= 1:
-            peers.append(("f", l - 1))
-        if not from_top:
-            if hidden_waits_up:
-                peers.append(("f", l + 1))
-        else:
-            peers += [("xsf", h) for h in range(halves)]
-        for s in range(steps):
-            buf = s % 2
+    names = [("hidden", l) for l in range(hidden)] + [("top", h, j) for h in range(halves) for j in range(chunks)]
+    for name in names:
+        progs[name] = []
+    for n in range(launches):
+        base = 0 if reset_base else n * steps
+        for l in range(hidden):
+            from_top = l == L2
+            prog = progs[("hidden", l)]
+            peers = []  # the workgroups it exchanges with
             if l >= 1:
-                prog.append(Op("write", ("xe", l, buf), s))
-            gslot = s % g_buffers_top if from_top else buf
-            prog.append(Op("write", ("xg", l, gslot), s))
-            prog.append(Op("publish", ("f", l), s + 1))
-            prog.append(Op("wait", conds=tuple((f, s + 1) for f in peers)))
-            if l >= 1:
-                prog.append(Op("read", ("xg", l - 1, buf), s))
-            if from_top:
-                prog += [Op("read", ("xs", h, buf), s) for h in range(halves)]
+                peers.append(("f", l - 1))
+            if not from_top:
+                if hidden_waits_up:
+                    peers.append(("f", l + 1))
             else:
-                prog.append(Op("read", ("xe", l + 1, buf), s))
-        progs[("hidden", l)] = prog
-    for h in range(halves):
-        for j in range(chunks):
-            prog = []
+                peers += [("xsf", h) for h in range(halves)]
             for s in range(steps):
-                buf = s % 2
-                prog.append(Op("write", ("xp", h, j, buf), s))
-                prog.append(Op("publish", ("f", ("top", h, j)), s + 1))
-                conds = [(("f", ("top", h, c)), s + 1) for c in range(chunks) if c != j]
-                if j == 0 and not chunk0_waits_siblings:
-                    conds = []
-                if top_waits_l2:
-                    conds.append((("f", L2), s))  # one step behind
-                prog.append(Op("wait", conds=tuple(conds)))
-                if s >= 1:
-                    prog.append(Op("read", ("xg", L2, (s - 1) % g_buffers_top), s - 1))
-                prog += [Op("read", ("xp", h, c, buf), s) for c in range(chunks)]
-                if j == 0:
-                    prog.append(Op("write", ("xs", h, buf), s))
-                    prog.append(Op("publish", ("xsf", h), s + 1))
-            progs[("top", h, j)] = prog
+                g, buf = n * steps + s, s % 2
+                if l >= 1:
+                    prog.append(Op("write", ("xe", l, buf), g))
+                gslot = s % g_buffers_top if from_top else buf
+                prog.append(Op("write", ("xg", l, gslot), g))
+                prog.append(Op("publish", ("f", l), base + s + 1))
+                prog.append(Op("wait", conds=tuple((f, base + s + 1) for f in peers)))
+                if l >= 1:
+                    prog.append(Op("read", ("xg", l - 1, buf), g))
+                if from_top:
+                    prog += [Op("read", ("xs", h, buf), g) for h in range(halves)]
+                else:
+                    prog.append(Op("read", ("xe", l + 1, buf), g))
+        for h in range(halves):
+            for j in range(chunks):
+                prog = progs[("top", h, j)]
+                for s in range(steps):
+                    g, buf = n * steps + s, s % 2
+                    prog.append(Op("write", ("xp", h, j, buf), g))
+                    prog.append(Op("publish", ("f", ("top", h, j)), base + s + 1))
+                    conds = [(("f", ("top", h, c)), base + s + 1) for c in range(chunks) if c != j]
+                    if j == 0 and not chunk0_waits_siblings:
+                        conds = []
+                    if top_waits_l2:
+                        conds.append((("f", L2), base + s))  # one step behind
+                    prog.append(Op("wait", conds=tuple(conds)))
+                    if s >= 1:
+                        prog.append(Op("read", ("xg", L2, (s - 1) % g_buffers_top), g - 1))
+                    prog += [Op("read", ("xp", h, c, buf), g) for c in range(chunks)]
+                    if j == 0:
+                        prog.append(Op("write", ("xs", h, buf), g))
+                        prog.append(Op("publish", ("xsf", h), base + s + 1))
+        if n + 1 < launches:
+            # stream order: every workgroup of launch n finishes before launch n + 1 starts
+            for name in names:
+                progs[name].append(Op("publish", ("done", name, n), 1))
+            for name in names:
+                progs[name].append(Op("wait", conds=tuple((("done", m, n), 1) for m in names)))
     return Model(progs)

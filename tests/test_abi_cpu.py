@@ -247,7 +247,8 @@ def test_plan_path_selection_and_wide_workspace():
 
 def _resident_ws_bytes(dims, B, recompute, esize=2):
     """Restated workspace of a layer-resident plan: the column kernel's
-    barrier words and f(x) buffers, then 256 bytes of step flags and the
+    barrier words and f(x) buffers, then 512 bytes of flags (step flags, the
+    cache generation, the workgroups' cache slots) and the
     double-buffered exchange of 16x16 tiles (1 KiB each): eps[l] for
     l = 1..L-2, W[l]^T eps[l] for l = 0..L-2 (three buffers for l = L-2, which
     the top chunks read one step late), and one partial product per
@@ -256,7 +257,7 @@ def _resident_ws_bytes(dims, B, recompute, esize=2):
     n = 256
     if recompute:
         n += sum((dims[l] * B * 4 + 255) // 256 * 256 for l in range(1, L + 1))
-    n = (n + 255) // 256 * 256 + 256
+    n = (n + 255) // 256 * 256 + 512
 
     def tiles(d):
         return -(-d // 16) * -(-B // 16)

@@ -1,9 +1,10 @@
 """Exhaustive interleaving checks of the whole-step kernels' synchronisation
 schedules (tests/protocol_model.py): every read of an exchange slot sees the
 step it must see, no schedule deadlocks, the column kernel's counters are
-clear for the next launch, and each planted mistake (a dropped wait, a
-counter left uncleared, one buffer too few next to the top layer, a missing
-peer) is caught."""
+clear for the next launch, the layer-resident kernel's step flags count on
+across launches, and each planted mistake (a dropped wait, a counter left
+uncleared, one buffer too few next to the top layer, a missing peer, a launch
+counting its steps from zero again) is caught."""
 import pytest
 
 from protocol_model import Violation, column_kernel, resident_kernel
@@ -29,6 +30,16 @@ def test_column_kernel_exit_must_clear_both_counters(clears):
     (1, 2, 1, 4), (2, 2, 1, 3), (3, 1, 1, 4), (2, 1, 2, 3), (1, 1, 2, 4), (1, 3, 1, 3), (2, 2, 2, 3)])
 def test_resident_kernel_exchange(hidden, chunks, halves, steps):
     assert resident_kernel(hidden, chunks, halves, steps).explore() > 1
+
+
+@pytest.mark.parametrize("hidden,chunks,halves,steps", [(1, 2, 1, 2), (2, 1, 1, 3), (2, 1, 2, 2), (1, 1, 2, 3)])
+def test_resident_kernel_flags_count_across_launches(hidden, chunks, halves, steps):
+    assert resident_kernel(hidden, chunks, halves, steps, launches=2).explore() > 1
+
+
+def test_resident_kernel_planted_mistake_counting_from_zero_again():
+    with pytest.raises(Violation):
+        resident_kernel(2, 1, 1, 2, launches=2, reset_base=True).explore()
 
 
 @pytest.mark.parametrize("mistake", [
