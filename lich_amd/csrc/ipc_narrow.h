@@ -33,7 +33,7 @@ struct NarrowArgs {
   float* a[NARROW_MAX_L + 1];  // saved activations (save mode) or nullptr
   float* fx[NARROW_MAX_L + 1]; // f(x[l]) as read by phase B: a[l] in save mode, else workspace
   unsigned* bar;               // workspace: [0] arrivals, [1] exits, [2] barrier timeout flag
-  unsigned* res_image_flag;    // layer-resident plans: the cache generation FORWARD bumps (x[L] changed), else nullptr
+  unsigned* res_image_flag;    // layer-resident plans: the cache generation every launch bumps, else nullptr
 };
 
 // Workspace bytes of a plan: 256 bytes of barrier counters, then (recompute
@@ -115,6 +115,8 @@ struct ResidentArgs {
   float* xg[NARROW_MAX_L];      // W[l]^T eps[l], l = 0..L-2: [2][tiles(d_{l+1})][RES_TILE]
   float* xp;                    // top-layer partial products: [2][chunks][tiles(d_{L-1})][RES_TILE]
   float* xs;                    // eps[L-1] as summed by each row block's chunk 0: [2][tiles(d_{L-1})][RES_TILE]
+  float* xn;                    // the top-layer partial products of the next launch's first step, computed
+                                // with the final W at the end of a launch: [chunks][tiles(d_{L-1})][RES_TILE]
   char* image;                  // per top chunk: its f(x[L]) operand LDS image, image_stride bytes apart
   long long image_stride;
   unsigned* flags;              // [nwg] steps each workgroup has published (counted across launches),

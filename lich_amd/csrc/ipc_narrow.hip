@@ -541,10 +541,12 @@ __global__ void __launch_bounds__(NT) narrow_kernel(const NarrowArgs p) {
   const int ncb = (p.B + NC - 1) / NC;
   const int ntile = p.wtile_start[p.L];
   const int nb = gridDim.x;
+  // a launch of this kernel on a layer-resident plan (the forward
+  // initialisation, which may change x[L], or a single phase, which changes x
+  // or W) makes that kernel's cached operands (input images, f(x) copies,
+  // first-step partial products) stale: a new generation marks them so
+  if (p.res_image_flag && blockIdx.x == 0 && threadIdx.x == 0) *p.res_image_flag += 1u;
   if (p.mode == NMODE_FORWARD) {
-    // x[L] may have changed: a layer-resident plan's cached input images (and
-    // f(x) copies) are stale; a new generation makes every cache slot stale
-    if (p.res_image_flag && blockIdx.x == 0 && threadIdx.x == 0) *p.res_image_flag += 1u;
     for (int cb = blockIdx.x; cb < ncb; cb += nb) k.forward(cb);
     return;
   }

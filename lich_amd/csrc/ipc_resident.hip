@@ -1000,6 +1000,15 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, ResidentArg
   // next step's eps[L-1]: their own chain (partial product, partial sums,
   // weight update) then waits for workgroup L-2's previous step only, and
   // workgroup L-2 writes x[L-1] after the last step.
+  //
+  // When the cached operands are current (warm), the previous launch has
+  // left the first step's partial products in xn, computed with the same W
+  // and f(x[L]) bits at its end: the first step skips its partial product
+  // and the exchange and sums them at once, so the first eps[L-1] reaches
+  // workgroup L-2 without waiting for the whole row block's first partial
+  // product (at the start of a launch the top chunks are not yet a step
+  // ahead of it).
+  float* xn = p.xn + (long long)j * nrec * RES_TILE;
   f32x4 ev_prev[MAXT];
 #pragma unroll
   for (int i = 0; i < MAXT; ++i) ev_prev[i] = zero4();
@@ -1008,9 +1017,10 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, ResidentArg
     const int lg = k.lg, lr = k.lr;
     const int buf = s & 1;
     const bool last = s + 1 == p.steps;
+    const bool pre = warm && s == 0;  // the partials are the previous launch's xn
     // ---- 1. partial product of the chunk
-    float* xp = p.xp + (long long)buf * C * nrec * RES_TILE;
-    {
+    float* xp = pre ? p.xn : p.xp + (long long)buf * C * nrec * RES_TILE;
+    if (!pre) {
       f32x4 cp[MAXT];
       k.pred_tiles(npr, cp);
 #pragma unroll
@@ -1021,12 +1031,13 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, ResidentArg
     }
     // ---- 2. exchange: the siblings' partials of this step, workgroup L-2's g
     // of the previous one; f'(x[L-1]) of the state the late update starts from
-    // meanwhile
-    publish(&p.flags[k.wg], ep.base + (unsigned)(s + 1));
+    // meanwhile (nothing to wait for in a first step from xn: its flag goes up
+    // once the step has read xn, below)
+    if (!pre) publish(&p.flags[k.wg], ep.base + (unsigned)(s + 1));
     f32x4 da[MAXT];
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) da[i] = dact4<ACT>(xa[i]);
-    wait_peers(p, peers, npeers, ep.base + (unsigned)(s + 1), 1);
+    if (!pre) wait_peers(p, peers, npeers, ep.base + (unsigned)(s + 1), 1);
     f32x4 g[MAXT];
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) g[i] = zero4();
@@ -1067,6 +1078,9 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, ResidentArg
       }
       publish(&p.flags[p.nwg + k.h], ep.base + (unsigned)(s + 1));
     }
+    // a first step from xn raises the step flag after its reads of xn (the
+    // launch's end rewrites xn once every sibling's flag is up)
+    if (pre) publish(&p.flags[k.wg], ep.base + 1u);
     // eps[L-1] into the weight-update A operand (and e[L-1] after the last step)
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) {
@@ -1119,7 +1133,20 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, ResidentArg
       }
     }
   }
-  mark_cached(p, k.wg, ep);  // the chunk's image was written by row block 0 this launch or before
+  // the next launch's first partial product, with the final W (staged by the
+  // last step) once every sibling has read this launch's xn (its first step's
+  // flag); the same instructions and operand bits as a step's partial product
+  if (p.steps > 0) {
+    wait_peers(p, peers, npeers, ep.base + 1u, 1);
+    f32x4 cp[MAXT];
+    k.pred_tiles(npr, cp);
+#pragma unroll
+    for (int i = 0; i < MAXT; ++i) {
+      const int t = wave + NWV * i;
+      if (t < npr) st_rec(xn + k.rec(k.toff + t), cp[i]);
+    }
+  }
+  mark_cached(p, k.wg, ep);  // the chunk's image (row block 0 wrote it this launch or before) and xn
 }
 
 // XCD-aware placement.  Blocks are dealt to the eight XCDs round-robin by
@@ -1263,7 +1290,7 @@ long long resident_plan(const int* dims, int L, int B, int split, int esize, boo
     if (l >= 1) bytes += 2LL * resident_tiles(dims[l], B) * RES_TILE * 4;
     bytes += (l + 2 == L ? 3LL : 2LL) * resident_tiles(dims[l + 1], B) * RES_TILE * 4;
   }
-  bytes += 2LL * (C + 1) * resident_tiles(dims[L - 1], B) * RES_TILE * 4;
+  bytes += (2LL * (C + 1) + C) * resident_tiles(dims[L - 1], B) * RES_TILE * 4;
   a.image_stride = res_round((o.ea - o.fh) * esize, 256);  // the fh .. ea region of the widest chunk
   bytes = res_round(bytes, 256) + C * a.image_stride;
   return bytes;
@@ -1286,6 +1313,8 @@ void resident_bind(ResidentArgs& a, char* ws) {
   at += 2LL * a.chunks * resident_tiles(a.dims[L - 1], B) * RES_TILE * 4;
   a.xs = reinterpret_cast<float*>(at);
   at += 2LL * resident_tiles(a.dims[L - 1], B) * RES_TILE * 4;
+  a.xn = reinterpret_cast<float*>(at);
+  at += (long long)a.chunks * resident_tiles(a.dims[L - 1], B) * RES_TILE * 4;
   a.image = ws + res_round((long long)(at - ws), 256);
 }
 

@@ -179,7 +179,7 @@ def _with_launch_order(progs, nblocks, ntile, launches):
 # --------------------------------------------------------------------------- layer-resident kernel
 def resident_kernel(hidden: int, chunks: int, halves: int, steps: int, *, launches: int = 1, g_buffers_top: int = 3,
                     top_waits_l2: bool = True, chunk0_waits_siblings: bool = True,
-                    hidden_waits_up: bool = True, reset_base: bool = False) -> Model:
+                    hidden_waits_up: bool = True, reset_base: bool = False, xn_wait: bool = True) -> Model:
     """``launches`` launches of the layer-resident kernel: hidden workgroups
     0..hidden-1 (hidden = L - 1; workgroup hidden-1 sits next to the top
     layer) and the top chunks (h, j), h < halves, j < chunks.  The flags are
@@ -189,9 +189,14 @@ def resident_kernel(hidden: int, chunks: int, halves: int, steps: int, *, launch
     base + s + 1.  Slots remember the step counted across launches; the
     exchange buffers are chosen by the step within the launch, as in the
     kernel.  Launch n + 1 starts once every workgroup of launch n has finished
-    (stream order).  The keyword switches plant the mistakes the tests expect
-    the model to catch (``reset_base``: a launch that counts from zero again
-    while the flags hold the previous launch's steps)."""
+    (stream order).  Every launch after the first starts warm: its top chunks
+    take their first step's partial products from xn, which each chunk writes
+    at the end of the launch before (after its siblings' first-step flags), so
+    their first step neither computes, publishes nor waits before summing.
+    The keyword switches plant the mistakes the tests expect the model to catch
+    (``reset_base``: a launch that counts from zero again while the flags hold
+    the previous launch's steps; ``xn_wait=False``: xn rewritten without
+    waiting for the siblings' first step)."""
     L2 = hidden - 1
     progs = {}
     names = [("hidden", l) for l in range(hidden)] + [("top", h, j) for h in range(halves) for j in range(chunks)]
@@ -229,20 +234,32 @@ def resident_kernel(hidden: int, chunks: int, halves: int, steps: int, *, launch
                 prog = progs[("top", h, j)]
                 for s in range(steps):
                     g, buf = n * steps + s, s % 2
-                    prog.append(Op("write", ("xp", h, j, buf), g))
-                    prog.append(Op("publish", ("f", ("top", h, j)), base + s + 1))
-                    conds = [(("f", ("top", h, c)), base + s + 1) for c in range(chunks) if c != j]
-                    if j == 0 and not chunk0_waits_siblings:
-                        conds = []
-                    if top_waits_l2:
-                        conds.append((("f", L2), base + s))  # one step behind
-                    prog.append(Op("wait", conds=tuple(conds)))
+                    pre = n >= 1 and s == 0
+                    if not pre:
+                        prog.append(Op("write", ("xp", h, j, buf), g))
+                        prog.append(Op("publish", ("f", ("top", h, j)), base + s + 1))
+                        conds = [(("f", ("top", h, c)), base + s + 1) for c in range(chunks) if c != j]
+                        if j == 0 and not chunk0_waits_siblings:
+                            conds = []
+                        if top_waits_l2:
+                            conds.append((("f", L2), base + s))  # one step behind
+                        prog.append(Op("wait", conds=tuple(conds)))
                     if s >= 1:
                         prog.append(Op("read", ("xg", L2, (s - 1) % g_buffers_top), g - 1))
-                    prog += [Op("read", ("xp", h, c, buf), g) for c in range(chunks)]
+                    if pre:
+                        prog += [Op("read", ("xn", h, c), n) for c in range(chunks)]
+                    else:
+                        prog += [Op("read", ("xp", h, c, buf), g) for c in range(chunks)]
                     if j == 0:
                         prog.append(Op("write", ("xs", h, buf), g))
                         prog.append(Op("publish", ("xsf", h), base + s + 1))
+                    if pre:
+                        prog.append(Op("publish", ("f", ("top", h, j)), base + 1))
+                # the next launch's first partials, after the siblings' first step
+                if xn_wait:
+                    prog.append(Op("wait", conds=tuple((("f", ("top", h, c)), base + 1)
+                                                       for c in range(chunks) if c != j)))
+                prog.append(Op("write", ("xn", h, j), n + 1))
         if n + 1 < launches:
             # stream order: every workgroup of launch n finishes before launch n + 1 starts
             for name in names:

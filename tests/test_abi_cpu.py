@@ -252,7 +252,8 @@ def _resident_ws_bytes(dims, B, recompute, esize=2):
     double-buffered exchange of 16x16 tiles (1 KiB each): eps[l] for
     l = 1..L-2, W[l]^T eps[l] for l = 0..L-2 (three buffers for l = L-2, which
     the top chunks read one step late), and one partial product per
-    128-column chunk of the top layer; then the chunks' input images."""
+    128-column chunk of the top layer (and one more for the next launch's
+    first step); then the chunks' input images."""
     L = len(dims) - 1
     n = 256
     if recompute:
@@ -267,7 +268,7 @@ def _resident_ws_bytes(dims, B, recompute, esize=2):
             n += 2 * tiles(dims[l]) * 1024
         n += (3 if l + 2 == L else 2) * tiles(dims[l + 1]) * 1024
     C = -(-dims[L] // 128)
-    n += 2 * (C + 1) * tiles(dims[L - 1]) * 1024   # the partials and chunk 0's summed eps[L-1]
+    n += (2 * (C + 1) + C) * tiles(dims[L - 1]) * 1024   # the partials, chunk 0's summed eps[L-1], the next ones
     # then, per top chunk, its cached f(x[L]) operands as laid out in LDS
     # (16-bit, split 3: hi and lo [B16][K32+8], hi [K16][B32+8]; fp32: [B16][K16+4]
     # and [K16][B16+4]), 256-byte aligned

@@ -4,7 +4,8 @@ step it must see, no schedule deadlocks, the column kernel's counters are
 clear for the next launch, the layer-resident kernel's step flags count on
 across launches, and each planted mistake (a dropped wait, a counter left
 uncleared, one buffer too few next to the top layer, a missing peer, a launch
-counting its steps from zero again) is caught."""
+counting its steps from zero again, first-step partials rewritten too early)
+is caught."""
 import pytest
 
 from protocol_model import Violation, column_kernel, resident_kernel
@@ -40,6 +41,17 @@ def test_resident_kernel_flags_count_across_launches(hidden, chunks, halves, ste
 def test_resident_kernel_planted_mistake_counting_from_zero_again():
     with pytest.raises(Violation):
         resident_kernel(2, 1, 1, 2, launches=2, reset_base=True).explore()
+
+
+def test_resident_kernel_planted_mistake_rewriting_the_first_partials_early():
+    # one step per launch: a chunk can finish before a sibling has summed xn
+    with pytest.raises(Violation):
+        resident_kernel(1, 2, 1, 1, launches=3, xn_wait=False).explore()
+
+
+@pytest.mark.parametrize("steps", [1, 2])
+def test_resident_kernel_first_partials_across_three_launches(steps):
+    assert resident_kernel(1, 2, 1, steps, launches=3).explore() > 1
 
 
 @pytest.mark.parametrize("mistake", [
