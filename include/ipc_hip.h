@@ -240,8 +240,10 @@ int ipc_plan_forward_init(ipc_plan* plan, void* stream);
 /* Wide path: re-derives the 16-bit operand copies from the fp32 masters x
  * and W.  Needed only after the caller wrote x[1..L] or W outside
  * ipc_plan_step / ipc_plan_forward_init.  Layer-resident plan: marks the
- * cached 16-bit copies of f(x[L]) stale (needed only after the caller wrote
- * x[L] without ipc_plan_forward_init).  A no-op for the other paths. */
+ * operands it caches between launches stale (the 16-bit copies of f(x[L]),
+ * the f(x) of the hidden states, the next launch's first partial products of
+ * the top layer): needed after the caller wrote x or W other than through
+ * this library's entry points.  A no-op for the other paths. */
 int ipc_plan_sync(ipc_plan* plan, void* stream);
 
 /* Enqueues only one phase of the step `reps` times (0 = prediction+error,

@@ -353,8 +353,10 @@ class HipIPC:
 
     def sync_operand_copies(self) -> None:
         """Declare writes of ``x`` or ``w`` made outside a step: re-derives the
-        wide path's 16-bit operand copies, marks the layer-resident path's
-        cached copies of f(x[L]) stale (no-op for the other paths)."""
+        wide path's 16-bit operand copies, marks the operands the
+        layer-resident path caches between launches stale (f(x[L]) copies,
+        f(x) of the hidden states, the top layer's next first-step partial
+        products); a no-op for the other paths."""
         if self._plan is not None:
             nat.check(nat.lib().ipc_plan_sync(self._plan, nat.current_stream_handle(self.device)))
 
