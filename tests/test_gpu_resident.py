@@ -229,6 +229,40 @@ def test_cached_input_images_follow_new_batches_and_direct_writes():
     assert res.barrier_timeouts() == 0
 
 
+def test_cached_operands_follow_single_phases_and_hidden_writes():
+    """A warm launch reuses the f(x[l+1]) the hidden workgroups wrote and the
+    top layer's first partial products the previous launch computed with its
+    final W.  Single phases run by the column kernel in between (they change
+    x and W) and a direct write of a hidden state declared with
+    sync_operand_copies must make them stale: the resident plan keeps matching
+    the column kernel bit for bit."""
+    from lich_amd import _native as nat
+    dims, B = (10,) + (64,) * 4 + (784,), 96
+    report("resident-cache-invalidation", dims=dims, B=B)
+    w0 = O.init_weights(dims, seed=14, init="xavier_uniform")
+    x_in, _l, y = O.make_batch(dims, B, seed=15)
+    x2 = torch.rand((dims[2], B), generator=torch.Generator().manual_seed(16)) - 0.5
+    ms = [_model(dims, w0, "tanh", F16, path) for path in ("resident", "narrow")]
+    for m in ms:
+        m.initialize_batch(x_in.to(DEV), y.to(DEV))
+        m.run_steps(4)
+        m.run_steps(3)                          # warm launch
+        stream = nat.current_stream_handle(DEV)
+        for phase in (0, 2):                    # prediction + inference, then the weight update
+            nat.check(nat.lib().ipc_plan_phase(m._plan, phase, 1, stream))
+        m.run_steps(4)
+        m.x[2].copy_(x2.to(DEV))                # direct write of a hidden state ...
+        m.sync_operand_copies()                 # ... declared to the plan
+        m.run_steps(2)
+        m.run_steps(1)
+    torch.cuda.synchronize()
+    res, col = ms
+    assert [res.path, col.path] == ["resident", "narrow"]
+    for a, b in zip(res.w + res.x + res.e[:-1], col.w + col.x + col.e[:-1]):
+        assert torch.equal(a, b)
+    assert res.barrier_timeouts() == 0
+
+
 # fp32 operands: the small-batch configuration and ragged nets, B <= 64
 SMALL = [
     ((10, 64, 64, 64, 784), 1),
