@@ -1078,9 +1078,11 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, ResidentArg
       }
       publish(&p.flags[p.nwg + k.h], ep.base + (unsigned)(s + 1));
     }
-    // a first step from xn raises the step flag after its reads of xn (the
-    // launch's end rewrites xn once every sibling's flag is up)
-    if (pre) publish(&p.flags[k.wg], ep.base + 1u);
+    // a first step from xn raises its step flag after its reads of xn (the
+    // launch's end rewrites xn once every sibling's flag has passed base + 1)
+    // only when it is the launch's last step: otherwise the second step's
+    // flag, base + 2, says as much, and nobody waits for base + 1
+    if (pre && last) publish(&p.flags[k.wg], ep.base + 1u);
     // eps[L-1] into the weight-update A operand (and e[L-1] after the last step)
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) {

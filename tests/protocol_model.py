@@ -191,8 +191,9 @@ def resident_kernel(hidden: int, chunks: int, halves: int, steps: int, *, launch
     kernel.  Launch n + 1 starts once every workgroup of launch n has finished
     (stream order).  Every launch after the first starts warm: its top chunks
     take their first step's partial products from xn, which each chunk writes
-    at the end of the launch before (after its siblings' first-step flags), so
-    their first step neither computes, publishes nor waits before summing.
+    at the end of the launch before (after its siblings' flags pass base + 1),
+    so their first step neither computes, publishes nor waits before summing
+    (it raises its flag afterwards only when it is the launch's only step).
     The keyword switches plant the mistakes the tests expect the model to catch
     (``reset_base``: a launch that counts from zero again while the flags hold
     the previous launch's steps; ``xn_wait=False``: xn rewritten without
@@ -253,7 +254,7 @@ def resident_kernel(hidden: int, chunks: int, halves: int, steps: int, *, launch
                     if j == 0:
                         prog.append(Op("write", ("xs", h, buf), g))
                         prog.append(Op("publish", ("xsf", h), base + s + 1))
-                    if pre:
+                    if pre and steps == 1:  # else the next step's flag covers it
                         prog.append(Op("publish", ("f", ("top", h, j)), base + 1))
                 # the next launch's first partials, after the siblings' first step
                 if xn_wait:
