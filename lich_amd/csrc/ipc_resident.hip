@@ -36,6 +36,10 @@
 // One flag exchange per step replaces the two grid barriers; W, the states
 // and the staged operands never leave the chip between steps.  The launch ends
 // by writing e, x, f(x) and W, as the column kernel's multi-step launch does.
+// The step flags count steps across launches and are never cleared; operands
+// that do not change between launches (the top chunks' f(x[L]) copies, the
+// hidden workgroups' f(x[l+1]), the top layer's next first-step partial
+// products) are kept in the workspace under a cache generation (load_epoch).
 //
 // Every wait is bounded by a spin limit that raises the timeout flag shared
 // with the column kernel instead of hanging.
