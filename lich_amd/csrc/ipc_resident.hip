@@ -14,7 +14,8 @@
 //   for its chunk (x[L] is clamped).
 //
 // A step, per workgroup:
-//   1. P = W f(x[l+1]) with split-3 16-bit MFMA (hi*hi + lo*hi + hi*lo);
+//   1. P = W f(x[l+1]) with 16-bit MFMA (one product with unsplit operands,
+//      three with split 3: hi*hi + lo*hi + hi*lo), or fp32 MFMA;
 //      eps[l] = x[l] - P; g = W[l]^T eps[l] (the inference term of layer l+1).
 //      Top chunks publish their partial P instead.
 //   2. publish eps[l] and g (16x16 result tiles, one 16-byte record per
