@@ -242,8 +242,7 @@ def sweep_point_bytes_flops(kind, M, K, B, save=False, s=2):
 def time_launch(fn, reps, replays=3, graph=True):
     """Microseconds per call of `fn` (its launches on the current stream), from
     HIP events around graph replays of `reps` back-to-back calls, or around
-    `reps * replays` direct calls (graph=False: the standalone 16-bit calls
-    evaluate f(X) once into a pooled buffer, which they skip under capture)."""
+    `reps * replays` direct calls (graph=False)."""
     import torch
 
     fn()
@@ -281,10 +280,11 @@ def kernel_sweep(sizes=(1024, 4096, 8192), batches=(256, 2048, 8192), acts=("tan
     storage and operands (fp32 accumulation), W ~ N(0, 1/K), states and errors
     ~ N(0, 1), tanh/relu fused; the inference update with and without the saved
     activation output, the weight update recomputing f(X) and reading a saved
-    A.  Each point's bound is min(MFMA peak, AI x HBM peak)."""
+    A.  Each point's bound is min(MFMA peak, AI x HBM peak).  Each call is timed
+    as the allocation-free default and, where a caller workspace lets it
+    evaluate f(X) once, with one (``*_workspace`` fields)."""
     import torch
 
-    from lich_amd import _native as nat
     from lich_amd import kernels as K_
 
     dev = torch.device("cuda", 0)
@@ -302,22 +302,34 @@ def kernel_sweep(sizes=(1024, 4096, 8192), batches=(256, 2048, 8192), acts=("tan
             aout = torch.empty((M, B), device=dev, dtype=bf)
             big = 2 * M * K * B > 2e11
             reps = 3 if big else (10 if 2 * M * K * B > 1e10 else 50)
+            ws_buf = None  # the caller workspace of the pre-activating calls, allocated once per shape
             for act in acts:
-                cases = [("pred", False, lambda: K_.build_prediction_error(M, K, B, act, bf)(xu, w, xl, e))]
+                kp = K_.build_prediction_error(M, K, B, act, bf)
+                cases = [("pred", False, kp)]
                 for save in (False, True):
-                    kern = K_.build_inference_update(M, K, B, act, bf, None, 0.5, save)
-                    wl = w  # W_lower is [K, M]; M == K here
-                    cases.append(("infer", save, (lambda kern=kern, save=save:
-                                                  kern(xl, e, wl, el, aout if save else None))))
+                    cases.append(("infer", save, K_.build_inference_update(M, K, B, act, bf, None, 0.5, save)))
                 for rec in (True, False):
-                    kern = K_.build_weight_update(M, K, B, act, bf, None, 1e-4, rec)
-                    cases.append(("weight", not rec, (lambda kern=kern: kern(w, e, xu))))
-                for kind, save, fn in cases:
-                    # calls that evaluate f(X) once (the library's rule) are timed
-                    # as direct calls: under graph capture they keep the loader path
-                    phase = {"pred": 0, "weight": 2}.get(kind, 1)
-                    direct = not save and bool(nat.lib().ipc_s16_preactivates(phase, nat.act_code(act), M, K, B))
-                    us = time_launch(fn, reps, graph=not direct)
+                    cases.append(("weight", not rec, K_.build_weight_update(M, K, B, act, bf, None, 1e-4, rec)))
+                wl = w  # W_lower is [K, M]; M == K here
+
+                def call(kind, save, kern, ws=None):
+                    if kind == "pred":
+                        return lambda: kern(xu, w, xl, e, workspace=ws)
+                    if kind == "infer":
+                        return lambda: kern(xl, e, wl, el, aout if save else None)
+                    return lambda: kern(w, e, xu, workspace=ws)
+
+                for kind, save, kern in cases:
+                    # the default call (no workspace: f(X) in every row tile's
+                    # loader; the library allocates nothing) and, where the call
+                    # would evaluate f(X) once given one, the caller-workspace call
+                    us = time_launch(call(kind, save, kern), reps)
+                    need = kern.workspace_bytes if kind != "infer" else 0
+                    us_ws = None
+                    if need > 0:
+                        if ws_buf is None or ws_buf.numel() < need:
+                            ws_buf = torch.empty((need,), dtype=torch.uint8, device=dev)
+                        us_ws = time_launch(call(kind, save, kern, ws_buf), reps)
                     nbytes, flops = sweep_point_bytes_flops(kind, M, K, B, save=save and kind == "infer")
                     ai = flops / nbytes
                     attain = min(BF16_PEAK_TFLOPS, ai * HBM_PEAK_GBS / 1e3)
@@ -328,10 +340,14 @@ def kernel_sweep(sizes=(1024, 4096, 8192), batches=(256, 2048, 8192), acts=("tan
                            "us": round(us, 2), "TFLOP/s": round(tf, 2), "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1),
                            "AI": round(ai, 1), "bound": "mfma" if attain >= BF16_PEAK_TFLOPS else "hbm",
                            "attainable_TFLOP/s": round(attain, 1), "frac": round(tf / attain, 4),
-                           "timing": "direct calls, f(X) evaluated once" if direct else "graph replays"}
+                           "timing": "graph replays, no workspace"}
+                    if us_ws is not None:
+                        tfw = flops / (us_ws * 1e-6) / 1e12
+                        row.update({"us_workspace": round(us_ws, 2), "TFLOP/s_workspace": round(tfw, 2),
+                                    "frac_workspace": round(tfw / attain, 4)})
                     rows.append(row)
                     log(f"sweep: {row}")
-            del w, xu, xl, e, el, aout
+            del w, xu, xl, e, el, aout, ws_buf
             torch.cuda.empty_cache()
     return rows
 

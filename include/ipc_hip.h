@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define IPC_ABI_VERSION 5
+#define IPC_ABI_VERSION 6
 
 /* status codes */
 #define IPC_OK 0
@@ -208,17 +208,24 @@ int ipc_plan_fused(const ipc_plan* plan);
 int ipc_plan_path(const ipc_plan* plan);
 
 /* Bytes of zero-initialised device workspace ipc_plan_bind needs (0 for the
- * phased path).  The first 256 bytes hold the whole-step kernel's
- * grid-barrier counters, which it leaves zero after every launch (word 2
- * becomes non-zero if a barrier wait ever ran past its spin limit); in
- * recompute mode the whole-step kernel keeps the f(x[l]) values phase A
- * evaluates for the weight update after them, and a layer-resident plan its
- * per-workgroup step flags (also left zero after every launch), the
- * double-buffered eps / W^T eps exchange and the top chunks' cached 16-bit
- * copies of f(x[L]) after those.  The wide path keeps its
- * 16-bit operand copies there (W as hi and lo terms, W^T, f(x) and eps in
- * both layouts, zero padded; their padding must stay zero), then the fp32
- * partial products of a k-split output-layer prediction. */
+ * phased path).  The first 256 bytes hold the column-block whole-step
+ * kernel's grid-barrier counters, which it leaves zero after every launch
+ * (word 2 becomes non-zero if a wait ever ran past its spin limit); in
+ * recompute mode that kernel keeps the f(x[l]) values phase A evaluates for
+ * the weight update after them.  A layer-resident plan then keeps, after
+ * those: its per-workgroup step flags, which count steps across launches
+ * (they are never cleared), the cache generation and one cache slot per
+ * workgroup; the double-buffered eps / W^T eps exchange; and caches tied to
+ * the bound buffers (the top chunks' 16-bit images of f(x[L]), the hidden
+ * f(x) values and the next launch's first-step partial products), which a
+ * launch reuses while their generation is current.  ipc_plan_bind and
+ * ipc_plan_sync make them stale, so a rebound plan starts cold.  A workspace
+ * belongs to one bound plan at a time: binding another plan to it hands it
+ * over, and the first plan must be bound again before it runs again.  The
+ * wide path keeps its 16-bit operand copies there (W as hi and lo terms,
+ * W^T, f(x) and eps in both layouts, zero padded; their padding must stay
+ * zero), then the fp32 partial products of a k-split output-layer
+ * prediction. */
 long long ipc_plan_workspace_bytes(const ipc_plan* plan);
 
 /* Binds the caller's buffers: x and e hold L+1 pointers ([d_l, B] each; e[L]
@@ -344,34 +351,84 @@ int ipc_plan_graph_steps(const ipc_plan* plan);
  * initialisation.  Each call clears the scratch words that must start at
  * zero; calls that overlap on one GPU (other streams or threads) race on the
  * scratch and must be serialised.  A wait that gives up (see ipc_plan_check)
- * marks only the scratch, which the next call clears: callers that need that
- * report use a plan.  Calls no hipMalloc, hipFree or other allocating
- * routine.
+ * sets the scratch's timeout word, which later calls leave set until
+ * ipc_noalloc_check reads it.  Calls no hipMalloc, hipFree or other
+ * allocating routine.
  */
 int ipc_steps_noalloc(int L, const int* dims, int B, void* const* x, void* const* e, void* const* w,
                       int operand, int split, int act, float alpha, float gamma, int weight_mode, int steps,
                       void* stream);
+
+/* Test hook: the host-side check that every LDS-DMA GEMM launch (wide path
+ * and standalone 16-bit calls) makes of each of its problems before any HIP
+ * call, for one problem of `phase` (IPC_PHASE_PRED, _INFER, _WEIGHT or
+ * IPC_PHASE_FORWARD), prediction split `split`, fp32_w != 0 when the kernel
+ * splits the fp32 W into its hi and lo operands itself, has_lo != 0 when a
+ * 16-bit lo operand is passed, contraction K and k-slices `ksplit`.
+ * IPC_ERR_CONFIG when a launch would refuse it: a split-2 kernel without
+ * its lo operand (it would read through a null pointer), or a k-split that
+ * does not cut K into whole 64-k steps.  No counterpart in the reference. */
+#define IPC_PHASE_FORWARD 3
+int ipc_wide_problem_check(int phase, int split, int fp32_w, int has_lo, int K, int ksplit);
+
+/* No counterpart in the reference; the health check of ipc_steps_noalloc
+ * for callers that cannot allocate.  Synchronises `stream`, then returns
+ * IPC_ERR_TIMEOUT (and clears the word) if a wait of any ipc_steps_noalloc
+ * call on the current device gave up since the last check: those calls'
+ * outputs are invalid.  IPC_OK otherwise.  Allocates nothing. */
+int ipc_noalloc_check(void* stream);
+
+/* Test hook: >= 0 sets the polls per wait of ipc_steps_noalloc's kernels
+ * (0 gives up at the first unsatisfied poll, so a host test can force the
+ * timeout path while every kernel still exits normally); < 0 restores the
+ * default.  Not thread-safe. */
+int ipc_noalloc_set_spin_limit(int limit);
 
 /* Test hook: > 0 replaces the device's co-resident workgroup capacity in the
  * checks of ipc_plan_create (a compute-partitioned device can be modelled
  * without one); 0 restores the device query.  Not thread-safe. */
 int ipc_set_coresident_limit(int blocks);
 
-/* Tuning hook of the standalone 16-bit-storage calls (ipc_pred_err,
- * ipc_forward, ipc_weight_update with recompute) on the LDS-DMA kernel: their
- * B operand f(X_upper) is either activated in the loader of every row tile
- * (0) or evaluated once by an elementwise pass into a buffer from a
- * library-owned stream-ordered pool and then read like the other operands
- * (1); -1 (the default) pre-activates by the rule of ipc_s16_preactivates
- * when the stream is not being captured.  Both give the same bits.  No counterpart in the reference
- * (TileLang fuses the activation into its loader).  Not thread-safe. */
+/*
+ * Caller workspace of the standalone 16-bit-storage calls on the LDS-DMA
+ * kernel (ipc_pred_err, ipc_forward, ipc_weight_update with recompute).
+ * Their B operand f(X_upper) is activated in the loader of every row tile,
+ * which for the exponential activations costs more VALU work than the tile's
+ * MFMAs once there are many row tiles.  The _ws variants take a device
+ * workspace (16-byte aligned, owned by the caller, `workspace_bytes` long):
+ * when it holds ipc_s16_workspace_bytes(...) bytes (> 0) the call activates
+ * f(X_upper) once into it, in its own launch on `stream`, and the GEMM then
+ * reads it like its other operands; otherwise (NULL or too small) the
+ * loader path runs.  Same bits either way.  Calls that share a workspace must
+ * be ordered on one stream.  The variants without _ws are the _ws calls with
+ * no workspace.  No counterpart in the reference (TileLang fuses the
+ * activation into its loader and has no workspace); the library allocates
+ * nothing on either path.
+ *
+ * ipc_s16_workspace_bytes gives the bytes a call of `kind` (IPC_PHASE_PRED
+ * for ipc_pred_err_ws / ipc_forward_ws, IPC_PHASE_WEIGHT for a recomputing
+ * ipc_weight_update_ws) with M rows, contraction K, batch B and `groups`
+ * groups uses: groups * K * B * 2 when it pre-activates under the current
+ * mode, else 0.  The automatic rule: exp-based activations from M >= 1024 and
+ * K * B >= 2^20, relu from M >= 4096 and K * B >= 2^22, never identity or the
+ * inference update.  ipc_s16_preactivates(kind, act, M, K, B) reports the
+ * same decision (1 / 0).  ipc_set_s16_preactivate, a tuning hook, sets the
+ * mode: -1 (default) the rule, 0 never, 1 whenever a workspace is given.
+ * Not thread-safe.
+ */
+int ipc_pred_err_ws(const void* x_upper, const void* w, const void* x_lower, void* e,
+                    int M, int K, int B, int groups,
+                    int storage, int operand, int split, int act, int tile,
+                    void* workspace, long long workspace_bytes, void* stream);
+int ipc_forward_ws(const void* x_upper, const void* w, void* out,
+                   int M, int K, int B, int groups,
+                   int storage, int operand, int split, int act, int tile,
+                   void* workspace, long long workspace_bytes, void* stream);
+int ipc_weight_update_ws(void* w, const void* e, const void* x_upper, int M, int K, int B, int groups,
+                         float alpha, int recompute, int storage, int operand, int act, int tile,
+                         void* workspace, long long workspace_bytes, void* stream);
+long long ipc_s16_workspace_bytes(int kind, int act, int M, int K, int B, int groups);
 int ipc_set_s16_preactivate(int mode);
-
-/* Whether such a call of M rows, contraction K and batch B pre-activates under
- * the current mode (kind: IPC_PHASE_PRED for ipc_pred_err / ipc_forward,
- * IPC_PHASE_WEIGHT for a recomputing ipc_weight_update; 0 for any other), not
- * counting graph capture.  The automatic rule: exp-based activations from
- * M >= 1024 and K * B >= 2^20, relu from M >= 4096 and K * B >= 2^22. */
 int ipc_s16_preactivates(int kind, int act, int M, int K, int B);
 
 void ipc_plan_destroy(ipc_plan* plan);

@@ -76,6 +76,10 @@ def _declare(lib):
         "ipc_infer_update": ([vp, vp, vp, vp, vp, i, i, i, i, f, i, i, i, i, vp], i),
         "ipc_weight_update": ([vp, vp, vp, i, i, i, i, f, i, i, i, i, i, vp], i),
         "ipc_weight_update_outer": ([vp, vp, vp, i, i, i, i, f, i, i, i, vp], i),
+        "ipc_pred_err_ws": ([vp, vp, vp, vp, i, i, i, i, i, i, i, i, i, vp, c_longlong, vp], i),
+        "ipc_forward_ws": ([vp, vp, vp, i, i, i, i, i, i, i, i, i, vp, c_longlong, vp], i),
+        "ipc_weight_update_ws": ([vp, vp, vp, i, i, i, i, f, i, i, i, i, i, vp, c_longlong, vp], i),
+        "ipc_s16_workspace_bytes": ([i, i, i, i, i, i], c_longlong),
         "ipc_plan_create": ([POINTER(vp), i, POINTER(c_int), i, i, i, i, i, f, f, i, i, i], i),
         "ipc_plan_fused": ([vp], i),
         "ipc_plan_path": ([vp], i),
@@ -94,6 +98,9 @@ def _declare(lib):
         "ipc_set_coresident_limit": ([i], i),
         "ipc_set_s16_preactivate": ([i], i),
         "ipc_s16_preactivates": ([i, i, i, i, i], i),
+        "ipc_wide_problem_check": ([i, i, i, i, i, i], i),
+        "ipc_noalloc_check": ([vp], i),
+        "ipc_noalloc_set_spin_limit": ([i], i),
         "ipc_plan_graph_capture": ([vp, i], i),
         "ipc_plan_graph_launch": ([vp, i, vp], i),
         "ipc_plan_graph_steps": ([vp], i),

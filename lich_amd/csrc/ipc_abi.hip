@@ -234,31 +234,6 @@ std::vector<WideProblem> s16_groups(const WideProblem& q, int groups, long long 
 // -1 automatic, 0 never, 1 always.
 int g_s16_preact = -1;
 
-// The library's stream-ordered pool of one device for the pre-activated
-// operands: a call allocates its buffer on its own stream and frees it there,
-// so calls on different streams never share one, and freed blocks stay in the
-// pool for the next call (release threshold: unlimited).
-hipMemPool_t s16_pool(int dev) {
-  static std::mutex mu;
-  static hipMemPool_t pools[64] = {};
-  if (dev < 0 || dev >= 64) return nullptr;
-  std::lock_guard<std::mutex> lock(mu);
-  if (!pools[dev]) {
-    hipMemPoolProps props{};
-    props.allocType = hipMemAllocationTypePinned;
-    props.location.type = hipMemLocationTypeDevice;
-    props.location.id = dev;
-    hipMemPool_t pool = nullptr;
-    if (hipMemPoolCreate(&pool, &props) != hipSuccess) return nullptr;
-    uint64_t keep = ~0ull;
-    // if the threshold cannot be set the pool hands freed memory back to the
-    // device at synchronisations instead: slower reuse, the same results
-    (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
-    pools[dev] = pool;
-  }
-  return pools[dev];
-}
-
 // Whether a call evaluates its B operand f(X_upper) once instead of in the
 // loader of every row tile (the same bits: f of the stored value, one
 // rounding; then the GEMM reads the result through LDS DMA like every other
@@ -273,40 +248,40 @@ bool s16_preact_rule(int mode, int act, int M, long long kb) {
   return M >= 1024 && kb >= (1LL << 20);
 }
 
-// The rule, and not while the stream is being captured into a graph (then the
-// register path runs, as it does when the pool cannot supply the buffer).
-bool s16_preactivates(int mode, int act, int M, long long kb, hipStream_t s) {
-  if (!s16_preact_rule(mode, act, M, kb)) return false;
-  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(s, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) {
-    (void)hipGetLastError();
-    return false;
-  }
-  return true;
+// Bytes of caller workspace a pre-activating call uses: the groups' activated
+// B operands, 16-bit, contiguous (0 when the rule says the call does not
+// pre-activate).
+long long s16_workspace_need(int mode, int act, int M, long long kb, int groups) {
+  return s16_preact_rule(mode, act, M, kb) ? (long long)groups * kb * 2 : 0;
 }
 
+// A standalone call on the LDS-DMA kernel.  With a caller workspace of at
+// least s16_workspace_need bytes the B operand is activated once into it
+// (an elementwise launch) and the GEMM reads it like the other operands;
+// otherwise every row tile activates its B block in its loader.  The library
+// allocates nothing either way.
 int run_s16(int mode, const WideProblem& q, int groups, long long a_gs, long long b_gs, long long o_gs,
-            long long x_gs, long long o2_gs, int operand, int act, void* stream, const char* what) {
+            long long x_gs, long long o2_gs, int operand, int act, void* workspace, long long ws_bytes, void* stream,
+            const char* what) {
   hipStream_t s = (hipStream_t)stream;
-  if (s16_preactivates(mode, act, q.M, b_gs, s)) {
-    int dev = 0;
-    hipMemPool_t pool = hipGetDevice(&dev) == hipSuccess ? s16_pool(dev) : nullptr;
+  const long long need = s16_workspace_need(mode, act, q.M, b_gs, groups);
+  if (need > 0 && workspace && ws_bytes >= need) {
     const long long n = (long long)groups * b_gs;  // the groups' B operands are contiguous, b_gs apart
-    void* buf = nullptr;
-    if (pool && hipMallocFromPoolAsync(&buf, (size_t)n * 2, pool, s) == hipSuccess) {
-      WideProblem qa = q;
-      qa.b = buf;
-      const std::vector<WideProblem> v = s16_groups(qa, groups, a_gs, b_gs, o_gs, x_gs, o2_gs);
-      hipError_t e = launch_s16_activate(q.b, buf, n, operand, act, s);
-      if (e == hipSuccess) e = launch_s16(mode, v.data(), groups, operand, IPC_ACT_IDENTITY, s);
-      const hipError_t ef = hipFreeAsync(buf, s);
-      if (e == hipSuccess) e = ef;
-      return launch_rc(e, what);
-    }
-    (void)hipGetLastError();
+    WideProblem qa = q;
+    qa.b = workspace;
+    const std::vector<WideProblem> v = s16_groups(qa, groups, a_gs, b_gs, o_gs, x_gs, o2_gs);
+    TRY(launch_rc(launch_s16_activate(q.b, workspace, n, operand, act, s), what));
+    return launch_rc(launch_s16(mode, v.data(), groups, operand, IPC_ACT_IDENTITY, s), what);
   }
   const std::vector<WideProblem> v = s16_groups(q, groups, a_gs, b_gs, o_gs, x_gs, o2_gs);
   return launch_rc(launch_s16(mode, v.data(), groups, operand, act, s), what);
+}
+
+int check_workspace(const void* workspace, long long ws_bytes) {
+  if (ws_bytes < 0) return fail(IPC_ERR_SHAPE, "workspace_bytes must be >= 0");
+  if (workspace && reinterpret_cast<uintptr_t>(workspace) % 16)
+    return fail(IPC_ERR_ALIGN, "workspace must be 16-byte aligned");
+  return ok();
 }
 
 }  // namespace
@@ -334,6 +309,14 @@ int ipc_device_check(int device, char* buf, int buflen) {
 
 int ipc_pred_err(const void* x_upper, const void* w, const void* x_lower, void* e, int M, int K, int B,
                  int groups, int storage, int operand, int split, int act, int tile, void* stream) {
+  return ipc_pred_err_ws(x_upper, w, x_lower, e, M, K, B, groups, storage, operand, split, act, tile, nullptr, 0,
+                         stream);
+}
+
+int ipc_pred_err_ws(const void* x_upper, const void* w, const void* x_lower, void* e, int M, int K, int B,
+                    int groups, int storage, int operand, int split, int act, int tile, void* workspace,
+                    long long workspace_bytes, void* stream) {
+  TRY(check_workspace(workspace, workspace_bytes));
   TRY(check_dtypes(storage, operand));
   TRY(check_split(split));
   TRY(check_act(act));
@@ -354,7 +337,7 @@ int ipc_pred_err(const void* x_upper, const void* w, const void* x_lower, void* 
     q.out = e; q.ldo = B; q.aux = x_lower; q.ldx = B;
     q.vec = B % 4 == 0 && al8(e) && al8(x_lower);
     return run_s16(S16_PRED, q, groups, (long long)M * K, (long long)K * B, (long long)M * B, (long long)M * B, 0,
-                   operand, act, stream, "ipc_pred_err");
+                   operand, act, workspace, workspace_bytes, stream, "ipc_pred_err");
   }
   GemmProblem p = make_pf(KIND_PRED, x_upper, w, x_lower, e, M, K, B, groups, act, es);
   return launch_rc(launch_gemm(&p, 1, storage, operand, effective_split(storage, operand, split), tile,
@@ -363,6 +346,13 @@ int ipc_pred_err(const void* x_upper, const void* w, const void* x_lower, void* 
 
 int ipc_forward(const void* x_upper, const void* w, void* out, int M, int K, int B, int groups, int storage,
                 int operand, int split, int act, int tile, void* stream) {
+  return ipc_forward_ws(x_upper, w, out, M, K, B, groups, storage, operand, split, act, tile, nullptr, 0, stream);
+}
+
+int ipc_forward_ws(const void* x_upper, const void* w, void* out, int M, int K, int B, int groups, int storage,
+                   int operand, int split, int act, int tile, void* workspace, long long workspace_bytes,
+                   void* stream) {
+  TRY(check_workspace(workspace, workspace_bytes));
   TRY(check_dtypes(storage, operand));
   TRY(check_split(split));
   TRY(check_act(act));
@@ -382,7 +372,7 @@ int ipc_forward(const void* x_upper, const void* w, void* out, int M, int K, int
     q.out = out; q.ldo = B;
     q.vec = B % 4 == 0 && al8(out);
     return run_s16(S16_FWD, q, groups, (long long)M * K, (long long)K * B, (long long)M * B, 0, 0, operand, act,
-                   stream, "ipc_forward");
+                   workspace, workspace_bytes, stream, "ipc_forward");
   }
   GemmProblem p = make_pf(KIND_FWD, x_upper, w, nullptr, out, M, K, B, groups, act, es);
   return launch_rc(launch_gemm(&p, 1, storage, operand, effective_split(storage, operand, split), tile,
@@ -414,7 +404,7 @@ int ipc_infer_update(void* x, const void* e, const void* w_lower, const void* e_
     q.scal = gamma;
     q.vec = B % 4 == 0 && al8(x) && al8(e) && al8(a_out);
     return run_s16(S16_INFER, q, groups, (long long)K * M, (long long)K * B, (long long)M * B, (long long)M * B,
-                   (long long)M * B, operand, act, stream, "ipc_infer_update");
+                   (long long)M * B, operand, act, nullptr, 0, stream, "ipc_infer_update");
   }
   GemmProblem p = make_inf(x, e, w_lower, e_lower, a_out, M, K, B, groups, gamma, act, es);
   return launch_rc(launch_gemm(&p, 1, storage, operand, IPC_SPLIT_NONE, tile, (hipStream_t)stream),
@@ -423,6 +413,14 @@ int ipc_infer_update(void* x, const void* e, const void* w_lower, const void* e_
 
 int ipc_weight_update(void* w, const void* e, const void* x_upper, int M, int K, int B, int groups,
                       float alpha, int recompute, int storage, int operand, int act, int tile, void* stream) {
+  return ipc_weight_update_ws(w, e, x_upper, M, K, B, groups, alpha, recompute, storage, operand, act, tile, nullptr,
+                              0, stream);
+}
+
+int ipc_weight_update_ws(void* w, const void* e, const void* x_upper, int M, int K, int B, int groups,
+                         float alpha, int recompute, int storage, int operand, int act, int tile, void* workspace,
+                         long long workspace_bytes, void* stream) {
+  TRY(check_workspace(workspace, workspace_bytes));
   TRY(check_dtypes(storage, operand));
   TRY(check_act(act));
   TRY(check_dims(M, K, B, groups));
@@ -442,7 +440,7 @@ int ipc_weight_update(void* w, const void* e, const void* x_upper, int M, int K,
     q.scal = alpha;
     q.vec = K % 4 == 0 && al8(w);
     return run_s16(S16_WEIGHT, q, groups, (long long)M * B, (long long)K * B, (long long)M * K, 0, 0, operand,
-                   recompute ? act : IPC_ACT_IDENTITY, stream, "ipc_weight_update");
+                   recompute ? act : IPC_ACT_IDENTITY, workspace, workspace_bytes, stream, "ipc_weight_update");
   }
   GemmProblem p = make_wgt(w, e, x_upper, M, K, B, groups, alpha, recompute, act, es);
   return launch_rc(launch_gemm(&p, 1, storage, operand, IPC_SPLIT_NONE, tile, (hipStream_t)stream),
@@ -485,6 +483,7 @@ struct ipc_plan {
   bool narrow = false;
   NarrowArgs nargs{};
   bool resident = false;
+  bool res_stale = false;  // bound since the last layer-resident launch: invalidate its caches first
   ResidentArgs rargs{};
   long long res_ws_off = 0;
   // wide GEMM path
@@ -532,6 +531,10 @@ constexpr int kNarrowSpinLimit = 1 << 22;
 // (ipc_set_coresident_limit, a test hook).
 int g_coresident_limit = 0;
 
+// >= 0: the spin limit of ipc_steps_noalloc's waits instead of the default
+// (ipc_noalloc_set_spin_limit, a test hook).
+int g_noalloc_spin_limit = -1;
+
 // Static device scratch of the no-allocation entry point (ipc_steps_noalloc):
 // every GPU the library runs on holds its own copy for the life of the
 // process.  Host code never uses the array's name as an address (on the host
@@ -562,8 +565,11 @@ int scratch_address(char** out) {
 
 // Zeroes the column kernel's barrier words and, when given, the resident
 // kernel's flag words (64 words each) before a launch on the scratch.
+// Word 2 (the timeout word) is left alone: it stays set until
+// ipc_noalloc_check reads and clears it, so a call whose waits gave up is
+// reported even after later calls.
 __global__ void scratch_clear_kernel(unsigned* bar, unsigned* flags) {
-  if (threadIdx.x < 64) bar[threadIdx.x] = 0u;
+  if (threadIdx.x < 64 && threadIdx.x != 2) bar[threadIdx.x] = 0u;
   if (flags) flags[threadIdx.x] = 0u;  // the layer-resident flag area, RES_FLAG_BYTES / 4 words
 }
 
@@ -705,6 +711,13 @@ long long resident_eligible(int L, const int* dims, int B, int operand, int spli
 
 int launch_narrow_mode(ipc_plan* plan, int mode, int steps, hipStream_t s) {
   if (mode == NMODE_STEPS && plan->resident) {
+    // The caches a resident launch keeps in the workspace (f(x[L]) images,
+    // hidden f(x), the next launch's first-step partials) belong to the
+    // buffers bound when they were written: after a (re)bind, start cold.
+    if (plan->res_stale) {
+      TRY(launch_rc(resident_invalidate(plan->rargs, s), "layer-resident cache invalidation"));
+      plan->res_stale = false;
+    }
     ResidentArgs a = plan->rargs;
     a.steps = steps;
     return launch_rc(launch_resident(a, plan->operand, plan->split, plan->act, s), "layer-resident whole-step kernel");
@@ -1076,6 +1089,7 @@ int ipc_plan_bind(ipc_plan* plan, void* const* x, void* const* e, void* const* w
   }
   plan->workspace = workspace;
   plan->bound = true;
+  plan->res_stale = plan->resident;
   return ok();
 }
 
@@ -1381,7 +1395,8 @@ int ipc_steps_noalloc(int L, const int* dims, int B, void* const* x, void* const
   cap = cap < 0 || cap > 256 ? 256 : cap;
   NarrowArgs na{};
   TRY(bind_whole_step(na, res_bytes >= 0 ? &ra : nullptr, L, dims, B, x, e, w, nullptr, act, operand, esplit, alpha,
-                      gamma, narrow_outer(B, weight_mode), kNarrowSpinLimit, cap, ws, res_off));
+                      gamma, narrow_outer(B, weight_mode),
+                      g_noalloc_spin_limit >= 0 ? g_noalloc_spin_limit : kNarrowSpinLimit, cap, ws, res_off));
   hipStream_t s = (hipStream_t)stream;
   // the scratch keeps the previous call's contents: the barrier words and the
   // resident flag area (step flags, cache generation and the workgroups'
@@ -1399,15 +1414,75 @@ int ipc_steps_noalloc(int L, const int* dims, int B, void* const* x, void* const
   return launch_rc(launch_narrow(na, operand, esplit, s), "whole-step kernel");
 }
 
+int ipc_noalloc_check(void* stream) {
+  hipStream_t s = (hipStream_t)stream;
+  if (hipStreamSynchronize(s) != hipSuccess) return fail(IPC_ERR_LAUNCH, "stream synchronisation failed");
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(IPC_ERR_DEVICE, "no current device");
+  char* ws = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    ws = g_scratch_ptr[dev];
+  }
+  if (!ws) return ok();  // no call has run on this device yet
+  unsigned* word = reinterpret_cast<unsigned*>(ws) + 2;
+  unsigned flag = 0;
+  if (hipMemcpyAsync(&flag, word, sizeof(flag), hipMemcpyDeviceToHost, s) != hipSuccess ||
+      hipStreamSynchronize(s) != hipSuccess)
+    return fail(IPC_ERR_LAUNCH, "reading the scratch's timeout word failed");
+  if (flag == 0) return ok();
+  const unsigned zero = 0;
+  if (hipMemcpyAsync(word, &zero, sizeof(zero), hipMemcpyHostToDevice, s) != hipSuccess ||
+      hipStreamSynchronize(s) != hipSuccess)
+    return fail(IPC_ERR_LAUNCH, "clearing the scratch's timeout word failed");
+  return fail(IPC_ERR_TIMEOUT,
+              "a wait of an ipc_steps_noalloc call ran past its spin limit: the outputs of the calls on this device "
+              "since the last check are invalid");
+}
+
+int ipc_noalloc_set_spin_limit(int limit) {
+  g_noalloc_spin_limit = limit < 0 ? -1 : limit;
+  return ok();
+}
+
 int ipc_set_coresident_limit(int blocks) {
   if (blocks < 0) return fail(IPC_ERR_CONFIG, "the co-resident limit must be >= 0 (got %d)", blocks);
   g_coresident_limit = blocks;
   return ok();
 }
 
+int ipc_wide_problem_check(int phase, int split, int fp32_w, int has_lo, int K, int ksplit) {
+  int mode;
+  switch (phase) {
+    case IPC_PHASE_PRED: mode = WIDE_PRED; break;
+    case IPC_PHASE_INFER: mode = WIDE_INFER; break;
+    case IPC_PHASE_WEIGHT: mode = WIDE_WEIGHT; break;
+    case IPC_PHASE_FORWARD: mode = WIDE_FWD; break;
+    default: return fail(IPC_ERR_CONFIG, "unknown phase %d", phase);
+  }
+  WideProblem q{};
+  static const unsigned char dummy[16] = {};
+  q.M = q.N = 64;
+  q.K = K;
+  q.a = q.b = dummy;
+  q.a_lo = has_lo ? dummy : nullptr;
+  q.ksplit = ksplit;
+  if (!wide_problem_ok(mode, split, fp32_w != 0, q))
+    return fail(IPC_ERR_CONFIG, "LDS-DMA GEMM problem refused on the host (phase %d, split %d, fp32 W %d, lo %d, "
+                "K %d, k-split %d)", phase, split, fp32_w, has_lo, K, ksplit);
+  return ok();
+}
+
 int ipc_s16_preactivates(int kind, int act, int M, int K, int B) {
   const int mode = kind == IPC_PHASE_PRED ? S16_PRED : kind == IPC_PHASE_WEIGHT ? S16_WEIGHT : S16_INFER;
   return s16_preact_rule(mode, act, M, (long long)K * B) ? 1 : 0;
+}
+
+long long ipc_s16_workspace_bytes(int kind, int act, int M, int K, int B, int groups) {
+  if (M < 1 || K < 1 || B < 1 || groups < 1) return 0;
+  const int mode = kind == IPC_PHASE_PRED ? S16_PRED : kind == IPC_PHASE_WEIGHT ? S16_WEIGHT : S16_INFER;
+  return s16_workspace_need(mode, act, M, (long long)K * B, groups);
 }
 
 int ipc_set_s16_preactivate(int mode) {

@@ -608,6 +608,19 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
   }
 }
 
+// Host-side check of one problem, made for every problem of a launch before
+// any HIP call.  A split-2 kernel that does not split the fp32 W itself (A32)
+// DMA-loads an A_lo block next to every A block (prediction and forward
+// alike), so a problem without A_lo would make every workgroup read through a
+// null pointer: a GPU memory fault, not an error code.  A k-split prediction
+// slice must be a whole number of k-steps.
+inline bool problem_ok(int mode, int split, bool a32, const WideProblem& q) {
+  if (split == 2 && !a32 && !q.a_lo) return false;
+  const int ks = mode == WIDE_PRED && q.ksplit > 1 ? q.ksplit : 1;
+  if (ks > 1 && q.K % (ks * WIDE_BK) != 0) return false;
+  return true;
+}
+
 // One kernel configuration: LDS limit set once per process, launch over a
 // ragged batch of up to WIDE_MAX_BATCH problems.
 template <typename OT, int MODE, int SPLIT, int ACT, bool BREG, int BM, int BN, int S, int WGM, int WGN,
@@ -623,6 +636,8 @@ struct Cfg {
     return e;
   }
   static hipError_t launch(const WideProblem* probs, int count, hipStream_t s) {
+    for (int i = 0; i < count; ++i)
+      if (!problem_ok(MODE, SPLIT, A32, probs[i])) return hipErrorInvalidValue;
     const hipError_t pe = prepare();
     if (pe != hipSuccess) return pe;
     Batch bt;
@@ -630,10 +645,8 @@ struct Cfg {
     bt.tail = count;
     int total = 0;
     for (int i = 0; i < count; ++i) {
-      if (SPLIT == 2 && MODE == WIDE_PRED && !A32 && !probs[i].a_lo) return hipErrorInvalidValue;
       const int ks = MODE == WIDE_PRED && probs[i].ksplit > 1 ? probs[i].ksplit : 1;
       if (ks > 1) {
-        if (probs[i].K % (ks * WIDE_BK) != 0) return hipErrorInvalidValue;
         if (bt.tail == count) bt.tail = i;
       } else if (bt.tail != count) {
         return hipErrorInvalidValue;  // k-split problems must come last

@@ -111,6 +111,10 @@ void wide_pred_tile(int split, int cfg, int* bm, int* bn);
 hipError_t launch_wide(int mode, const WideProblem* probs, int count, int operand, int split, int act,
                        hipStream_t s, int cfg = 0, bool a32 = false);
 
+// The host-side check every LDS-DMA launch makes of each problem before any
+// HIP call (mode WIDE_PRED / _INFER / _WEIGHT / _FWD or an S16_* mode).
+bool wide_problem_ok(int mode, int split, bool a32, const WideProblem& q);
+
 // Raises the dynamic-LDS limit of every wide-path kernel instantiation.
 hipError_t wide_prepare();
 

@@ -297,6 +297,10 @@ hipError_t launch_wide(int mode, const WideProblem* probs, int count, int operan
   return hipSuccess;
 }
 
+bool wide_problem_ok(int mode, int split, bool a32, const WideProblem& q) {
+  return dma::problem_ok(mode, split, a32, q);
+}
+
 hipError_t launch_wide_reduce(const WideReduce& r, int operand, hipStream_t s) {
   if (r.slices < 1 || r.M <= 0 || r.N <= 0) return hipErrorInvalidValue;
   const dim3 grid(((r.M + CP_T - 1) / CP_T) * ((r.N + CP_T - 1) / CP_T));

@@ -110,32 +110,71 @@ class _Kernel:
     def _shape(self, *dims):
         return (self.groups, *dims) if self.groups > 1 else tuple(dims)
 
+    # kind code of ipc_s16_workspace_bytes (IPC_PHASE_*): -1 = never uses a workspace
+    _ws_kind = -1
+
+    @property
+    def workspace_bytes(self) -> int:
+        """Bytes of caller workspace that let a call evaluate f(X_upper) once
+        instead of in every row tile's loader (0: the call never uses one).
+        Only 16-bit storage on the LDS-DMA kernel uses it; the library itself
+        allocates nothing."""
+        if self._ws_kind < 0 or self.storage == nat.DT_F32:
+            return 0
+        return int(nat.lib().ipc_s16_workspace_bytes(self._ws_kind, self.act, self.M, self.K, self.B, self.groups))
+
+    def new_workspace(self, device=None) -> torch.Tensor | None:
+        """A caller-owned workspace of ``workspace_bytes`` (None when the call
+        uses none), to be passed as ``workspace=`` to calls on one stream."""
+        n = self.workspace_bytes
+        if n <= 0:
+            return None
+        return torch.empty(((n + 15) // 16 * 16,), dtype=torch.uint8, device=device or torch.device("cuda"))
+
+    @staticmethod
+    def _ws(workspace):
+        if workspace is None:
+            return None, 0
+        if not isinstance(workspace, torch.Tensor) or workspace.device.type != "cuda" or not workspace.is_contiguous():
+            raise ValueError("workspace must be a contiguous device tensor")
+        return workspace.data_ptr(), workspace.numel() * workspace.element_size()
+
 
 class PredictionErrorKernel(_Kernel):
-    """``k(X_upper[K,B], W[M,K], X_lower[M,B], E[M,B])``: ``E = X_lower - W f(X_upper)``."""
+    """``k(X_upper[K,B], W[M,K], X_lower[M,B], E[M,B], *, workspace=None)``:
+    ``E = X_lower - W f(X_upper)``.  ``workspace`` (optional, caller-owned,
+    ``new_workspace()``) lets a large 16-bit call activate f(X_upper) once."""
 
-    def __call__(self, x_upper, w, x_lower, e):
+    _ws_kind = 0
+
+    def __call__(self, x_upper, w, x_lower, e, *, workspace=None):
         M, K, B, dt = self.M, self.K, self.B, self.dtype
         _check(x_upper, "X_upper", self._shape(K, B), dt)
         _check(w, "W", self._shape(M, K), dt)
         _check(x_lower, "X_lower", self._shape(M, B), dt)
         _check(e, "E", self._shape(M, B), dt)
-        nat.check(nat.lib().ipc_pred_err(
+        ws, nbytes = self._ws(workspace)
+        nat.check(nat.lib().ipc_pred_err_ws(
             x_upper.data_ptr(), w.data_ptr(), x_lower.data_ptr(), e.data_ptr(), M, K, B, self.groups,
-            self.storage, self.operand, self.split, self.act, self.tile, nat.current_stream_handle(e.device)))
+            self.storage, self.operand, self.split, self.act, self.tile, ws, nbytes,
+            nat.current_stream_handle(e.device)))
 
 
 class ForwardKernel(_Kernel):
-    """``k(X_upper[K,B], W[M,K], OUT[M,B])``: ``OUT = W f(X_upper)``."""
+    """``k(X_upper[K,B], W[M,K], OUT[M,B], *, workspace=None)``: ``OUT = W f(X_upper)``."""
 
-    def __call__(self, x_upper, w, out):
+    _ws_kind = 0
+
+    def __call__(self, x_upper, w, out, *, workspace=None):
         M, K, B, dt = self.M, self.K, self.B, self.dtype
         _check(x_upper, "X_upper", self._shape(K, B), dt)
         _check(w, "W", self._shape(M, K), dt)
         _check(out, "OUT", self._shape(M, B), dt)
-        nat.check(nat.lib().ipc_forward(
+        ws, nbytes = self._ws(workspace)
+        nat.check(nat.lib().ipc_forward_ws(
             x_upper.data_ptr(), w.data_ptr(), out.data_ptr(), M, K, B, self.groups,
-            self.storage, self.operand, self.split, self.act, self.tile, nat.current_stream_handle(out.device)))
+            self.storage, self.operand, self.split, self.act, self.tile, ws, nbytes,
+            nat.current_stream_handle(out.device)))
 
 
 class InferenceUpdateKernel(_Kernel):
@@ -166,22 +205,25 @@ class InferenceUpdateKernel(_Kernel):
 
 
 class WeightUpdateKernel(_Kernel):
-    """``k(W[M,K], E[M,B], X_upper_or_A[K,B])``: ``W += alpha E f(X_upper)^T``
-    (recompute) or ``W += alpha E A^T`` (saved activation)."""
+    """``k(W[M,K], E[M,B], X_upper_or_A[K,B], *, workspace=None)``:
+    ``W += alpha E f(X_upper)^T`` (recompute) or ``W += alpha E A^T`` (saved
+    activation; no workspace is used then)."""
 
     def __init__(self, *a, alpha: float, recompute_activation: bool, **kw):
         super().__init__(*a, **kw)
         self.alpha = float(alpha)
         self.recompute_activation = bool(recompute_activation)
+        self._ws_kind = 2 if self.recompute_activation else -1
 
-    def __call__(self, w, e, x_upper):
+    def __call__(self, w, e, x_upper, *, workspace=None):
         M, K, B, dt = self.M, self.K, self.B, self.dtype
         _check(w, "W", self._shape(M, K), dt)
         _check(e, "E", self._shape(M, B), dt)
         _check(x_upper, "X_upper", self._shape(K, B), dt)
-        nat.check(nat.lib().ipc_weight_update(
+        ws, nbytes = self._ws(workspace)
+        nat.check(nat.lib().ipc_weight_update_ws(
             w.data_ptr(), e.data_ptr(), x_upper.data_ptr(), M, K, B, self.groups, self.alpha,
-            int(self.recompute_activation), self.storage, self.operand, self.act, self.tile,
+            int(self.recompute_activation), self.storage, self.operand, self.act, self.tile, ws, nbytes,
             nat.current_stream_handle(w.device)))
 
 

@@ -1,23 +1,29 @@
-"""Per-shape kernel tuning tables, schema version 1 (reference ``src/ipc_tilelang/tuning.py:10-108``).
+"""Per-shape kernel tuning tables in the reference's schema version 1.
 
-The file format is the reference's, so a table written by either side reads
-on the other: ``{"schema_version": 1, "device", "capability", "entries":
-[{"kind", "shape": {"M", "K", "B"}, "activation", "dtype", "median_ms",
-"spill_suspected", "config": {...KernelConfig fields...}}]}``.  A config
-written here carries this library's ``tile`` id next to the reference's
-block sizes; a reference config (block sizes only) maps to the nearest tile
-(``KernelConfig.tile_id``).
+The format (reference ``src/ipc_tilelang/tuning.py:10-108``) is kept so that a
+table written on either side reads on the other::
+
+    {"schema_version": 1, "device": ..., "capability": [major, minor] | null,
+     "entries": [{"kind", "shape": {"M", "K", "B"}, "activation", "dtype",
+                  "median_ms", "spill_suspected", "config": {...}}]}
+
+``config`` holds ``KernelConfig`` fields.  A config written here carries this
+library's ``tile`` id next to the block sizes; a config without one (a
+reference table) maps to the nearest tile through ``KernelConfig.tile_id``.
+The reader is stricter than the format needs: a row without its kind, shape or
+config is reported with its index instead of being half-read.
 """
 from __future__ import annotations
 
 import json
-from dataclasses import dataclass, fields
+from dataclasses import dataclass, field, fields
 from pathlib import Path
 from typing import Iterable
 
 from .kernels import KernelConfig
 
 SCHEMA_VERSION = 1
+_ROW_DEFAULTS = {"activation": "relu", "dtype": "float16"}
 
 
 def config_from_dict(data: dict) -> KernelConfig:
@@ -30,17 +36,14 @@ def config_from_dict(data: dict) -> KernelConfig:
 def config_to_dict(cfg: KernelConfig) -> dict:
     """The JSON form of a config: every field set, ``tile`` only when given,
     so a config without one serialises exactly like the reference's."""
-    out = {}
-    for f in fields(KernelConfig):
-        v = getattr(cfg, f.name)
-        if f.name == "tile" and v is None:
-            continue
-        out[f.name] = v
-    return out
+    return {f.name: getattr(cfg, f.name) for f in fields(KernelConfig)
+            if not (f.name == "tile" and getattr(cfg, f.name) is None)}
 
 
 @dataclass(frozen=True)
 class TuningKey:
+    """What a tuned config is for: the kernel kind, its GEMM shape, the fused
+    activation and the storage dtype name."""
     kind: str
     M: int
     K: int
@@ -57,9 +60,43 @@ class TuningEntry:
     spill_suspected: bool | None = None
 
 
+def _row_to_entry(index: int, row: object, source: str) -> TuningEntry:
+    if not isinstance(row, dict):
+        raise ValueError(f"{source}: entry {index} is a {type(row).__name__}, not an object")
+    missing = [k for k in ("kind", "shape", "config") if k not in row]
+    if missing:
+        raise ValueError(f"{source}: entry {index} lacks {', '.join(missing)}")
+    shape = row["shape"]
+    try:
+        M, K, B = (int(shape[d]) for d in ("M", "K", "B"))
+    except (KeyError, TypeError, ValueError) as exc:
+        raise ValueError(f"{source}: entry {index} has no integer M, K and B in its shape") from exc
+    key = TuningKey(str(row["kind"]), M, K, B, str(row.get("activation", _ROW_DEFAULTS["activation"])),
+                    str(row.get("dtype", _ROW_DEFAULTS["dtype"])))
+    ms = row.get("median_ms")
+    return TuningEntry(key, config_from_dict(row["config"]), None if ms is None else float(ms),
+                       row.get("spill_suspected"))
+
+
+def _entry_to_row(e: TuningEntry) -> dict:
+    k = e.key
+    return {"kind": k.kind, "shape": {"M": k.M, "K": k.K, "B": k.B}, "activation": k.activation,
+            "dtype": k.dtype, "median_ms": e.median_ms, "spill_suspected": e.spill_suspected,
+            "config": config_to_dict(e.config)}
+
+
 @dataclass(frozen=True)
 class TuningTable:
+    """An ordered list of entries; a lookup returns the first entry's config
+    whose key matches exactly (later duplicates never win)."""
     entries: tuple[TuningEntry, ...]
+    _index: dict = field(default=None, init=False, repr=False, compare=False, hash=False)
+
+    def __post_init__(self):
+        index: dict[TuningKey, KernelConfig] = {}
+        for e in self.entries:
+            index.setdefault(e.key, e.config)
+        object.__setattr__(self, "_index", index)
 
     @classmethod
     def from_entries(cls, entries: Iterable[TuningEntry]) -> "TuningTable":
@@ -67,34 +104,27 @@ class TuningTable:
 
     @classmethod
     def from_json(cls, path: str | Path) -> "TuningTable":
+        source = str(path)
         payload = json.loads(Path(path).read_text(encoding="utf-8"))
-        if payload.get("schema_version") != SCHEMA_VERSION:
-            raise ValueError(f"Unsupported tuning schema: {payload.get('schema_version')!r}; "
-                             f"expected {SCHEMA_VERSION}")
-        entries = []
-        for row in payload.get("entries", []):
-            shape = row["shape"]
-            key = TuningKey(kind=row["kind"], M=int(shape["M"]), K=int(shape["K"]), B=int(shape["B"]),
-                            activation=str(row.get("activation", "relu")), dtype=str(row.get("dtype", "float16")))
-            ms = row.get("median_ms")
-            entries.append(TuningEntry(key, config_from_dict(row["config"]), None if ms is None else float(ms),
-                                       row.get("spill_suspected")))
-        return cls(tuple(entries))
+        if not isinstance(payload, dict):
+            raise ValueError(f"{source}: a tuning table is a JSON object")
+        version = payload.get("schema_version")
+        if version != SCHEMA_VERSION:
+            raise ValueError(f"Unsupported tuning schema: {source} has schema_version {version!r}, "
+                             f"and this reader handles version {SCHEMA_VERSION} only")
+        rows = payload.get("entries", [])
+        if not isinstance(rows, list):
+            raise ValueError(f"{source}: 'entries' is not a list")
+        return cls(tuple(_row_to_entry(i, r, source) for i, r in enumerate(rows)))
 
     def lookup(self, *, kind: str, M: int, K: int, B: int, activation: str, dtype: str) -> KernelConfig | None:
-        key = TuningKey(kind, int(M), int(K), int(B), activation, dtype)
-        for entry in self.entries:
-            if entry.key == key:
-                return entry.config
-        return None
+        return self._index.get(TuningKey(kind, int(M), int(K), int(B), activation, dtype))
 
     def to_json(self, path: str | Path, *, device: str | None = None,
                 capability: tuple[int, int] | None = None) -> None:
-        rows = [{"kind": e.key.kind, "shape": {"M": e.key.M, "K": e.key.K, "B": e.key.B},
-                 "activation": e.key.activation, "dtype": e.key.dtype, "median_ms": e.median_ms,
-                 "spill_suspected": e.spill_suspected, "config": config_to_dict(e.config)} for e in self.entries]
         payload = {"schema_version": SCHEMA_VERSION, "device": device,
-                   "capability": list(capability) if capability is not None else None, "entries": rows}
+                   "capability": None if capability is None else list(capability),
+                   "entries": [_entry_to_row(e) for e in self.entries]}
         out = Path(path)
         out.parent.mkdir(parents=True, exist_ok=True)
         out.write_text(json.dumps(payload, indent=2), encoding="utf-8")

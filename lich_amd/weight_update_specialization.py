@@ -33,32 +33,43 @@ class WeightPolicyKey:
     dtype: str = "float16"
 
 
+_BACKENDS = ("gemm", "outer")
+
+
+def _policy_row(row: object):
+    """``(key, backend)`` of one policy row, or None for a row a reader must
+    skip: not an object, a shape field missing or not an integer, or a
+    backend other than gemm / outer."""
+    if not isinstance(row, dict):
+        return None
+    backend = str(row.get("backend", "gemm")).lower()
+    if backend not in _BACKENDS:
+        return None
+    try:
+        shape = tuple(int(row[k]) for k in ("M", "K", "B")) + (int(row.get("count", 1)),)
+    except (KeyError, TypeError, ValueError):
+        return None
+    return shape + (str(row.get("activation", "relu")), str(row.get("dtype", "float16"))), backend
+
+
 class SmallBWeightPolicy:
-    """Read-only exact-shape policy (same JSON rows as the reference:
-    ``M, K, B, count, activation, dtype, backend``)."""
+    """Read-only exact-shape policy: JSON rows ``M, K, B, count, activation,
+    dtype, backend`` (the reference's policy format), each choosing "gemm" or
+    "outer" for one layer shape; any shape without a row uses "gemm"."""
 
     def __init__(self, path: str | Path):
         self.path = Path(path)
-        with self.path.open("r", encoding="utf-8") as f:
-            data = json.load(f)
+        data = json.loads(self.path.read_text(encoding="utf-8"))
         if not isinstance(data, dict):
-            raise ValueError(f"Invalid weight-update policy: {self.path}")
+            raise ValueError(f"{self.path}: a small-batch weight-update policy is a JSON object with an "
+                             f"'entries' list, not a {type(data).__name__}")
         self.data = data
-        self.entries: dict[tuple[int, int, int, int, str, str], str] = {}
-        for row in data.get("entries", []):
-            if not isinstance(row, dict):
-                continue
-            try:
-                key = (int(row["M"]), int(row["K"]), int(row["B"]), int(row.get("count", 1)),
-                       str(row.get("activation", "relu")), str(row.get("dtype", "float16")))
-            except (KeyError, TypeError, ValueError):
-                continue
-            backend = str(row.get("backend", "gemm")).lower()
-            if backend in {"gemm", "outer"}:
-                self.entries[key] = backend
+        self.entries: dict[tuple[int, int, int, int, str, str], str] = dict(
+            parsed for parsed in map(_policy_row, data.get("entries", [])) if parsed is not None)
 
     def backend(self, *, M: int, K: int, B: int, activation: str, dtype: Any, count: int = 1) -> str:
-        return self.entries.get((int(M), int(K), int(B), int(count), str(activation), _dtype_name(dtype)), "gemm")
+        key = (int(M), int(K), int(B), int(count), str(activation), _dtype_name(dtype))
+        return self.entries.get(key, "gemm")
 
 
 class SmallBWeightUpdater:

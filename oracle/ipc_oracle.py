@@ -17,16 +17,18 @@ Conventions (reference ``README.md:41-50``, ``src/ipc_tilelang/reference.py:35-5
   where the state update reads time-t ``x, W, eps`` and the weight update
   reads the just-updated ``x`` (``reference.py:45-57``).
 
-Parity status: every function here is pinned by ``tests/test_oracle.py``
-against the independent float64 loops of ``oracle/ipc_brute.py``, against
-``torch.autograd`` (activation derivatives) and against closed forms and
-invariants (forward-init wavefront, gamma=0, alpha=0, W=0, linearity, phase
-order).  No function is left unpinned.
+Parity status: ``tests/test_oracle.py`` calls every function here and pins
+each one against the independent float64 loops of ``oracle/ipc_brute.py``
+(``ipc_step``, ``run_steps`` over one and three steps, the single-kernel
+helpers), against ``torch.autograd`` (activation derivatives) and against
+closed forms and invariants (forward-init wavefront, gamma=0, alpha=0, W=0,
+linearity, phase order, the kaiming / Xavier bounds, the one-hot layout).
+``tests/test_oracle.py::test_every_oracle_function_is_exercised`` fails if a
+function is added here without a test that calls it.
 """
 from __future__ import annotations
 
 import math
-from dataclasses import dataclass
 from typing import Sequence
 
 import torch
@@ -128,12 +130,6 @@ def make_batch(dims: Sequence[int], batch: int, *, seed: int = 0, input_dist: st
     return x_in.to(dtype), labels, one_hot(labels, int(dims[0]), dtype=dtype)
 
 
-@dataclass
-class State:
-    x: list[torch.Tensor]
-    w: list[torch.Tensor]
-
-
 def forward_init(x_input: torch.Tensor, y_target: torch.Tensor, w: Sequence[torch.Tensor],
                  act: str) -> list[torch.Tensor]:
     """Trainer semantics (``trainer.py:509-516``): ``x[L]`` = input, hidden
@@ -145,15 +141,6 @@ def forward_init(x_input: torch.Tensor, y_target: torch.Tensor, w: Sequence[torc
         pred = w[l] @ act_forward(act, x[l + 1])
         x[l] = pred if l > 0 else None  # type: ignore[assignment]
     x[0] = y_target.clone()
-    return x
-
-
-def zero_init(x_input: torch.Tensor, y_target: torch.Tensor, dims: Sequence[int]) -> list[torch.Tensor]:
-    """The oracle-only quirk of ``reference.py:24-33``: hidden states stay 0."""
-    B = x_input.shape[1]
-    x = [torch.zeros((int(d), B), dtype=x_input.dtype) for d in dims]
-    x[0] = y_target.clone()
-    x[-1] = x_input.clone()
     return x
 
 

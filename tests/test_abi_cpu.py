@@ -558,3 +558,27 @@ def test_s16_preactivation_rule():
         assert lib.ipc_set_s16_preactivate(1) == nat.IPC_OK and q(0, relu, 8, 64, 8) == 1
     finally:
         lib.ipc_set_s16_preactivate(-1)
+
+
+def test_split2_problem_without_lo_operand_is_refused_on_the_host():
+    """A split-2 LDS-DMA kernel that does not split the fp32 W itself loads a
+    lo block next to every W block; a problem without that operand would read
+    through a null pointer on every workgroup (a GPU memory fault, not an error
+    code).  Every launch checks each problem on the host first, before its
+    first HIP call, for the prediction and the forward initialisation alike."""
+    lib = _lib()
+    P, I, W, F = 0, 1, 2, 3
+    chk = lib.ipc_wide_problem_check
+    for phase in (P, F):
+        assert chk(phase, 2, 0, 0, 4096, 1) == nat.ERR_CONFIG, phase
+        assert "refused" in nat.last_error()
+        assert chk(phase, 2, 0, 1, 4096, 1) == nat.IPC_OK   # lo operand passed
+        assert chk(phase, 2, 1, 0, 4096, 1) == nat.IPC_OK   # the kernel splits the fp32 W itself
+        assert chk(phase, 1, 0, 0, 4096, 1) == nat.IPC_OK   # unsplit: no lo operand read
+    for phase in (I, W):
+        assert chk(phase, 1, 0, 0, 1024, 1) == nat.IPC_OK
+    # k-split slices are whole 64-k steps
+    assert chk(P, 2, 1, 0, 4096, 8) == nat.IPC_OK
+    assert chk(P, 2, 1, 0, 4096, 128) == nat.ERR_CONFIG
+    assert chk(P, 1, 0, 0, 4160, 2) == nat.ERR_CONFIG
+    assert chk(7, 1, 0, 0, 64, 1) == nat.ERR_CONFIG

@@ -12,6 +12,8 @@ import torch
 
 from oracle import ipc_oracle as O
 
+from tests.helpers import delta_w_check
+
 FIXTURES = sorted((Path(__file__).parent / "golden").glob("*.npz"))
 
 
@@ -61,4 +63,8 @@ def test_hip_path_reproduces_fixture(path, fused):
     torch.cuda.synchronize()
     assert O.global_rel_err(m.x, g["xT"]) <= 1e-5
     assert O.global_rel_err(m.w, g["wT"]) <= 1e-5
+    ok, msg = delta_w_check(m.w, g["w0"], g["wT"], g["x0"], g["T"], act=g["act"], alpha=g["alpha"],
+                            gamma=g["gamma"])
+    print(f"golden {path.stem} fused={fused}: {msg}")
+    assert ok, msg
     assert O.global_rel_err(m.e[:-1], g["eT"]) <= 1e-5

@@ -166,10 +166,10 @@ def _preact(mode):
 @pytest.mark.parametrize("act", ACTS)
 @pytest.mark.parametrize("M,K,B,G", [(1024, 128, 256, 1), (1088, 1088, 192, 2), (300, 192, 128, 1)])
 def test_preactivated_operand_gives_the_register_path_bits(M, K, B, G, act, op):
-    """f(X_upper) evaluated once into a pooled buffer (ipc_set_s16_preactivate(1))
-    against the loader's register path (0): prediction, forward and the
-    recomputing weight update agree bit for bit, grouped (square layers) or
-    not, above and below the automatic threshold (M >= 1024)."""
+    """f(X_upper) evaluated once into a caller workspace (mode 1: whenever one
+    is given) against the loader's register path (no workspace): prediction,
+    forward and the recomputing weight update agree bit for bit, grouped
+    (square layers) or not, above and below the automatic threshold."""
     report("dma16-preact", M=M, K=K, B=B, G=G, act=act, op=op)
     dt = OPS[op]
     g = gen(13 * M + K + B + G)
@@ -177,54 +177,101 @@ def test_preactivated_operand_gives_the_register_path_bits(M, K, B, G, act, op):
     wk, e = randn((G, M, K), g, 1 / math.sqrt(K)), randn((G, M, B), g)
     res = {}
     try:
-        for mode in (0, 1):
-            _preact(mode)
+        _preact(1)
+        for use_ws in (False, True):
             ep = torch.empty((G, M, B), device=DEV, dtype=dt)
             fp = torch.empty((G, M, B), device=DEV, dtype=dt)
             wd = _t(wk, dt)
             if G == 1:
-                build_prediction_error(M, K, B, act, dt, DMA)(_t(xu[0], dt), _t(w[0], dt), _t(xl[0], dt), ep[0])
-                build_forward(M, K, B, act, dt, DMA)(_t(xu[0], dt), _t(w[0], dt), fp[0])
-                build_weight_update(M, K, B, act, dt, DMA, 0.01, True)(wd[0], _t(e[0], dt), _t(xu[0], dt))
+                kp = build_prediction_error(M, K, B, act, dt, DMA)
+                kf = build_forward(M, K, B, act, dt, DMA)
+                kw = build_weight_update(M, K, B, act, dt, DMA, 0.01, True)
+                kp(_t(xu[0], dt), _t(w[0], dt), _t(xl[0], dt), ep[0], workspace=kp.new_workspace() if use_ws else None)
+                kf(_t(xu[0], dt), _t(w[0], dt), fp[0], workspace=kf.new_workspace() if use_ws else None)
+                kw(wd[0], _t(e[0], dt), _t(xu[0], dt), workspace=kw.new_workspace() if use_ws else None)
             else:
-                build_prediction_error_batched(M, K, B, G, act, dt, DMA)(_t(xu, dt), _t(w, dt), _t(xl, dt), ep)
-                build_weight_update_batched(M, K, B, G, act, dt, DMA, 0.01, True)(wd, _t(e, dt), _t(xu, dt))
-            res[mode] = (ep, wd) + ((fp,) if G == 1 else ())  # forward has no grouped form
+                kp = build_prediction_error_batched(M, K, B, G, act, dt, DMA)
+                kw = build_weight_update_batched(M, K, B, G, act, dt, DMA, 0.01, True)
+                kp(_t(xu, dt), _t(w, dt), _t(xl, dt), ep, workspace=kp.new_workspace() if use_ws else None)
+                kw(wd, _t(e, dt), _t(xu, dt), workspace=kw.new_workspace() if use_ws else None)
+            if use_ws and act != "identity":
+                assert kp.workspace_bytes == G * K * B * 2 and kw.workspace_bytes == G * K * B * 2
+            res[use_ws] = (ep, wd) + ((fp,) if G == 1 else ())  # forward has no grouped form
         torch.cuda.synchronize()
     finally:
         _preact(-1)
-    for a, b in zip(res[0], res[1]):
+    for a, b in zip(res[False], res[True]):
         assert torch.equal(a, b)
 
 
-def test_preactivation_is_skipped_under_graph_capture():
-    """A captured standalone call keeps the register path (no pool allocation
-    inside the capture); its replays match the direct call bit for bit."""
+def test_preactivation_into_a_caller_workspace_under_graph_capture():
+    """A captured standalone call with a caller workspace records its
+    activation launch and its GEMM (nothing is allocated, so nothing keeps it
+    out of the graph); its replays match the direct call bit for bit."""
     report("dma16-preact-graph")
     dt = torch.bfloat16
-    M, K, B = 1024, 128, 256
+    M, K, B = 1024, 1024, 1024
     g = gen(17)
     xu, w, xl = _t(randn((K, B), g), dt), _t(randn((M, K), g, 1 / math.sqrt(K)), dt), _t(randn((M, B), g), dt)
     fn = build_prediction_error(M, K, B, "tanh", dt, DMA)
+    assert fn.workspace_bytes == K * B * 2  # the automatic rule pre-activates this call
+    ws = fn.new_workspace()
     direct = torch.empty((M, B), device=DEV, dtype=dt)
+    loader = torch.empty((M, B), device=DEV, dtype=dt)
     captured = torch.empty((M, B), device=DEV, dtype=dt)
-    try:
-        _preact(1)
-        fn(xu, w, xl, direct)
+    fn(xu, w, xl, direct, workspace=ws)
+    fn(xu, w, xl, loader)
+    torch.cuda.synchronize()
+    assert torch.equal(direct, loader)
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn(xu, w, xl, captured, workspace=ws)  # warm-up outside the capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        fn(xu, w, xl, captured, workspace=ws)
+    for _ in range(3):
+        captured.zero_()
+        ws.zero_()
+        graph.replay()
         torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s):
-            fn(xu, w, xl, captured)  # warm-up outside the capture
-        torch.cuda.current_stream().wait_stream(s)
-        torch.cuda.synchronize()
-        with torch.cuda.graph(graph):
-            fn(xu, w, xl, captured)
-        for _ in range(3):
-            captured.zero_()
-            graph.replay()
-            torch.cuda.synchronize()
-            assert torch.equal(captured, direct)
-    finally:
-        _preact(-1)
+        assert torch.equal(captured, direct)
+
+
+def test_default_standalone_calls_allocate_no_device_memory():
+    """The standalone calls without a workspace take the loader path at every
+    C5 shape and size: the device's free memory is the same before and after
+    them (a call that allocated, even from a pool it keeps, would lower it by
+    at least its K * B * 2-byte operand)."""
+    report("dma16-noalloc")
+    dt = torch.bfloat16
+    g = gen(23)
+    shapes = [(256, 256), (1024, 8192), (4096, 2048), (8192, 2048)]
+    tensors = {}
+    for n, B in shapes:
+        tensors[(n, B)] = (_t(randn((n, B), g), dt), _t(randn((n, n), g, 1 / math.sqrt(n)), dt),
+                           _t(randn((n, B), g), dt), torch.empty((n, B), device=DEV, dtype=dt),
+                           _t(randn((n, n), g, 1 / math.sqrt(n)), dt))
+
+    def calls(n, B):
+        xu, w, xl, e, wk = tensors[(n, B)]
+        for act in ("tanh", "relu"):
+            kp = build_prediction_error(n, n, B, act, dt, DMA)
+            assert n < 1024 or kp.workspace_bytes > 0 or act == "relu"  # would pre-activate given a workspace
+            kp(xu, w, xl, e)
+            build_forward(n, n, B, act, dt, DMA)(xu, w, e)
+            build_weight_update(n, n, B, act, dt, DMA, 1e-4, True)(wk, xl, xu)
+
+    # the same kernels once at a small size first: the runtime's first launch
+    # of a kernel may set up its code object and private-segment memory
+    calls(256, 256)
+    torch.cuda.synchronize()
+    free0, _total = torch.cuda.mem_get_info(DEV)
+    for n, B in shapes[1:]:
+        calls(n, B)
+    torch.cuda.synchronize()
+    free1, _total = torch.cuda.mem_get_info(DEV)
+    print(f"free device memory before {free0} after {free1}", flush=True)
+    assert free1 == free0

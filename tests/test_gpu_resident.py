@@ -20,7 +20,7 @@ import torch
 
 from lich_amd.trainer import HipIPC, IPCConfig
 from oracle import ipc_oracle as O
-from tests.helpers import DEV, report
+from tests.helpers import DEV, delta_w_check, report
 
 pytestmark = pytest.mark.gpu
 
@@ -301,8 +301,10 @@ def test_fp32_resident_matches_oracle(dims, B, wmode):
     x_t, w_t, _e = O.run_steps(x, w0, T, act=act, alpha=1e-4, gamma=0.5)
     s_err = O.global_rel_err(m.x, x_t)
     w_err = O.global_rel_err(m.w, w_t)
-    print(f"resident fp32 {dims} B={B} {wmode}: state_err={s_err:.3e} w_err={w_err:.3e}")
+    ok, msg = delta_w_check(m.w, w0, w_t, x, T, act=act, alpha=1e-4, gamma=0.5)
+    print(f"resident fp32 {dims} B={B} {wmode}: state_err={s_err:.3e} w_err={w_err:.3e} {msg}")
     assert s_err <= 1e-5 and w_err <= 1e-5
+    assert ok, msg
 
 
 def test_fp32_resident_forward_init_leaves_errors_exactly_zero():

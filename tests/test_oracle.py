@@ -258,3 +258,86 @@ def test_global_rel_err_never_reads_nan_as_agreement():
     assert O.global_rel_err(a, b) == float("inf")
     assert O.global_rel_err(b, a) == float("inf")
     assert O.global_rel_err(b, b) == 0.0
+
+
+@pytest.mark.parametrize("act", ACTS)
+@pytest.mark.parametrize("T", [1, 3])
+def test_run_steps_matches_brute_force_loops(act, T):
+    """``run_steps`` (the T-step driver every whole-step GPU test compares
+    with) against ``brute.step`` looped T times: a driver that skipped the
+    last step, fed back the pre-update W or x, or returned the first step's
+    errors instead of the last fails this."""
+    xs, ws = _tiny(act, seed=40 + T, dims=(3, 4, 5, 6), B=2)
+    gx, gw, ge = O.run_steps(xs, ws, T, act=act, alpha=0.07, gamma=0.4)
+    bx, bw = [_to_list(v) for v in xs], [_to_list(v) for v in ws]
+    be = None
+    for _ in range(T):
+        bx, bw, be = brute.step(bx, bw, act, 0.07, 0.4)
+    assert max(_tol(a, b) for a, b in zip(gx, bx)) < 1e-12
+    assert max(_tol(a, b) for a, b in zip(gw, bw)) < 1e-12
+    assert max(_tol(a, b) for a, b in zip(ge, be)) < 1e-12
+    # the inputs are not modified in place
+    xs2, ws2 = _tiny(act, seed=40 + T, dims=(3, 4, 5, 6), B=2)
+    assert all(torch.equal(a, b) for a, b in zip(xs, xs2)) and all(torch.equal(a, b) for a, b in zip(ws, ws2))
+
+
+def test_run_steps_zero_steps_is_the_identity():
+    xs, ws = _tiny("tanh", seed=9)
+    gx, gw, ge = O.run_steps(xs, ws, 0, act="tanh", alpha=0.1, gamma=0.5)
+    assert ge is None
+    assert all(torch.equal(a, b) for a, b in zip(gx, xs)) and all(torch.equal(a, b) for a, b in zip(gw, ws))
+
+
+@pytest.mark.parametrize("act", ["tanh", "relu"])
+def test_step_metrics_and_frozen_weights_match_loops(act):
+    """``reference.py:58``: energy = sum over l < L of mean(eps[l]^2) and the
+    largest |eps| over the same layers; ``update_weights=False`` still updates
+    the states and leaves every W untouched (``reference.py:52``)."""
+    xs, ws = _tiny(act, seed=17)
+    nx, nw, _e, m = O.ipc_step(xs, ws, act=act, alpha=0.05, gamma=0.3, update_weights=False)
+    bx, _bw, be = brute.step([_to_list(v) for v in xs], [_to_list(v) for v in ws], act, 0.05, 0.3)
+    energy = sum(sum(v * v for row in el for v in row) / (len(el) * len(el[0])) for el in be)
+    biggest = max(abs(v) for el in be for row in el for v in row)
+    assert abs(m["energy"] - energy) < 1e-12 and abs(m["max_abs_error"] - biggest) < 1e-12
+    assert all(torch.equal(a, b) for a, b in zip(nw, ws))
+    assert max(_tol(a, b) for a, b in zip(nx, bx)) < 1e-12
+
+
+def test_operand_emulation_reduces_to_the_oracle_at_fp32():
+    """``oracle/emulate.py`` with fp32 operands rounds nothing and its lo
+    terms are exactly zero, so every split gives the oracle's step, forward
+    initialisation and T-step run (in float32 arithmetic, the same order of
+    operations: bit for bit)."""
+    from oracle import emulate as E
+
+    dims = (10, 16, 16, 40)
+    ws = O.init_weights(dims, seed=5, init="xavier_uniform")
+    x_in, _lab, y = O.make_batch(dims, 6, seed=5)
+    x0 = O.forward_init(x_in, y, ws, "tanh")
+    for split in (1, 2, 3):
+        xe = E.forward_init_operand16(x_in, y, ws, act="tanh", op=torch.float32, split=split)
+        assert all(torch.equal(a, b) for a, b in zip(xe[1:], x0[1:]))
+        sx, sw, se = E.step_operand16(x0, ws, act="tanh", alpha=1e-2, gamma=0.5, op=torch.float32, split=split)
+        ox, ow, oe, _m = O.ipc_step(x0, ws, act="tanh", alpha=1e-2, gamma=0.5)
+        assert all(torch.equal(a, b) for a, b in zip(sx, ox))
+        assert all(torch.equal(a, b) for a, b in zip(sw, ow))
+        assert all(torch.equal(a, b) for a, b in zip(se, oe))
+    rx, rw = E.run(E.step_operand16, x0, ws, 3, act="tanh", alpha=1e-2, gamma=0.5, op=torch.float32)
+    ox, ow, _oe = O.run_steps(x0, ws, 3, act="tanh", alpha=1e-2, gamma=0.5)
+    assert all(torch.equal(a, b) for a, b in zip(rx, ox)) and all(torch.equal(a, b) for a, b in zip(rw, ow))
+    # and with 16-bit operands it does round: the emulation is not the oracle there
+    bx, _bw, _be = E.step_operand16(x0, ws, act="tanh", alpha=1e-2, gamma=0.5, op=torch.bfloat16)
+    assert not all(torch.equal(a, b) for a, b in zip(bx[1:-1], ox[1:-1]))
+
+
+def test_every_oracle_function_is_exercised():
+    """Each public function of ``oracle/ipc_oracle.py`` is called by a test in
+    this file, so no oracle function is left without a pin."""
+    import inspect
+    from pathlib import Path
+
+    src = Path(__file__).read_text()
+    names = [n for n, f in inspect.getmembers(O, inspect.isfunction)
+             if f.__module__ == O.__name__ and not n.startswith("_")]
+    missing = [n for n in names if f"O.{n}(" not in src]
+    assert not missing, missing

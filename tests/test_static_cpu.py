@@ -98,3 +98,15 @@ def test_only_the_cli_uses_the_cpu_reference_api():
             continue
         text = path.read_text()
         assert "from .reference" not in text and "lich_amd.reference" not in text, path
+
+
+@pytest.mark.parametrize("path", NATIVE_FILES, ids=lambda p: str(p.relative_to(ROOT)))
+def test_native_sources_allocate_no_device_memory(path):
+    """The library allocates nothing: every buffer comes from the caller (plan
+    workspaces, the standalone calls' optional workspace) or is the static
+    scratch of the no-allocation entry point.  No allocating HIP routine, pool
+    or host-pinning call appears in any native source."""
+    code = _strip_c_comments(path.read_text())
+    for token in ("hipMalloc", "hipFree", "hipMemPool", "hipExtMalloc", "hipHostMalloc", "hipHostRegister",
+                  "hipMallocManaged", "hipMemCreate", "hipMemAddressReserve"):
+        assert token not in code, f"{path.name}: {token}"

@@ -114,3 +114,38 @@ def test_gridz_lookup_rules(tmp_path):
     bad.write_text(json.dumps({"entries": []}))
     with pytest.raises(ValueError):
         GZ.lookup_grid_z_cap(bad, dims=d4, dtype="float16", **RTX)
+
+
+def test_table_reader_names_the_bad_row(tmp_path):
+    p = tmp_path / "t.json"
+    good = {"kind": "weight", "shape": {"M": 64, "K": 64, "B": 128}, "config": {"tile": 1}}
+    for bad, needle in (({"kind": "weight", "config": {}}, "entry 1 lacks shape"),
+                        ({"kind": "weight", "shape": {"M": 64, "K": "x", "B": 1}, "config": {}}, "entry 1 has no integer"),
+                        ([1, 2], "entry 1 is a list")):
+        p.write_text(json.dumps({"schema_version": 1, "entries": [good, bad]}))
+        with pytest.raises(ValueError, match=needle):
+            TU.TuningTable.from_json(p)
+    # duplicates: the first matching entry wins, as a linear scan would give
+    dup = dict(good, config={"tile": 2})
+    p.write_text(json.dumps({"schema_version": 1, "entries": [good, dup]}))
+    t = TU.TuningTable.from_json(p)
+    assert t.lookup(kind="weight", M=64, K=64, B=128, activation="relu", dtype="float16").tile == 1
+    p.write_text(json.dumps([good]))
+    with pytest.raises(ValueError, match="JSON object"):
+        TU.TuningTable.from_json(p)
+
+
+def test_small_b_policy_skips_unusable_rows(tmp_path):
+    from lich_amd.weight_update_specialization import SmallBWeightPolicy
+
+    p = tmp_path / "p.json"
+    rows = [{"M": 64, "K": 64, "B": 4, "backend": "outer", "activation": "tanh", "dtype": "float32"},
+            {"M": 64, "K": 64, "B": 8, "backend": "cublas"}, {"K": 64, "B": 8}, "row", {"M": "a", "K": 1, "B": 1}]
+    p.write_text(json.dumps({"entries": rows}))
+    pol = SmallBWeightPolicy(p)
+    assert len(pol.entries) == 1
+    assert pol.backend(M=64, K=64, B=4, activation="tanh", dtype="torch.float32") == "outer"
+    assert pol.backend(M=64, K=64, B=8, activation="relu", dtype="float16") == "gemm"
+    p.write_text(json.dumps(rows))
+    with pytest.raises(ValueError, match="JSON object"):
+        SmallBWeightPolicy(p)

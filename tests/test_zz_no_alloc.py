@@ -69,3 +69,39 @@ def test_noalloc_refuses_what_it_cannot_run():
     ws = [torch.zeros((a, b), device=DEV) for a, b in zip(dims[:-1], dims[1:])]
     rc = _noalloc(dims, 4096, t, t, ws, nat.DT_F16, 3, nat.act_code("tanh"), 0, 1)
     assert rc == nat.ERR_SHAPE and "scratch" in nat.last_error()
+
+
+@pytest.mark.parametrize("dims,dtype,B", [(D6, torch.float16, 128), ((10, 64, 64, 64, 784), torch.float32, 128)])
+def test_noalloc_timeout_is_reported_until_checked(dims, dtype, B):
+    """A spin limit of 0 (set from the host) makes every wait give up at its
+    first unsatisfied poll; the kernels still run to their end.  The timeout
+    word stays set across later calls until ipc_noalloc_check reports it, and
+    calls at the default limit then check clean and match the plan path."""
+    lib = nat.lib()
+    report("noalloc-timeout", dims=len(dims) - 1, dtype=str(dtype), B=B)
+    w0 = O.init_weights(dims, seed=5, init="xavier_uniform")
+    x_in, _l, y = O.make_batch(dims, B, seed=5)
+    m = HipIPC(IPCConfig(dims=dims, activation="tanh", dtype=dtype, hierarchical_policy_auto=False), device=DEV,
+               weights=w0)
+    m.initialize_batch(x_in.to(DEV), y.to(DEV))
+    x_init = [t.clone() for t in m.x]
+    stream = nat.current_stream_handle(DEV)
+    assert lib.ipc_noalloc_check(stream) in (nat.IPC_OK, nat.ERR_TIMEOUT)  # a clean start
+    args = (nat.dtype_code(dtype), m.pred_split, nat.act_code("tanh"), nat.WMODE["gemm"])
+    xs, es, ws = [t.clone() for t in m.x], [t.clone() for t in m.e], [t.clone() for t in m.w]
+    try:
+        lib.ipc_noalloc_set_spin_limit(0)
+        nat.check(_noalloc(dims, B, xs, es, ws, *args, T))
+        lib.ipc_noalloc_set_spin_limit(-1)
+        nat.check(_noalloc(dims, B, xs, es, ws, *args, 1))  # a later call does not erase the report
+        assert lib.ipc_noalloc_check(stream) == nat.ERR_TIMEOUT and "spin limit" in nat.last_error()
+        assert lib.ipc_noalloc_check(stream) == nat.IPC_OK
+    finally:
+        lib.ipc_noalloc_set_spin_limit(-1)
+    xs, es, ws = [t.clone() for t in x_init], [t.clone() for t in m.e], [w.to(DEV).clone() for w in w0]
+    nat.check(_noalloc(dims, B, xs, es, ws, *args, T))
+    assert lib.ipc_noalloc_check(stream) == nat.IPC_OK
+    m.run_steps(T)
+    m.check_steps()
+    for a, b in zip(m.x + m.w, xs + ws):
+        assert torch.equal(a, b)
