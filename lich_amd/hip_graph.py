@@ -47,5 +47,8 @@ class IPCGraphRunner:
         if (self._plan is None or plan is None or plan.value != self._plan.value
                 or self._generation != getattr(self.model, "_graph_generation", None)):
             raise RuntimeError("Graph has not been captured (or was discarded by a later capture or a new plan)")
+        # writes of x / W counted by torch since the last launch: re-sync the
+        # plan's operand copies and caches first (outside the graph)
+        self.model._sync_if_written()
         # the library refuses a plan whose graph a rebind discarded (IPC_ERR_STATE)
         nat.check(nat.lib().ipc_plan_graph_launch(plan, int(repeats), nat.current_stream_handle(self.model.device)))

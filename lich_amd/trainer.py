@@ -180,6 +180,8 @@ class HipIPC:
         self.a: list[torch.Tensor | None] | None = None
         self._plan = None
         self._plan_key = None
+        self._caches_operands = False  # the bound plan keeps operand copies or caches between launches
+        self._synced_versions = None   # torch version counters of x[1..L] and W when last in sync
         self._steady_state_runner = None
         self._steady_state_graph_steps: int | None = None
         self._steady_state_graph_key = None
@@ -330,6 +332,8 @@ class HipIPC:
         ws = None if self._workspace is None else self._workspace.data_ptr()
         nat.check(nat.lib().ipc_plan_bind(handle, _ptr_array(self.x), _ptr_array(self.e), _ptr_array(self.w), a, ws))
         self._plan_key = (int(B), tuple(t.data_ptr() for t in self.w))
+        self._caches_operands = self.path in ("resident", "wide")
+        self._synced_versions = None
 
     def runtime_plan_ready(self) -> bool:
         return self._plan is not None
@@ -356,9 +360,32 @@ class HipIPC:
         wide path's 16-bit operand copies, marks the operands the
         layer-resident path caches between launches stale (f(x[L]) copies,
         f(x) of the hidden states, the top layer's next first-step partial
-        products); a no-op for the other paths."""
+        products); a no-op for the other paths.
+
+        Writes through torch (``copy_``, in-place ops, views of ``x[l]`` or
+        ``w[l]``) are detected by their version counters before the next
+        launch and need no call; writes torch does not count (through
+        ``.data``, ``data_ptr()`` or another library) do."""
         if self._plan is not None:
             nat.check(nat.lib().ipc_plan_sync(self._plan, nat.current_stream_handle(self.device)))
+            self._mark_synced()
+
+    def _tracked_versions(self) -> tuple:
+        # x[0] (the target) is read directly by every launch and never cached
+        return tuple(t._version for t in self.x[1:]) + tuple(t._version for t in self.w)
+
+    def _mark_synced(self) -> None:
+        if self._caches_operands and self.x is not None:
+            self._synced_versions = self._tracked_versions()
+
+    def _sync_if_written(self) -> None:
+        """The reference re-reads x and W at every launch (trainer.py:601-679),
+        so a caller may write them in place between steps (trainer.py:798-817).
+        The resident and wide paths keep copies and caches of them between
+        launches: if torch has counted a write to x[1..L] or W since the
+        library last made them consistent, re-sync before launching."""
+        if self._caches_operands and self._tracked_versions() != self._synced_versions:
+            self.sync_operand_copies()
 
     def barrier_timeouts(self) -> int:
         """Non-zero if a wait of a whole-step kernel hit its spin limit since
@@ -403,14 +430,18 @@ class HipIPC:
         if self._plan is None:
             self._build_plan(B)
         self.x[-1].copy_(x_input)
+        # the forward initialisation re-derives every cached operand (wide
+        # copies of W and f(x); a column-kernel launch makes the resident caches stale)
         nat.check(nat.lib().ipc_plan_forward_init(self._plan, nat.current_stream_handle(self.device)))
         self.x[0].copy_(y_target)
+        self._mark_synced()
 
     # ------------------------------------------------------------------ step
     @torch.no_grad()
     def step_initialized(self, *, collect_metrics: bool = False) -> dict[str, float]:
         if self.x is None or self._plan is None:
             raise RuntimeError("Call initialize_batch before step_initialized")
+        self._sync_if_written()
         nat.check(nat.lib().ipc_plan_step(self._plan, 1, nat.current_stream_handle(self.device)))
         if collect_metrics:
             return self.metrics()
@@ -431,6 +462,7 @@ class HipIPC:
         """Enqueue ``steps`` steps with one library call (no Python loop)."""
         if self._plan is None:
             raise RuntimeError("Call initialize_batch first")
+        self._sync_if_written()
         nat.check(nat.lib().ipc_plan_step(self._plan, int(steps), nat.current_stream_handle(self.device)))
 
     # ------------------------------------------------------------------ steady state / graph
@@ -525,6 +557,7 @@ class HipIPC:
                 dst.copy_(src)
         if ws_backup is not None:
             self._workspace.copy_(ws_backup)
+        self._mark_synced()  # the workspace's copies and caches are restored with the buffers
         torch.cuda.synchronize(self.device)
 
     def capture_graph(self, steps: int):

@@ -323,3 +323,75 @@ def test_fp32_resident_forward_init_leaves_errors_exactly_zero():
     for l in range(len(w0)):
         nz = torch.count_nonzero(m.w[l].cpu() - w0[l])
         assert (nz == 0) if l >= T else (nz > 0), l
+
+
+def test_torch_writes_between_launches_need_no_sync_call():
+    """The reference re-reads x and W at every launch, so its callers write
+    them in place between steps (trainer.py:798-817).  Writes torch counts
+    (copy_, in-place ops, views) of W, the input x[L] and a hidden state,
+    between launches and before a graph replay, with no sync_operand_copies
+    call: the resident plan (which caches operands across launches) stays bit
+    for bit equal to the column kernel (which caches nothing)."""
+    dims, B = (10,) + (64,) * 4 + (784,), 96
+    report("resident-torch-writes", dims=dims, B=B)
+    w0 = O.init_weights(dims, seed=31, init="xavier_uniform")
+    x_in, _l, y = O.make_batch(dims, B, seed=31)
+    g = torch.Generator().manual_seed(32)
+    x_in2 = torch.rand((dims[-1], B), generator=g)
+    x2 = torch.rand((dims[2], B), generator=g) - 0.5
+    ms = [_model(dims, w0, "tanh", F16, path) for path in ("resident", "narrow")]
+    for m in ms:
+        m.initialize_batch(x_in.to(DEV), y.to(DEV))
+        m.run_steps(4)
+        m.run_steps(2)                          # warm: caches in use
+        m.w[1].mul_(1.01)                       # weights loaded in place
+        m.run_steps(3)
+        m.x[-1].copy_(x_in2.to(DEV))            # a new input without initialize_batch
+        m.run_steps(2)
+        m.x[2][:, :8].copy_(x2[:, :8].to(DEV))  # a write through a view of a hidden state
+        m.w[len(w0) - 1].add_(1e-3)             # the top layer's weights (its first-step partials are cached)
+        m.run_steps(1)
+        runner = m.capture_graph(2)
+        m.w[0].mul_(0.99)
+        runner.replay(2)
+    torch.cuda.synchronize()
+    res, col = ms
+    assert [res.path, col.path] == ["resident", "narrow"]
+    for name, a, b in (("x", res.x, col.x), ("e", res.e[:-1], col.e[:-1]), ("w", res.w, col.w)):
+        for l, (u, v) in enumerate(zip(a, b)):
+            assert torch.equal(u, v), (name, l, float((u - v).abs().max()))
+    assert res.barrier_timeouts() == 0
+
+
+def test_rebinding_a_warm_resident_plan_starts_cold():
+    """ipc_plan_bind of a plan whose workspace holds warm caches of other
+    buffers (f(x[L]) images, hidden f(x), next first-step partials): the
+    rebound plan's steps equal a fresh plan's bit for bit."""
+    from lich_amd import _native as nat
+    from lich_amd.trainer import _ptr_array
+
+    dims, B = (10,) + (64,) * 4 + (784,), 96
+    report("resident-rebind", dims=dims, B=B)
+    nets = []
+    for seed in (41, 42, 42):
+        w0 = O.init_weights(dims, seed=seed, init="xavier_uniform")
+        x_in, _l, y = O.make_batch(dims, B, seed=seed)
+        m = _model(dims, w0, "tanh", F16, "resident")
+        m.initialize_batch(x_in.to(DEV), y.to(DEV))
+        nets.append(m)
+    a, b, fresh = nets
+    assert a.path == b.path == fresh.path == "resident"
+    stream = nat.current_stream_handle(DEV)
+    a.run_steps(4)
+    a.run_steps(2)  # a's workspace now holds warm caches of a's buffers
+    nat.check(nat.lib().ipc_plan_bind(a._plan, _ptr_array(b.x), _ptr_array(b.e), _ptr_array(b.w), None,
+                                      a._workspace.data_ptr()))
+    nat.check(nat.lib().ipc_plan_step(a._plan, 4, stream))
+    nat.check(nat.lib().ipc_plan_step(a._plan, 2, stream))
+    fresh.run_steps(4)
+    fresh.run_steps(2)
+    nat.check(nat.lib().ipc_plan_check(a._plan, stream))
+    torch.cuda.synchronize()
+    for name, u_list, v_list in (("x", b.x, fresh.x), ("e", b.e[:-1], fresh.e[:-1]), ("w", b.w, fresh.w)):
+        for l, (u, v) in enumerate(zip(u_list, v_list)):
+            assert torch.equal(u, v), (name, l, float((u - v).abs().max()))

@@ -193,3 +193,37 @@ def test_wide_sync_after_external_weight_write():
     wd, ph = models["wide"], models["phased"]
     assert O.global_rel_err(wd.x[1:-1], ph.x[1:-1]) <= 1e-5
     assert O.global_rel_err(wd.w, ph.w) <= 1e-5
+
+
+def test_wide_torch_writes_need_no_sync_call():
+    """Writes of W and x that torch counts re-derive the wide path's operand
+    copies before the next launch by themselves: the same edits with and
+    without sync_operand_copies() give the same bits, and the phased path
+    (no copies) agrees to the fp32 bar."""
+    dims, B, T = (10, 300, 200, 784), 128, 2
+    report("wide-torch-writes", dims=dims, B=B)
+    w0, x_in, y = _setup(dims, B, seed=19)
+    x_in2 = torch.randn((dims[-1], B), generator=torch.Generator().manual_seed(20))
+    models = {}
+    for name, path, explicit in (("auto", "wide", False), ("explicit", "wide", True), ("phased", "phased", False)):
+        m = HipIPC(IPCConfig(dims=dims, activation="tanh", dtype=BF16, fused=path), device=DEV, weights=w0)
+        m.initialize_batch(x_in.to(DEV), y.to(DEV))
+        m.run_steps(T)
+        m.w[1].mul_(1.01)
+        m.x[2].add_(0.01)
+        if explicit:
+            m.sync_operand_copies()
+        m.run_steps(T)
+        m.x[-1].copy_(x_in2.to(DEV))
+        m.w[0][:16].mul_(0.5)
+        if explicit:
+            m.sync_operand_copies()
+        m.run_steps(T)
+        models[name] = m
+    torch.cuda.synchronize()
+    au, ex, ph = models["auto"], models["explicit"], models["phased"]
+    assert au.path == ex.path == "wide"
+    for u, v in zip(au.x + au.w + au.e[:-1], ex.x + ex.w + ex.e[:-1]):
+        assert torch.equal(u, v)
+    assert O.global_rel_err(au.x[1:-1], ph.x[1:-1]) <= 1e-5
+    assert O.global_rel_err(au.w, ph.w) <= 1e-5
