@@ -509,6 +509,7 @@ def main() -> int:
                                           f"(d_0+d_L) B) x {T if pmodel.fused else 1} steps per launch",
                 "avg_launch_us": round(launch_us, 3),
                 "achieved_tflops": round(launch_flops / (launch_us * 1e-6) / 1e12, 4)}
+    pmodel_fused = pmodel.fused
     del pmodel
 
     model, x, y = make_model(dims, B, "tanh", torch.float16, seed=0)
@@ -541,7 +542,13 @@ def main() -> int:
                                "T=4 steps per replay of the captured steps (one whole-step kernel launch), fp32 master x/eps/W, "
                                "fp16 operands, fp32 accumulate",
                    "global_batch": B, "seq_len": None, "parallelism": "single GPU",
-                   "fused_whole_step_kernel": model.fused, "path": model.path, "phases": phases},
+                   "fused_whole_step_kernel": model.fused, "path": model.path, "phases": phases,
+                   "replay_forms": {
+                       "direct_relaunch_us_per_step": round(ms_per_step * 1e3, 4),
+                       "hipgraph_replay_us_per_step": round(launch_us / T, 4) if pmodel_fused else None,
+                       "note": "headline: the captured T steps replayed by relaunching their one whole-step "
+                               "launch; hipgraph: the same launch recorded 50 times into a torch.cuda.graph, "
+                               "HIP events around its replays"}},
         "roofline": roofline, "cpu_baseline": cpu, "wide": wide, "small_batch": small,
     }
     print(json.dumps(line), flush=True)

@@ -60,19 +60,24 @@ extern "C" {
 #define IPC_ACT_GELU 5
 
 /* tile configurations of the MFMA GEMM family; IPC_TILE_AUTO picks by shape.
- * IPC_TILE_DMA_256x128 is the LDS-DMA kernel (256 x 128 tiles, 4 waves of
- * 128 x 64, operands streamed HBM -> LDS without VGPR staging, transposed
- * operands read with the LDS transpose read).  It serves 16-bit storage
- * (storage == operand == fp16/bf16) with a contraction that is a multiple of
- * 64, 16-byte aligned tensors and, for operands read transposed, a contiguous
- * extent that is a multiple of 8; IPC_TILE_AUTO picks it whenever those hold,
- * and asking for it otherwise is IPC_ERR_CONFIG. */
+ * IPC_TILE_DMA_* are the LDS-DMA kernel (operands streamed HBM -> LDS without
+ * VGPR staging, transposed operands read with the LDS transpose read) in
+ * three tile configurations: 256 x 128 (the automatic choice), 128 x 256 and
+ * 128 x 128 (more tiles for small shapes).  They give bit-identical results
+ * (the same k order) and serve 16-bit storage (storage == operand ==
+ * fp16/bf16) with a contraction that is a multiple of 64, 16-byte aligned
+ * tensors and, for operands read transposed, a contiguous extent that is a
+ * multiple of 8; IPC_TILE_AUTO picks the 256 x 128 one whenever those hold,
+ * and asking for a DMA tile otherwise is IPC_ERR_CONFIG.  The autotuner
+ * searches all of them per shape. */
 #define IPC_TILE_AUTO (-1)
 #define IPC_TILE_32x32 0
 #define IPC_TILE_64x64 1
 #define IPC_TILE_128x128 2
 #define IPC_TILE_DMA_256x128 3
-#define IPC_TILE_COUNT 4
+#define IPC_TILE_DMA_128x256 4
+#define IPC_TILE_DMA_128x128 5
+#define IPC_TILE_COUNT 6
 
 /* weight-update backends of a plan */
 #define IPC_WMODE_GEMM 0
@@ -285,6 +290,20 @@ int ipc_plan_set_tiles(ipc_plan* plan, int tile_pred, int tile_infer, int tile_w
  * net cannot take fails at bind with IPC_ERR_CONFIG. */
 int ipc_plan_wide_config_count(int phase, int split);
 int ipc_plan_set_wide_config(ipc_plan* plan, int pred_cfg, int infer_cfg, int weight_cfg, int ksplit);
+
+/* Row-block size of a layer-resident plan (the tuning surface of
+ * IPC_PATH_RESIDENT plans): the top layer W[L-1] is cut into blocks of
+ * `rows` rows (16, 32 or 64; -1 = the default 32) times column chunks of 128,
+ * one workgroup each; smaller blocks give more, shorter top workgroups.
+ * Results are bit-identical for every size (each block adds its chunks'
+ * partial products in chunk order).  Called after ipc_plan_create and before
+ * ipc_plan_workspace_bytes / ipc_plan_bind (the size sets the workspace);
+ * IPC_ERR_CONFIG when the plan is not layer-resident or the net's blocks of
+ * that size do not fit the LDS, the flag area or the device's co-resident
+ * capacity (the plan is then unchanged).  ipc_plan_resident_rows reports the
+ * current size (0 for other plans). */
+int ipc_plan_set_resident_rows(ipc_plan* plan, int rows);
+int ipc_plan_resident_rows(const ipc_plan* plan);
 
 /* Kernel launches one ipc_plan_step(steps=1) enqueues. */
 int ipc_plan_launch_count(const ipc_plan* plan);

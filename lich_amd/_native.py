@@ -24,7 +24,8 @@ DT_F32, DT_F16, DT_BF16 = 0, 1, 2
 ACT_CODES = {"identity": 0, "linear": 0, "relu": 1, "tanh": 2, "sigmoid": 3, "silu": 4, "gelu": 5}
 TILE_AUTO = -1
 TILE_DMA = 3
-TILE_COUNT = 4
+TILE_DMA_TILES = (3, 4, 5)  # LDS-DMA kernel: 256 x 128, 128 x 256, 128 x 128
+TILE_COUNT = 6
 WMODE = {"gemm": 0, "outer": 1, "auto": 2}
 SPLIT_NONE, SPLIT_W, SPLIT_WX = 1, 2, 3
 PATH_AUTO, PATH_PHASED, PATH_NARROW, PATH_WIDE, PATH_RESIDENT = -1, 0, 1, 2, 3
@@ -95,6 +96,8 @@ def _declare(lib):
         "ipc_plan_set_spin_limit": ([vp, i], i),
         "ipc_plan_wide_config_count": ([i, i], i),
         "ipc_plan_set_wide_config": ([vp, i, i, i, i], i),
+        "ipc_plan_set_resident_rows": ([vp, i], i),
+        "ipc_plan_resident_rows": ([vp], i),
         "ipc_set_coresident_limit": ([i], i),
         "ipc_set_s16_preactivate": ([i], i),
         "ipc_s16_preactivates": ([i, i, i, i, i], i),

@@ -23,9 +23,18 @@ this library's choices), every candidate gated on correctness.
   kernel table as a ``kernel_profiles`` entry, so ``HipIPC`` reads its
   choices through the reference's precedence.
 
+* Standalone kernels with 16-bit storage (the per-kernel sweep's operator
+  calls, ``tune_standalone``): the generic tiles and the three LDS-DMA tile
+  configurations (256x128, 128x256, 128x128) per (kind, M, K, B), under the
+  same probe.
+* Layer-resident plans: the top layer's row-block size (16, 32 or 64 rows,
+  ``ipc_plan_set_resident_rows``) is part of the execution search; every
+  execution candidate runs one step from the forward-initialised state and
+  must pass the probe on states, errors and weight deltas against a float32
+  torch step before it is timed.
+
 Candidates that fail the probe are never selected; they are recorded with
-the reason (``rejected``).  The layer-resident kernel's row-block size is a
-compile-time constant of its kernel and is not searched.
+the reason (``rejected``).
 
     python -m lich_amd.autotune --dims 10,64,64,64,784 --batch 128 --activation tanh \\
         --dtype float16 --table results/tuning_cdna4.json --policy results/hierarchical_policy.json
@@ -47,7 +56,8 @@ from .reference import get_activation
 from .trainer import HipIPC, IPCConfig, init_weights_cpu
 from .tuning import TuningEntry, TuningKey, TuningTable, config_to_dict
 
-TILES = (0, 1, 2, 3)
+TILES = (0, 1, 2, 3, 4, 5)  # generic 32x32, 64x64, 128x128; LDS-DMA 256x128, 128x256, 128x128
+RESIDENT_ROWS = (16, 32, 64)
 RTOL = ATOL = 2e-2
 MAX_BAD = 0.01
 
@@ -132,15 +142,16 @@ def _kernel_case(kind, M, K, B, activation, dtype, storage, cfg, g, dev):
 
 def tune_kernels(dims, B: int, activation: str, dtype: torch.dtype, *, reps: int = 20, replays: int = 3,
                  storage: torch.dtype = torch.float32, seed: int = 0, rejected: list | None = None,
-                 perturb=None, timer=None) -> TuningTable:
-    """Fastest passing tile per (kind, M, K).  ``perturb(kind, M, K, tile, out)``
-    (tests) may alter a candidate's output before the probe;
-    ``timer(kind, M, K, tile, us)`` may replace a measured time."""
+                 perturb=None, timer=None, shapes=None) -> TuningTable:
+    """Fastest passing tile per (kind, M, K) of the net (or of ``shapes``).
+    ``perturb(kind, M, K, tile, out)`` (tests) may alter a candidate's output
+    before the probe; ``timer(kind, M, K, tile, us)`` may replace a measured
+    time."""
     dev = torch.device("cuda", torch.cuda.current_device())
     g = torch.Generator().manual_seed(seed)
     dt = str(dtype).split(".")[-1]
     entries = []
-    for kind, M, K in net_shapes([int(d) for d in dims]):
+    for kind, M, K in (shapes if shapes is not None else net_shapes([int(d) for d in dims])):
         best = None
         for tile in TILES:
             cfg = KernelConfig(tile=tile)
@@ -165,6 +176,23 @@ def tune_kernels(dims, B: int, activation: str, dtype: torch.dtype, *, reps: int
                 best = (us, cfg)
         if best is not None:
             entries.append(TuningEntry(TuningKey(kind, M, K, B, activation, dt), best[1], best[0] / 1e3, False))
+    return TuningTable.from_entries(entries)
+
+
+def tune_standalone(points, activation: str, dtype: torch.dtype, *, reps: int = 5, replays: int = 3, seed: int = 0,
+                    rejected: list | None = None, perturb=None, timer=None) -> TuningTable:
+    """The operator calls with 16-bit storage (``dtype`` both storage and
+    operand type), as the per-kernel sweep makes them: for every (M, K, B) of
+    ``points`` the prediction, inference and weight kernels over every tile
+    (the three LDS-DMA configurations where the shape allows them), gated and
+    timed like ``tune_kernels``."""
+    entries = []
+    for M, K, B in points:
+        t = tune_kernels(None, int(B), activation, dtype, reps=reps, replays=replays, storage=dtype, seed=seed,
+                         rejected=rejected, perturb=perturb, timer=timer,
+                         shapes=[("prediction", int(M), int(K)), ("inference", int(M), int(K)),
+                                 ("weight", int(M), int(K))])
+        entries += list(t.entries)
     return TuningTable.from_entries(entries)
 
 
@@ -273,34 +301,64 @@ def nat_phase(name: str) -> int:
 
 
 def tune_execution(dims, B: int, activation: str, dtype: torch.dtype, *, steps: int = 4, replays: int = 50,
-                   seed: int = 0, wide_config=None) -> tuple[dict, list[dict]]:
-    """Best (path, recompute, graph) for one step, and every trial."""
+                   seed: int = 0, wide_config=None, rejected: list | None = None, perturb=None,
+                   timer=None) -> tuple[dict, list[dict]]:
+    """Best (path, recompute, graph, resident row blocks) for one step, and
+    every trial.  Each candidate first runs one step from the forward
+    initialisation and must pass the probe (states, errors, weight deltas)
+    against a float32 torch step; ``perturb(trial, model)`` (tests) may alter
+    its state before the probe, ``timer(trial, step_ms)`` replace a time."""
     dev = torch.device("cuda", torch.cuda.current_device())
     w0 = init_weights_cpu(dims, seed=seed, init="xavier_uniform")
     g = torch.Generator().manual_seed(seed + 7919)
     x_in = torch.rand((dims[-1], B), generator=g).to(dev)
     y = torch.nn.functional.one_hot(torch.randint(0, dims[0], (B,), generator=g), dims[0]).float().T.contiguous().to(dev)
+    act = get_activation(activation)
+    L = len(dims) - 1
     trials = []
     for path in ("resident", "narrow", "wide", "phased"):
-        for recompute in (True, False):
-            for graph in (True, False):
-                cfg = IPCConfig(dims=tuple(dims), activation=activation, dtype=dtype, fused=path,
-                                recompute_activation=recompute, hierarchical_policy_auto=False,
-                                wide_config=wide_config if path == "wide" else None)
-                try:
-                    m = HipIPC(cfg, device=dev, weights=w0)
+        for rows in (RESIDENT_ROWS if path == "resident" else (None,)):
+            for recompute in (True, False):
+                for graph in (True, False):
+                    trial = {"path": path, "recompute_activation": recompute, "use_cuda_graph": graph,
+                             "grid_z_max_layers": 1}
+                    if rows is not None:
+                        trial["resident_rows"] = rows
+                    cfg = IPCConfig(dims=tuple(dims), activation=activation, dtype=dtype, fused=path,
+                                    recompute_activation=recompute, hierarchical_policy_auto=False,
+                                    wide_config=wide_config if path == "wide" else None, resident_rows=rows)
+                    try:
+                        m = HipIPC(cfg, device=dev, weights=w0)
+                        m.initialize_batch(x_in, y)
+                    except (ValueError, nat.IPCNativeError):
+                        continue  # path (or row-block size) not eligible for this net
+                    x0 = [t.clone() for t in m.x]
+                    m.run_steps(1)
+                    m.check_steps()
+                    if perturb is not None:
+                        perturb(trial, m)
+                    ref_x, ref_e, ref_w = _torch_step(x0, [w.to(dev) for w in w0], act)
+                    fails = _probe_group("x", m.x[1:L], ref_x[1:L]) + _probe_group("eps", m.e[:L], ref_e) + \
+                        _probe_group("dW", [m.w[l] - w0[l].to(dev) for l in range(L)],
+                                     [rw - w.to(dev) for rw, w in zip(ref_w, w0)])
+                    if fails:
+                        if rejected is not None:
+                            rejected.append(dict(trial, reason="; ".join(fails)))
+                        del m
+                        continue
+                    for l, w in enumerate(w0):
+                        m.w[l].copy_(w.to(dev))
                     m.prepare_steady_state(x_in, y, steps=steps, use_graph=graph)
-                except (ValueError, nat.IPCNativeError):
-                    continue  # path not eligible for this net
-                m.run_prepared_steady_state(steps=steps, repeats=3, use_graph=graph)
-                t0 = time.perf_counter()
-                m.run_prepared_steady_state(steps=steps, repeats=replays, use_graph=graph)
-                dt = time.perf_counter() - t0
-                step_ms = dt * 1e3 / (steps * replays)
-                trials.append({"path": path, "recompute_activation": recompute, "use_cuda_graph": graph,
-                               "grid_z_max_layers": 1, "step_ms": step_ms, "samples_per_s": B / step_ms * 1e3,
-                               "status": "ok", "source": "gpu"})
-                del m
+                    m.run_prepared_steady_state(steps=steps, repeats=3, use_graph=graph)
+                    t0 = time.perf_counter()
+                    m.run_prepared_steady_state(steps=steps, repeats=replays, use_graph=graph)
+                    dt = time.perf_counter() - t0
+                    step_ms = dt * 1e3 / (steps * replays)
+                    if timer is not None:
+                        step_ms = timer(trial, step_ms)
+                    trials.append(dict(trial, step_ms=step_ms, samples_per_s=B / step_ms * 1e3, status="ok",
+                                       source="gpu"))
+                    del m
     best = min(trials, key=lambda t: t["step_ms"])
     return best, trials
 
@@ -349,16 +407,28 @@ def main(argv=None) -> int:
     ap.add_argument("--policy", default="results/hierarchical_policy.json")
     ap.add_argument("--steps", type=int, default=4)
     ap.add_argument("--no-kernels", action="store_true", help="skip the standalone kernel table")
+    ap.add_argument("--standalone", default="",
+                    help="semicolon-separated M,K,B points: tune the 16-bit-storage operator calls at those "
+                         "shapes (the per-kernel sweep) into --table, and nothing else")
     a = ap.parse_args(argv)
     dims = [int(v) for v in a.dims.split(",")]
     dtype = {"float16": torch.float16, "bfloat16": torch.bfloat16}[a.dtype]
     rejected: list = []
+    if a.standalone:
+        points = [tuple(int(v) for v in pt.split(",")) for pt in a.standalone.split(";") if pt]
+        table = tune_standalone(points, a.activation, dtype, rejected=rejected)
+        table.to_json(a.table, device=torch.cuda.get_device_name(0))
+        print(json.dumps({"table": a.table, "kernels": len(table.entries), "rejected": len(rejected),
+                          "tiles": {f"{e.key.kind} {e.key.M}x{e.key.K}x{e.key.B}": e.config.tile
+                                    for e in table.entries}}), flush=True)
+        return 0
     table = TuningTable.from_entries([]) if a.no_kernels else \
         tune_kernels(dims, a.batch, a.activation, dtype, rejected=rejected)
     table.to_json(a.table, device=torch.cuda.get_device_name(0))
     wide = tune_wide(dims, a.batch, a.activation, dtype, rejected=rejected)
     wide_tuple = None if wide is None else tuple(wide[k] for k in ("pred", "infer", "weight", "ksplit"))
-    best, trials = tune_execution(dims, a.batch, a.activation, dtype, steps=a.steps, wide_config=wide_tuple)
+    best, trials = tune_execution(dims, a.batch, a.activation, dtype, steps=a.steps, wide_config=wide_tuple,
+                                  rejected=rejected)
     write_policy(a.policy, dims, a.batch, a.activation, dtype, table, best, trials,
                  wide_config=wide, rejected=rejected)
     print(json.dumps({"table": a.table, "policy": a.policy, "kernels": len(table.entries), "wide": wide,

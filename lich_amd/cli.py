@@ -119,15 +119,25 @@ def reference_main(argv=None) -> int:
     p.add_argument("--steps", type=int, default=5)
     p.add_argument("--activation", default="relu")
     a = p.parse_args(argv)
+    # the script's random stream: one global seed, then the input, then the
+    # weights layer by layer from the same global generator
     torch.manual_seed(0)
     dims = (10,) + (a.hidden,) * a.depth + (28 * 28,)
-    cpu, f32 = torch.device("cpu"), torch.float32
+    f32 = torch.float32
     x_in = torch.randn((dims[-1], a.batch), dtype=f32)
     y = R.one_hot(torch.arange(a.batch) % 10, 10, dtype=f32)
-    st = R.initialize_state(x_in, y, dims, dtype=f32, device=cpu, seed=0)
+    w = []
+    for rows, cols in zip(dims[:-1], dims[1:]):
+        t = torch.empty((rows, cols), dtype=f32)
+        torch.nn.init.kaiming_uniform_(t, a=5 ** 0.5)
+        w.append(t)
     act = R.get_activation(a.activation)
-    for l in reversed(range(1, len(st.w))):  # forward initialisation of the hidden states
-        st.x[l] = st.w[l] @ act.forward(st.x[l + 1])
+    x = [torch.zeros((d, a.batch), dtype=f32) for d in dims]
+    x[-1].copy_(x_in)
+    for l in reversed(range(1, len(w))):  # forward initialisation of the hidden states
+        x[l].copy_(w[l] @ act.forward(x[l + 1]))
+    x[0].copy_(y)
+    st = R.ReferenceState(x=x, w=w)
     for i in range(a.steps):
         st, m = R.ipc_step(st, act=act, alpha=1e-4, gamma=0.5, fixed_low=y, fixed_high=x_in)
         print(i, float(m["energy"]), float(m["max_abs_error"]), flush=True)

@@ -203,14 +203,17 @@ bool dma_eligible(int storage, int contraction, std::initializer_list<const void
   return true;
 }
 
-// Tile selection of a standalone call: returns 1 if the LDS-DMA kernel runs
-// it, 0 for the generic kernel (tile resolved), or an error.
+// Tile selection of a standalone call: returns 1 + the LDS-DMA configuration
+// (0: 256 x 128, 1: 128 x 256, 2: 128 x 128) if that kernel runs it, 0 for
+// the generic kernel (tile resolved), or an error.
 int select_tile(int& tile, bool eligible, long long M, long long N, long long groups) {
-  if (tile == IPC_TILE_DMA_256x128 && !eligible)
+  const bool dma_tile = tile >= IPC_TILE_DMA_256x128;
+  if (dma_tile && !eligible)
     return fail(IPC_ERR_CONFIG,
                 "tile %d (LDS-DMA) needs 16-bit storage, a contraction that is a multiple of %d, 16-byte "
-                "aligned tensors and row lengths that are multiples of 8", IPC_TILE_DMA_256x128, WIDE_BK);
-  if (eligible && (tile == IPC_TILE_AUTO || tile == IPC_TILE_DMA_256x128)) return 1;
+                "aligned tensors and row lengths that are multiples of 8", tile, WIDE_BK);
+  if (eligible && tile == IPC_TILE_AUTO) return 1;
+  if (dma_tile) return 1 + tile - IPC_TILE_DMA_256x128;
   if (tile == IPC_TILE_AUTO) tile = pick_tile(M, N, groups);
   return 0;
 }
@@ -261,8 +264,8 @@ long long s16_workspace_need(int mode, int act, int M, long long kb, int groups)
 // otherwise every row tile activates its B block in its loader.  The library
 // allocates nothing either way.
 int run_s16(int mode, const WideProblem& q, int groups, long long a_gs, long long b_gs, long long o_gs,
-            long long x_gs, long long o2_gs, int operand, int act, void* workspace, long long ws_bytes, void* stream,
-            const char* what) {
+            long long x_gs, long long o2_gs, int operand, int act, int cfg, void* workspace, long long ws_bytes,
+            void* stream, const char* what) {
   hipStream_t s = (hipStream_t)stream;
   const long long need = s16_workspace_need(mode, act, q.M, b_gs, groups);
   if (need > 0 && workspace && ws_bytes >= need) {
@@ -271,10 +274,10 @@ int run_s16(int mode, const WideProblem& q, int groups, long long a_gs, long lon
     qa.b = workspace;
     const std::vector<WideProblem> v = s16_groups(qa, groups, a_gs, b_gs, o_gs, x_gs, o2_gs);
     TRY(launch_rc(launch_s16_activate(q.b, workspace, n, operand, act, s), what));
-    return launch_rc(launch_s16(mode, v.data(), groups, operand, IPC_ACT_IDENTITY, s), what);
+    return launch_rc(launch_s16(mode, v.data(), groups, operand, IPC_ACT_IDENTITY, cfg, s), what);
   }
   const std::vector<WideProblem> v = s16_groups(q, groups, a_gs, b_gs, o_gs, x_gs, o2_gs);
-  return launch_rc(launch_s16(mode, v.data(), groups, operand, act, s), what);
+  return launch_rc(launch_s16(mode, v.data(), groups, operand, act, cfg, s), what);
 }
 
 int check_workspace(const void* workspace, long long ws_bytes) {
@@ -337,7 +340,7 @@ int ipc_pred_err_ws(const void* x_upper, const void* w, const void* x_lower, voi
     q.out = e; q.ldo = B; q.aux = x_lower; q.ldx = B;
     q.vec = B % 4 == 0 && al8(e) && al8(x_lower);
     return run_s16(S16_PRED, q, groups, (long long)M * K, (long long)K * B, (long long)M * B, (long long)M * B, 0,
-                   operand, act, workspace, workspace_bytes, stream, "ipc_pred_err");
+                   operand, act, use_dma - 1, workspace, workspace_bytes, stream, "ipc_pred_err");
   }
   GemmProblem p = make_pf(KIND_PRED, x_upper, w, x_lower, e, M, K, B, groups, act, es);
   return launch_rc(launch_gemm(&p, 1, storage, operand, effective_split(storage, operand, split), tile,
@@ -372,7 +375,7 @@ int ipc_forward_ws(const void* x_upper, const void* w, void* out, int M, int K, 
     q.out = out; q.ldo = B;
     q.vec = B % 4 == 0 && al8(out);
     return run_s16(S16_FWD, q, groups, (long long)M * K, (long long)K * B, (long long)M * B, 0, 0, operand, act,
-                   workspace, workspace_bytes, stream, "ipc_forward");
+                   use_dma - 1, workspace, workspace_bytes, stream, "ipc_forward");
   }
   GemmProblem p = make_pf(KIND_FWD, x_upper, w, nullptr, out, M, K, B, groups, act, es);
   return launch_rc(launch_gemm(&p, 1, storage, operand, effective_split(storage, operand, split), tile,
@@ -404,7 +407,7 @@ int ipc_infer_update(void* x, const void* e, const void* w_lower, const void* e_
     q.scal = gamma;
     q.vec = B % 4 == 0 && al8(x) && al8(e) && al8(a_out);
     return run_s16(S16_INFER, q, groups, (long long)K * M, (long long)K * B, (long long)M * B, (long long)M * B,
-                   (long long)M * B, operand, act, nullptr, 0, stream, "ipc_infer_update");
+                   (long long)M * B, operand, act, use_dma - 1, nullptr, 0, stream, "ipc_infer_update");
   }
   GemmProblem p = make_inf(x, e, w_lower, e_lower, a_out, M, K, B, groups, gamma, act, es);
   return launch_rc(launch_gemm(&p, 1, storage, operand, IPC_SPLIT_NONE, tile, (hipStream_t)stream),
@@ -440,7 +443,8 @@ int ipc_weight_update_ws(void* w, const void* e, const void* x_upper, int M, int
     q.scal = alpha;
     q.vec = K % 4 == 0 && al8(w);
     return run_s16(S16_WEIGHT, q, groups, (long long)M * B, (long long)K * B, (long long)M * K, 0, 0, operand,
-                   recompute ? act : IPC_ACT_IDENTITY, workspace, workspace_bytes, stream, "ipc_weight_update");
+                   recompute ? act : IPC_ACT_IDENTITY, use_dma - 1, workspace, workspace_bytes, stream,
+                   "ipc_weight_update");
   }
   GemmProblem p = make_wgt(w, e, x_upper, M, K, B, groups, alpha, recompute, act, es);
   return launch_rc(launch_gemm(&p, 1, storage, operand, IPC_SPLIT_NONE, tile, (hipStream_t)stream),
@@ -701,12 +705,13 @@ bool narrow_outer(int B, int wmode) {
 // fp32 operands run it with either weight update (the rank-B one as the column
 // kernel computes it); 16-bit operands with the GEMM update only.
 long long resident_eligible(int L, const int* dims, int B, int operand, int split, int wmode, bool narrow,
-                            ResidentArgs& ra) {
+                            ResidentArgs& ra, int top_rows = RES_TOP_ROWS) {
   if (!narrow) return -1;
   const bool outer = narrow_outer(B, wmode);
-  if (operand == IPC_DT_F32) return split == IPC_SPLIT_NONE ? resident_plan(dims, L, B, 1, 4, outer, ra) : -1;
+  if (operand == IPC_DT_F32)
+    return split == IPC_SPLIT_NONE ? resident_plan(dims, L, B, 1, 4, outer, top_rows, ra) : -1;
   if (outer || (split != IPC_SPLIT_NONE && split != IPC_SPLIT_WX)) return -1;
-  return resident_plan(dims, L, B, split == IPC_SPLIT_WX ? 3 : 1, 2, false, ra);
+  return resident_plan(dims, L, B, split == IPC_SPLIT_WX ? 3 : 1, 2, false, top_rows, ra);
 }
 
 int launch_narrow_mode(ipc_plan* plan, int mode, int steps, hipStream_t s) {
@@ -1243,6 +1248,33 @@ int ipc_plan_set_wide_config(ipc_plan* plan, int pred_cfg, int infer_cfg, int we
       WideLayout(plan->dims, plan->L, plan->B, plan->split == IPC_SPLIT_W, plan->wcfg[0], plan->wdirect).total;
   return ok();
 }
+
+int ipc_plan_set_resident_rows(ipc_plan* plan, int rows) {
+  if (!plan) return fail(IPC_ERR_NULL, "plan is NULL");
+  if (!plan->resident) return fail(IPC_ERR_CONFIG, "the plan does not run the layer-resident kernel");
+  if (plan->bound) return fail(IPC_ERR_STATE, "set the row-block size before ipc_plan_bind");
+  if (rows == -1) rows = RES_TOP_ROWS;
+  if (rows != 16 && rows != 32 && rows != 64)
+    return fail(IPC_ERR_CONFIG, "the top layer's row blocks are 16, 32 or 64 rows (-1 = default %d); got %d",
+                RES_TOP_ROWS, rows);
+  ResidentArgs ra{};
+  const long long res_bytes = resident_eligible(plan->L, plan->dims.data(), plan->B, plan->operand, plan->split,
+                                                plan->wmode, true, ra, rows);
+  if (res_bytes < 0)
+    return fail(IPC_ERR_CONFIG, "row blocks of %d rows do not fit this net's layer-resident launch (LDS or flags)",
+                rows);
+  const int cap = coresident_capacity(
+      [&] { return resident_prepare(plan->operand, plan->split, plan->act, ra.lds_bytes); },
+      [&](int* n) { return resident_occupancy(plan->operand, plan->split, plan->act, ra.lds_bytes, n); });
+  if (cap >= 0 && resident_launch_blocks(ra) > cap)
+    return fail(IPC_ERR_CONFIG, "row blocks of %d rows need %d co-resident workgroups; this device holds %d", rows,
+                resident_launch_blocks(ra), cap);
+  plan->rargs = ra;
+  plan->ws_bytes = plan->res_ws_off + res_bytes;
+  return ok();
+}
+
+int ipc_plan_resident_rows(const ipc_plan* plan) { return plan && plan->resident ? plan->rargs.top_rows : 0; }
 
 int ipc_plan_set_spin_limit(ipc_plan* plan, int limit) {
   if (!plan) return fail(IPC_ERR_NULL, "plan is NULL");

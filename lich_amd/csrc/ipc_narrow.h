@@ -99,11 +99,12 @@ constexpr int RES_MAX_B = 128;
 constexpr int RES_MAX_WG = 63;      // word 63 of the flag area is the cache generation
 constexpr int RES_FLAG_BYTES = 512;  // flag area: step flags, generation, per-workgroup cache slots
 constexpr int RES_TILE = 256;       // floats per exchanged 16x16 tile (64 lanes x 4)
-constexpr int RES_TOP_ROWS = 32;    // rows of W[L-1] per top workgroup (a 64-row layer takes two)
+constexpr int RES_TOP_ROWS = 32;    // default rows of W[L-1] per top workgroup (a 64-row layer takes two)
 
 struct ResidentArgs {
   int L, B, steps, nwg, chunks, kc, spin_limit, lds_bytes;
-  int halves;                   // top-layer row blocks of RES_TOP_ROWS (one workgroup per chunk and block)
+  int halves;                   // top-layer row blocks of top_rows (one workgroup per chunk and block)
+  int top_rows;                 // rows of W[L-1] per top workgroup: 16, 32 (default) or 64
   int outer;                    // weight update as a rank-B outer product on the VALU (fp32 operands, B <= 16)
   float alpha, gamma;
   int dims[NARROW_MAX_L + 1];
@@ -171,7 +172,8 @@ inline int resident_tiles(int d, int B) { return ((d + 15) / 16) * ((B + 15) / 1
 // (NARROW_KCHUNK columns of the top layer each), kc, nwg, outer and
 // lds_bytes of `a` and returns the workspace bytes its flags and exchange
 // buffers need, or -1 when the net is not eligible.
-long long resident_plan(const int* dims, int L, int B, int split, int esize, bool outer, ResidentArgs& a);
+long long resident_plan(const int* dims, int L, int B, int split, int esize, bool outer, int top_rows,
+                        ResidentArgs& a);
 
 // Lays the flags, exchange buffers and input images out in `ws` (resident_plan's bytes).
 void resident_bind(ResidentArgs& a, char* ws);

@@ -235,21 +235,21 @@ struct Resident {
     l = hidden ? wg : L - 1;
     // the layer's argument scalars in one batch of loads with one wait (loaded
     // where first used, they would cost a memory round trip each)
-    const int dm = p.dims[l], dk = p.dims[l + 1], din = p.dims[L], kc = p.kc, nch = p.chunks;
+    const int dm = p.dims[l], dk = p.dims[l + 1], din = p.dims[L], kc = p.kc, nch = p.chunks, trows = p.top_rows;
     const long long istride = p.image_stride;
     x_g = p.x[l];
     xu_g = p.x[l + 1];
     fu_g = p.fx[l + 1];
     w_g = p.w[l];
     image_g = p.image;
-    asm volatile("" ::"s"(dm), "s"(dk), "s"(din), "s"(kc), "s"(nch), "s"(istride), "s"(x_g), "s"(xu_g), "s"(fu_g),
-                 "s"(w_g), "s"(image_g), "s"(p.flags));
+    asm volatile("" ::"s"(dm), "s"(dk), "s"(din), "s"(kc), "s"(nch), "s"(trows), "s"(istride), "s"(x_g), "s"(xu_g),
+                 "s"(fu_g), "s"(w_g), "s"(image_g), "s"(p.flags));
     const int top = hidden ? 0 : wg - (L - 1);
     j = hidden ? 0 : top % nch;
     image_g += (long long)j * istride;
     h = hidden ? 0 : top / nch;
-    row0 = h * RES_TOP_ROWS;
-    M = hidden ? dm : min(RES_TOP_ROWS, dm - row0);
+    row0 = h * trows;
+    M = hidden ? dm : min(trows, dm - row0);
     k0 = hidden ? 0 : j * kc;
     K = hidden ? dk : min(kc, din - k0);
     ldw_g = dk;
@@ -1258,7 +1258,9 @@ hipError_t dispatch(int operand, int split, int act, bool prep, int bytes, const
 
 }  // namespace
 
-long long resident_plan(const int* dims, int L, int B, int split, int esize, bool outer, ResidentArgs& a) {
+long long resident_plan(const int* dims, int L, int B, int split, int esize, bool outer, int top_rows,
+                        ResidentArgs& a) {
+  if (top_rows != 16 && top_rows != 32 && top_rows != 64) return -1;
   if (L < 2 || L > NARROW_MAX_L || B < 1 || B > RES_MAX_B) return -1;
   if (esize == 4 ? split >= 2 : esize != 2) return -1;
   if (outer && (esize != 4 || B > NARROW_OUTER_MAX_B)) return -1;
@@ -1274,13 +1276,14 @@ long long resident_plan(const int* dims, int L, int B, int split, int esize, boo
   }
   // top layer: one workgroup per NARROW_KCHUNK columns (the column kernel's
   // partial-sum order)
-  // and row blocks of RES_TOP_ROWS rows (a workgroup per chunk and block)
+  // and row blocks of top_rows rows (a workgroup per chunk and block; one
+  // XCD per row block, at least one XCD left for the hidden workgroups)
   const int dL = dims[L], kc = NARROW_KCHUNK, C = (dL + kc - 1) / kc;
-  const int halves = (dims[L - 1] + RES_TOP_ROWS - 1) / RES_TOP_ROWS;
+  const int halves = (dims[L - 1] + top_rows - 1) / top_rows;
+  if (halves > 7) return -1;
   if ((L - 1) + halves * C + halves > RES_MAX_WG) return -1;  // flags[nwg + h]: block h's eps flags
   ResidentLds o;
-  resident_lds_layout(dims[L - 1] < RES_TOP_ROWS ? dims[L - 1] : RES_TOP_ROWS, dL < kc ? dL : kc, B, false, s3, esize,
-                      o);
+  resident_lds_layout(dims[L - 1] < top_rows ? dims[L - 1] : top_rows, dL < kc ? dL : kc, B, false, s3, esize, o);
   need = o.bytes > need ? o.bytes : need;
   if (need > limit) return -1;
   a.L = L;
@@ -1288,6 +1291,7 @@ long long resident_plan(const int* dims, int L, int B, int split, int esize, boo
   a.chunks = C;
   a.kc = kc;
   a.halves = halves;
+  a.top_rows = top_rows;
   a.outer = outer ? 1 : 0;
   a.nwg = (L - 1) + halves * C;
   a.lds_bytes = res_round(need, 16);

@@ -3,43 +3,21 @@
 // storage design, src/ipc_tilelang/tilelang_kernels.py:114-349) on the
 // LDS-DMA MFMA kernel of ipc_dma_gemm.h: the caller's tensors are the
 // operands, f(X_upper) goes through the register path when an activation
-// applies (or, for large calls, is evaluated once into a buffer by
-// s16_activate_kernel and read through LDS DMA like every other operand).
-#include "ipc_dma_gemm.h"
+// applies (or, for large calls given a caller workspace, is evaluated once
+// into it by s16_activate_kernel and read through LDS DMA like every other
+// operand).  This file holds tile configuration 0 and the dispatch over the
+// configurations of ipc_s16_tiles.h.
+#include "ipc_s16_tiles.h"
 
 namespace ipc {
 namespace {
 
-using dma::Cfg;
-
-// Tile configurations (BM, BN, stages, waves along M, waves along N): the
-// prediction, forward and inference kernels run 256 x 128 tiles with 16 waves
-// (64 x 32 per wave, four per SIMD to hide the LDS reads and barriers), 1-10 %
-// faster than 8 waves at M = K >= 4096, B >= 2048; the weight update keeps 8
-// waves (64 x 64 each), within +-3 % of 16.  The k order, and so every result
-// bit, does not depend on the wave layout.
-#ifndef S16_CFG
-#define S16_CFG 256, 128, 3, 4, 4
-#endif
-#ifndef S16_WCFG
-#define S16_WCFG 256, 128, 3, 4, 2
-#endif
-
-template <typename OT>
-struct S16 {
-  template <int ACT>
-  struct Run {
-    static hipError_t run(int mode, const WideProblem* probs, int count, hipStream_t s) {
-      constexpr bool R = ACT != ACT_IDENTITY;  // activation in the B loader: register path
-      switch (mode) {
-        case S16_PRED: return Cfg<OT, S16_PRED, 1, ACT, R, S16_CFG>::launch(probs, count, s);
-        case S16_FWD: return Cfg<OT, S16_FWD, 1, ACT, R, S16_CFG>::launch(probs, count, s);
-        case S16_INFER: return Cfg<OT, S16_INFER, 1, ACT, false, S16_CFG>::launch(probs, count, s);
-        default: return Cfg<OT, S16_WEIGHT, 1, ACT, R, S16_WCFG>::launch(probs, count, s);
-      }
-    }
-  };
-};
+// Tile configuration 0, the default (IPC_TILE_DMA_256x128): 256 x 128 tiles;
+// the prediction, forward and inference kernels run 16 waves (64 x 32 per
+// wave, four per SIMD to hide the LDS reads and barriers), 1-10 % faster than
+// 8 waves at M = K >= 4096, B >= 2048; the weight update keeps 8 waves (64 x
+// 64 each), within +-3 % of 16.
+using Tiles0 = s16::Tiles<256, 128, 3, 4, 4, 4, 2>;
 
 // out[i] = f(in[i]) rounded to the storage type: the register path's value
 // (f in fp32 of the stored 16-bit input, then one rounding), 8 elements per
@@ -101,16 +79,13 @@ hipError_t launch_s16_activate(const void* in, void* out, long long n, int opera
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_s16(int mode, const WideProblem* probs, int count, int operand, int act, hipStream_t s) {
-  for (int base = 0; base < count; base += WIDE_MAX_BATCH) {
-    const int n = count - base < WIDE_MAX_BATCH ? count - base : WIDE_MAX_BATCH;
-    hipError_t e;
-    if (operand == DT_F16) e = dma::by_act<S16<f16>::template Run>(act, mode, probs + base, n, s);
-    else if (operand == DT_BF16) e = dma::by_act<S16<bf16>::template Run>(act, mode, probs + base, n, s);
-    else return hipErrorInvalidValue;
-    if (e != hipSuccess) return e;
+hipError_t launch_s16(int mode, const WideProblem* probs, int count, int operand, int act, int cfg, hipStream_t s) {
+  switch (cfg) {
+    case 0: return Tiles0::launch(mode, probs, count, operand, act, s);
+    case 1: return s16::launch_tiles1(mode, probs, count, operand, act, s);
+    case 2: return s16::launch_tiles2(mode, probs, count, operand, act, s);
+    default: return hipErrorInvalidValue;
   }
-  return hipSuccess;
 }
 
 }  // namespace ipc

@@ -121,7 +121,7 @@ hipError_t wide_prepare();
 // Standalone 16-bit-storage launches (modes S16_*) over `count` problems.
 // `act`: the loader activation of S16_PRED / S16_FWD / S16_WEIGHT (ACT_IDENTITY
 // for a saved activation), the epilogue activation of S16_INFER.
-hipError_t launch_s16(int mode, const WideProblem* probs, int count, int operand, int act, hipStream_t s);
+hipError_t launch_s16(int mode, const WideProblem* probs, int count, int operand, int act, int cfg, hipStream_t s);
 // out[i] = cvt(f(in[i])) over n 16-bit elements: the B operand of a standalone
 // S16_PRED / S16_FWD / recomputing S16_WEIGHT call evaluated once, so that the
 // call then runs with ACT_IDENTITY on the LDS-DMA path for that operand.

@@ -161,6 +161,15 @@ class HierarchicalPolicy:
         except (TypeError, ValueError):
             return default
 
+    def selected_resident_rows(self, *, default, **kw):
+        """The entry's layer-resident row-block size (written by
+        ``lich_amd.autotune``), else ``default``."""
+        rows = self._best(**kw).get("resident_rows")
+        try:
+            return default if rows is None else int(rows)
+        except (TypeError, ValueError):
+            return default
+
     def selected_use_graph(self, *, default: bool, **kw) -> bool:
         return bool(self._best(**kw).get("use_cuda_graph", default))
 

@@ -83,6 +83,10 @@ class IPCConfig:
     # Wide path tile configuration (pred, infer, weight, ksplit), -1 = default
     # (ipc_plan_set_wide_config); a policy file's tuned choice takes precedence.
     wide_config: tuple[int, int, int, int] | None = None
+    # Layer-resident plans: rows of the top layer per workgroup (16, 32 or
+    # 64; None = the library's default, 32) (ipc_plan_set_resident_rows); a
+    # policy file's tuned choice takes precedence.
+    resident_rows: int | None = None
     # Kernel path: "auto" (the layer-resident whole-step kernel when eligible,
     # else the column-block whole-step kernel for narrow nets, else the wide
     # GEMM path when eligible, else phased), "resident", "narrow" / "on",
@@ -193,6 +197,7 @@ class HipIPC:
                 self._hierarchical_policy = None
         self._runtime_recompute: bool = bool(cfg.recompute_activation)
         self.wide_config = cfg.wide_config
+        self.resident_rows = cfg.resident_rows
         self.grid_z_cap: int = max(0, int(cfg.grid_z_max_layers))
         self.layer_groups = self._groups_for(self.grid_z_cap)
         self._signature_cache: dict[int, str] = {}
@@ -257,12 +262,14 @@ class HipIPC:
         first, then for grid.z the grid.z policy file keyed by this device."""
         self._runtime_recompute = bool(self.cfg.recompute_activation)
         self.wide_config = self.cfg.wide_config
+        self.resident_rows = self.cfg.resident_rows
         cap = None
         pol = self._hierarchical_policy
         if pol is not None:
             kw = self._policy_kw(B)
             self._runtime_recompute = pol.selected_recompute_activation(default=self._runtime_recompute, **kw)
             self.wide_config = pol.selected_wide_config(default=self.wide_config, **kw)
+            self.resident_rows = pol.selected_resident_rows(default=self.resident_rows, **kw)
             if self.cfg.use_grid_z and self.cfg.grid_z_auto:
                 cap = pol.selected_grid_z(default=None, **kw)
         if cap is None and self.cfg.use_grid_z and self.cfg.grid_z_auto:
@@ -323,6 +330,8 @@ class HipIPC:
         nat.check(nat.lib().ipc_plan_set_tiles(handle, *self.phase_tiles(B)))
         if self.wide_config is not None and int(nat.lib().ipc_plan_path(handle)) == nat.PATH_WIDE:
             nat.check(nat.lib().ipc_plan_set_wide_config(handle, *[int(v) for v in self.wide_config]))
+        if self.resident_rows is not None and int(nat.lib().ipc_plan_path(handle)) == nat.PATH_RESIDENT:
+            nat.check(nat.lib().ipc_plan_set_resident_rows(handle, int(self.resident_rows)))
         nbytes = int(nat.lib().ipc_plan_workspace_bytes(handle))
         # zero-initialised (the wide path relies on zero padding); torch's
         # allocations are 256-byte aligned as the plan requires

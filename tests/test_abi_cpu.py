@@ -582,3 +582,57 @@ def test_split2_problem_without_lo_operand_is_refused_on_the_host():
     assert chk(P, 2, 1, 0, 4096, 128) == nat.ERR_CONFIG
     assert chk(P, 1, 0, 0, 4160, 2) == nat.ERR_CONFIG
     assert chk(7, 1, 0, 0, 64, 1) == nat.ERR_CONFIG
+
+
+def test_resident_row_blocks_are_a_plan_option():
+    """ipc_plan_set_resident_rows: 16, 32 (the default) or 64 rows of the top
+    layer per workgroup on a layer-resident plan, before bind; other sizes,
+    other paths and nets whose blocks do not fit are refused and leave the
+    plan as it was.  The exchange records are per 16-row tile, so the
+    workspace does not depend on the size."""
+    lib = _lib()
+    dims, B = (10,) + (64,) * 6 + (784,), 128
+    L = len(dims) - 1
+    d = (ctypes.c_int * (L + 1))(*dims)
+    h = ctypes.c_void_p()
+    assert lib.ipc_plan_create(ctypes.byref(h), L, d, B, 0, nat.DT_F16, 1, 2, 1e-4, 0.5, 1, 0, 3) == nat.IPC_OK
+    try:
+        ws = lib.ipc_plan_workspace_bytes(h)
+        assert lib.ipc_plan_resident_rows(h) == 32
+        for rows in (16, 64, 32, -1):
+            assert lib.ipc_plan_set_resident_rows(h, rows) == nat.IPC_OK, nat.last_error()
+            assert lib.ipc_plan_resident_rows(h) == (32 if rows == -1 else rows)
+            assert lib.ipc_plan_workspace_bytes(h) == ws
+        assert lib.ipc_plan_set_resident_rows(h, 48) == nat.ERR_CONFIG and "16, 32 or 64" in nat.last_error()
+        assert lib.ipc_plan_resident_rows(h) == 32
+    finally:
+        lib.ipc_plan_destroy(h)
+    assert lib.ipc_plan_set_resident_rows(None, 16) == nat.ERR_NULL
+    # a column-kernel plan has no row blocks
+    assert lib.ipc_plan_create(ctypes.byref(h), L, d, B, 0, nat.DT_F16, 1, 2, 1e-4, 0.5, 1, 0, 1) == nat.IPC_OK
+    try:
+        assert lib.ipc_plan_set_resident_rows(h, 16) == nat.ERR_CONFIG and lib.ipc_plan_resident_rows(h) == 0
+    finally:
+        lib.ipc_plan_destroy(h)
+    # split 3 with 64-row blocks of a 784-wide input: the block's operands exceed the LDS
+    assert lib.ipc_plan_create(ctypes.byref(h), L, d, B, 0, nat.DT_BF16, 3, 2, 1e-4, 0.5, 1, 0, 3) == nat.IPC_OK
+    try:
+        rc = lib.ipc_plan_set_resident_rows(h, 64)
+        assert rc in (nat.IPC_OK, nat.ERR_CONFIG)
+        assert lib.ipc_plan_resident_rows(h) == (64 if rc == nat.IPC_OK else 32)
+    finally:
+        lib.ipc_plan_destroy(h)
+
+
+def test_dma_tile_ids_are_refused_where_the_dma_kernel_cannot_run():
+    """The three LDS-DMA tile ids need 16-bit storage and a contraction of
+    whole 64-k steps; asked for otherwise they are an error, never a silent
+    fallback; an id past the table is unknown."""
+    lib = _lib()
+    for tile in nat.TILE_DMA_TILES:
+        rc = lib.ipc_pred_err(P, P, P, P, 64, 64, 128, 1, nat.DT_F32, nat.DT_F32, 1, 2, tile, None)
+        assert rc == nat.ERR_CONFIG and "LDS-DMA" in nat.last_error()
+        rc = lib.ipc_pred_err(P, P, P, P, 64, 100, 128, 1, nat.DT_BF16, nat.DT_BF16, 1, 2, tile, None)
+        assert rc == nat.ERR_CONFIG and "LDS-DMA" in nat.last_error()
+    assert lib.ipc_pred_err(P, P, P, P, 64, 64, 128, 1, nat.DT_BF16, nat.DT_BF16, 1, 2, nat.TILE_COUNT, None) == \
+        nat.ERR_CONFIG

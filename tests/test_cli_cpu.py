@@ -65,3 +65,26 @@ def test_toolchain_report_runs_without_a_gpu(capsys):
     assert cli.main(["toolchain"]) == 0
     rep = json.loads(capsys.readouterr().out)
     assert rep["library_built"] is True and rep["abi_version"] >= 5
+
+
+def test_reference_command_follows_the_scripts_random_stream(capsys):
+    """scripts/validate_reference.py:16-35 seeds the global generator once and
+    draws the input, then each W by kaiming_uniform_(a=sqrt(5)) from that same
+    generator; relu; forward initialisation; alpha 1e-4, gamma 0.5.  The
+    command's printed energies are that sequence's (recomputed here with the
+    oracle's step, itself pinned by tests/test_oracle.py)."""
+    from oracle import ipc_oracle as O
+
+    assert cli.main(["reference", "--depth", "3", "--hidden", "64", "--batch", "8", "--steps", "4"]) == 0
+    rows = [ln.split() for ln in capsys.readouterr().out.splitlines() if ln[:1].isdigit()]
+    torch.manual_seed(0)
+    dims = (10, 64, 64, 64, 784)
+    x_in = torch.randn((784, 8))
+    y = O.one_hot(torch.arange(8) % 10, 10)
+    w = [torch.nn.init.kaiming_uniform_(torch.empty((r, c)), a=5 ** 0.5) for r, c in zip(dims[:-1], dims[1:])]
+    x = O.forward_init(x_in, y, w, "relu")
+    for i in range(4):
+        x, w, _e, m = O.ipc_step(x, w, act="relu", alpha=1e-4, gamma=0.5)
+        assert int(rows[i][0]) == i
+        assert abs(float(rows[i][1]) - m["energy"]) <= 1e-5 * m["energy"]
+        assert abs(float(rows[i][2]) - m["max_abs_error"]) <= 1e-5 * m["max_abs_error"]

@@ -275,3 +275,42 @@ def test_default_standalone_calls_allocate_no_device_memory():
     free1, _total = torch.cuda.mem_get_info(DEV)
     print(f"free device memory before {free0} after {free1}", flush=True)
     assert free1 == free0
+
+
+@pytest.mark.parametrize("op", ["f16", "bf16"])
+@pytest.mark.parametrize("act", ["relu", "tanh", "identity"])
+@pytest.mark.parametrize("M,K,B", [(296, 192, 136), (1000, 256, 264), (64, 128, 8)])
+def test_dma_tile_configurations_agree(M, K, B, act, op):
+    """The three LDS-DMA tile configurations (the autotuner's search space
+    for the standalone calls) add the contraction in the same k order with
+    the same epilogue: prediction, forward, inference (with A_out) and both
+    weight updates agree with the default configuration bit for bit for relu
+    and identity, and within the activation-contraction allowance otherwise.
+    (M is a multiple of 8: the inference reads W_lower [K, M] transposed.)"""
+    report("dma16-tiles", M=M, K=K, B=B, act=act, op=op)
+    dt = OPS[op]
+    g = gen(7 * M + 3 * K + B)
+    xu, w, xl = _t(randn((K, B), g), dt), _t(randn((M, K), g, 1 / math.sqrt(K)), dt), _t(randn((M, B), g), dt)
+    e, wl, el = _t(randn((M, B), g), dt), _t(randn((K, M), g, 1 / math.sqrt(K)), dt), _t(randn((K, B), g), dt)
+    # weight update: W [M, Kw], contraction B (a multiple of 64)
+    Bw = 128
+    ew, xw, w0 = _t(randn((M, Bw), g), dt), _t(randn((K, Bw), g), dt), _t(randn((M, K), g, 1 / math.sqrt(K)), dt)
+    res = {}
+    for tile in (3, 4, 5):
+        cfg = KernelConfig(tile=tile)
+        ep = torch.empty((M, B), device=DEV, dtype=dt)
+        fp = torch.empty((M, B), device=DEV, dtype=dt)
+        x, a = xl.clone(), torch.empty((M, B), device=DEV, dtype=dt)
+        wr, ws = w0.clone(), w0.clone()
+        kp = build_prediction_error(M, K, B, act, dt, cfg)
+        assert kp.tile == tile
+        kp(xu, w, xl, ep)
+        build_forward(M, K, B, act, dt, cfg)(xu, w, fp)
+        build_inference_update(M, K, B, act, dt, cfg, 0.5, True)(x, e, wl, el, a)
+        build_weight_update(M, K, Bw, act, dt, cfg, 0.01, True)(wr, ew, xw)
+        build_weight_update(M, K, Bw, act, dt, cfg, 0.01, False)(ws, ew, xw)
+        res[tile] = (ep, fp, x, a, wr, ws)
+    torch.cuda.synchronize()
+    for tile in (4, 5):
+        for i, (u, v) in enumerate(zip(res[3], res[tile])):
+            assert _same(v, u, act), (tile, i)

@@ -129,5 +129,9 @@ def test_execution_tuning_times_every_eligible_path():
     best, trials = AT.tune_execution([10, 64, 64, 784], 128, "tanh", torch.float16, steps=4, replays=5)
     # fp16 operands default to split 1 on narrow nets, which the wide path also runs
     assert {t["path"] for t in trials} == {"resident", "narrow", "phased", "wide"}
-    assert len(trials) == 16 and best in trials and best["step_ms"] == min(t["step_ms"] for t in trials)
+    # recompute on / off x graph on / off per path, and per row-block size (16, 32, 64) on the resident path
+    per_path = {p: sum(t["path"] == p for t in trials) for p in ("resident", "narrow", "phased", "wide")}
+    assert per_path == {"resident": 12, "narrow": 4, "phased": 4, "wide": 4}
+    assert {t["resident_rows"] for t in trials if t["path"] == "resident"} == {16, 32, 64}
+    assert best in trials and best["step_ms"] == min(t["step_ms"] for t in trials)
     assert best["path"] == "resident"

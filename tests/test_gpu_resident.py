@@ -395,3 +395,44 @@ def test_rebinding_a_warm_resident_plan_starts_cold():
     for name, u_list, v_list in (("x", b.x, fresh.x), ("e", b.e[:-1], fresh.e[:-1]), ("w", b.w, fresh.w)):
         for l, (u, v) in enumerate(zip(u_list, v_list)):
             assert torch.equal(u, v), (name, l, float((u - v).abs().max()))
+
+
+@pytest.mark.parametrize("dims,B,op,split", [
+    ((10,) + (64,) * 6 + (784,), 128, F16, 1),
+    ((10,) + (64,) * 6 + (784,), 96, BF16, 3),
+    ((7, 33, 48, 130), 40, F16, 3),
+    ((10, 64, 64, 64, 784), 8, F32, 1),
+])
+def test_resident_row_blocks_agree_bitwise(dims, B, op, split):
+    """The top layer's row-block size (16, 32, 64: the tuner's search space
+    for layer-resident plans) changes only how the rows are dealt to
+    workgroups: every size gives the column kernel's bits over two launches."""
+    from lich_amd import _native as nat
+
+    report("resident-rows", dims=dims, B=B, op=op)
+    w0 = O.init_weights(dims, seed=51, init="xavier_uniform")
+    x_in, _l, y = O.make_batch(dims, B, seed=51)
+    col = _model(dims, w0, "tanh", op, "narrow", split=split)
+    col.initialize_batch(x_in.to(DEV), y.to(DEV))
+    col.run_steps(4)
+    col.run_steps(3)
+    ran = []
+    for rows in (16, 32, 64):
+        cfg = IPCConfig(dims=dims, activation="tanh", dtype=op, fused="resident", pred_split=split,
+                        weight_update_mode="gemm", resident_rows=rows, hierarchical_policy_auto=False)
+        try:
+            m = HipIPC(cfg, device=DEV, weights=w0)
+            m.initialize_batch(x_in.to(DEV), y.to(DEV))
+        except ValueError as exc:
+            print(f"rows {rows}: {exc}", flush=True)  # the blocks do not fit this net
+            continue
+        assert m.path == "resident" and nat.lib().ipc_plan_resident_rows(m._plan) == rows
+        m.run_steps(4)
+        m.run_steps(3)
+        m.check_steps()
+        torch.cuda.synchronize()
+        for name, a, b in (("x", m.x, col.x), ("e", m.e[:-1], col.e[:-1]), ("w", m.w, col.w)):
+            for l, (u, v) in enumerate(zip(a, b)):
+                assert torch.equal(u, v), (rows, name, l, float((u - v).abs().max()))
+        ran.append(rows)
+    assert 16 in ran and 32 in ran

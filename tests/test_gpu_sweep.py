@@ -14,7 +14,8 @@ and errors ~ N(0, 1), as ``bench.py --sweep`` times them.
   operands, exact products, the storage-precision epilogue of
   ``tilelang_kernels.py:173,227-231,319-320``): at most 2 bf16 ulps of the
   output's max-norm apart, with under 1 % of the elements differing at all.
-* M = K in {4096, 8192}, B in {2048, 8192}: a seeded sample of 64 rows x 64
+* every other point (M = K = 1024 with B = 8192, and M = K in {4096, 8192} with
+  every B): a seeded sample of 64 rows x 64
   columns of each output against the oracle (same gate), and for relu the
   LDS-DMA kernel bit-identical to the generic MFMA kernel on a 256-row slice
   (each output row depends only on its own rows of W and X, and both kernels
@@ -39,7 +40,7 @@ DMA = KernelConfig(tile=3)
 GEN = KernelConfig(tile=2)
 ALPHA, GAMMA = 0.01, 0.5
 SMALL = [(1024, 256), (1024, 2048)]
-LARGE = [(4096, 2048), (4096, 8192), (8192, 2048), (8192, 8192)]
+LARGE = [(1024, 8192), (4096, 256), (4096, 2048), (4096, 8192), (8192, 256), (8192, 2048), (8192, 8192)]
 
 
 def _inputs(n, B, seed):
