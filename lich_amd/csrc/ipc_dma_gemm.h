@@ -135,12 +135,40 @@ __device__ __forceinline__ float hi16(unsigned v) {
   return to_f32(__builtin_bit_cast(OT, (unsigned short)(v >> 16)));
 }
 
+// A buffer resource over `bytes` bytes at `base`: loads and stores take a
+// 32-bit per-lane offset and a uniform (scalar) one, so an epilogue can
+// address an element as (its lane's row and column) + (the row step of an
+// accumulator register, uniform) without a 64-bit address per element.
+// Offsets at or past `bytes` load zero and store nothing.
+struct Buf {
+  __amdgpu_buffer_rsrc_t r;
+  __device__ __forceinline__ Buf(const void* base, long long bytes)
+      : r(__builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0,
+                                            (int)(bytes < 0x7fffffffLL ? bytes : 0x7fffffffLL), 0x00020000)) {}
+  __device__ __forceinline__ float ld32(unsigned v, unsigned s) const {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, v, s, 0));
+  }
+  __device__ __forceinline__ void st32(float x, unsigned v, unsigned s) const {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, x), r, v, s, 0);
+  }
+  __device__ __forceinline__ void st16(unsigned short x, unsigned v, unsigned s) const {
+    __builtin_amdgcn_raw_buffer_store_b16(x, r, v, s, 0);
+  }
+};
+
 // Dynamic LDS of a configuration: the pipeline stages, reused by the fp32
-// epilogue tile (BM rows of BN + 1 floats).
+// epilogue tile (BM rows of BN + 1 floats) when that tile fits the CU's
+// 160 KB; a wide configuration whose tile does not (256 x 256) finishes from
+// the registers and stages only its 16-bit transposed copy (reg_epilogue).
 // (LO: the A_lo block, or A stored as fp32 rows of twice the bytes.)
-constexpr int smem_bytes(int BM, int BN, int S, bool LO) {
-  return S * (BM * 128 * (LO ? 2 : 1) + BN * 128) > BM * (BN + 1) * 4 ? S * (BM * 128 * (LO ? 2 : 1) + BN * 128)
-                                                                     : BM * (BN + 1) * 4;
+constexpr int stage_bytes(int BM, int BN, int S, bool LO) { return S * (BM * 128 * (LO ? 2 : 1) + BN * 128); }
+constexpr bool reg_epilogue(int BM, int BN, int S, bool LO, bool s16) {
+  return !s16 && BM * (BN + 1) * 4 > 160 * 1024 && stage_bytes(BM, BN, S, LO) <= 160 * 1024;
+}
+constexpr int smem_bytes(int BM, int BN, int S, bool LO, bool s16 = true) {
+  return reg_epilogue(BM, BN, S, LO, s16) || stage_bytes(BM, BN, S, LO) > BM * (BN + 1) * 4
+             ? stage_bytes(BM, BN, S, LO)
+             : BM * (BN + 1) * 4;
 }
 
 // Position (tile row mb, tile column nb) of tile `t` of a tm x tn tile grid
@@ -313,12 +341,16 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
     }
   };
   constexpr bool PRE = MODE != WIDE_FWD && MODE != S16_FWD;
+  constexpr bool REG = reg_epilogue(BM, BN, S, LO, S16);
   const bool pre_from_aux = MODE == WIDE_PRED || MODE == S16_PRED;
-  float pre[PRE ? IT : 1][4];
-  if (PRE && !partial) {
+  // the register epilogue loads its input block by block after the main loop
+  // (fetched here, IT groups of 4 would take the accumulators' registers)
+  constexpr bool PREF = PRE && !REG;
+  float pre[PREF ? IT : 1][4];
+  if (PREF && !partial) {
 #pragma unroll
     for (int u = 0; u < IT; ++u)
-      load_group(pre_from_aux ? p.aux : p.out, pre_from_aux ? p.ldx : p.ldo, u, pre[PRE ? u : 0]);
+      load_group(pre_from_aux ? p.aux : p.out, pre_from_aux ? p.ldx : p.ldo, u, pre[PREF ? u : 0]);
   }
 
   f32x16 acc[RM][RN];
@@ -481,6 +513,101 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
         }
     return;
   }
+  if constexpr (REG) {
+    // Register epilogue (wide configurations whose fp32 tile exceeds the
+    // LDS): every element is finished in the accumulator layout (lane column
+    // elr = lane % 32, rows 8 g + 4 elk + 0..3 of each 32 x 32 block) with
+    // the rounding steps of the LDS path below; the fp32 masters and the
+    // natural 16-bit copy are stored from the registers (32 lanes: 128 / 64
+    // contiguous bytes of one row), through buffer resources, so that an
+    // element's address is the lane's offset plus the register's uniform row
+    // step.  The 16-bit transposed copy is staged in LDS as a [BN][BM] tile
+    // (16-byte chunk c of row n at chunk c ^ (n % 32): conflict-free for both
+    // passes, BM >= 256) and then written row by row, 16 bytes per lane.
+    static_assert(BM >= 256 && BN * BM * (int)sizeof(OT) <= stage_bytes(BM, BN, S, LO), "transposed tile");
+    const int elr = lane & 31, elk = lane >> 5;
+    constexpr bool EIN = MODE == WIDE_INFER;
+    const long long xld = pre_from_aux ? p.ldx : p.ldo;
+    const Buf bx(pre_from_aux ? p.aux : p.out, PRE ? (long long)M * xld * 4 : 0);
+    const Buf be(p.aux, EIN ? (long long)M * p.ldx * 4 : 0);
+    const Buf bo(p.out, (long long)M * p.ldo * 4);
+    const Buf bh(p.h, p.h ? (long long)M * p.ldh * (long long)sizeof(OT) : 0);
+    const Buf bl(p.hl, p.hl ? (long long)M * p.ldhl * (long long)sizeof(OT) : 0);
+    const Buf b2(p.out2, p.out2 ? (long long)M * p.ld2 * 4 : 0);
+    unsigned short* tl = reinterpret_cast<unsigned short*>(smem);
+    wait_vmcnt<0>();
+    __syncthreads();  // every wave is done with the pipeline stages
+    auto qrow = [](int q) { return 8 * (q >> 2) + (q & 3); };
+#pragma unroll
+    for (int i = 0; i < RM; ++i)
+#pragma unroll
+      for (int j = 0; j < RN; ++j) {
+        const int nl = wn * WTN + j * 32 + elr, n = n0 + nl;
+        const int ml0 = wm * WTM + i * 32 + 4 * elk, mb = m0 + ml0;
+        const bool ncol = n < N;
+        float xin[PRE ? 16 : 1], ein[EIN ? 16 : 1];
+        const unsigned vx = (unsigned)(mb * xld + n) * 4u, ve = (unsigned)(mb * p.ldx + n) * 4u;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          if constexpr (PRE) xin[PRE ? q : 0] = ncol ? bx.ld32(vx, (unsigned)(qrow(q) * xld) * 4u) : 0.0f;
+          if constexpr (EIN) ein[EIN ? q : 0] = ncol ? be.ld32(ve, (unsigned)(qrow(q) * p.ldx) * 4u) : 0.0f;
+        }
+        const unsigned vo = (unsigned)(mb * p.ldo + n) * 4u, vh = (unsigned)(mb * p.ldh + n) * (unsigned)sizeof(OT),
+                       vl = (unsigned)(mb * p.ldhl + n) * (unsigned)sizeof(OT), v2 = (unsigned)(mb * p.ld2 + n) * 4u;
+        unsigned short hs[16];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+#pragma clang fp contract(off)
+          const float a = acc[i][j][q];
+          const float x = PRE ? xin[PRE ? q : 0] : 0.0f;
+          float v, fv = 0.0f;
+          OT hv, lv;
+          if (MODE == WIDE_PRED) {
+            v = x - a;                                                // eps
+            hv = cvt<OT>(v);
+          } else if (MODE == WIDE_INFER) {
+            v = x + p.scal * (-ein[EIN ? q : 0] + dact_t<ACT>(x) * a);  // x_new
+            fv = act_t<ACT>(v);
+            hv = cvt<OT>(fv);
+          } else if (MODE == WIDE_FWD) {
+            v = a;                                                    // x = W f(x_upper)
+            fv = act_t<ACT>(v);
+            hv = cvt<OT>(fv);
+          } else {
+            v = x + p.scal * a;                                       // W_new
+            hv = cvt<OT>(v);
+            lv = cvt<OT>(v - to_f32(hv));
+          }
+          const unsigned r = (unsigned)qrow(q);
+          if (ncol) {
+            bo.st32(v, vo, r * (unsigned)p.ldo * 4u);
+            if (MODE != WIDE_WEIGHT || p.h) bh.st16(__builtin_bit_cast(unsigned short, hv), vh, r * (unsigned)p.ldh * (unsigned)sizeof(OT));
+            if (MODE == WIDE_WEIGHT && p.hl) bl.st16(__builtin_bit_cast(unsigned short, lv), vl, r * (unsigned)p.ldhl * (unsigned)sizeof(OT));
+            if (MODE == WIDE_INFER && p.out2) b2.st32(fv, v2, r * (unsigned)p.ld2 * 4u);
+          }
+          hs[q] = mb + (int)r < M ? __builtin_bit_cast(unsigned short, hv) : (unsigned short)0;  // padding stays zero
+        }
+        // rows 8 g + 4 elk + (0, 1) and (2, 3): two 4-byte LDS stores per group
+#pragma unroll
+        for (int q = 0; q < 16; q += 2) {
+          const int ml = ml0 + qrow(q);
+          *reinterpret_cast<unsigned*>(tl + nl * BM + ((((ml >> 3) ^ (nl & 31))) << 3) + (ml & 7)) =
+              (unsigned)hs[q] | ((unsigned)hs[q + 1] << 16);
+        }
+      }
+    if (!p.t) return;
+    __syncthreads();
+    OT* tcopy = reinterpret_cast<OT*>(p.t);
+#pragma unroll 4
+    for (int idx = tid; idx < BN * BM / 8; idx += NT) {
+      const int nl = idx / (BM / 8), c = idx % (BM / 8);
+      const int n = n0 + nl, m = m0 + c * 8;
+      if (n < N && m < M)  // the chunk's rows at or past M hold zeros (the copy's padding)
+        *reinterpret_cast<uint4*>(tcopy + (long long)n * p.ldt + m) =
+            *reinterpret_cast<const uint4*>(tl + nl * BM + ((c ^ (nl & 31)) << 3));
+    }
+    return;
+  }
   // The accumulator tile goes through LDS (the pipeline stages are free now)
   // so that every global access of the epilogue is coalesced: pass 1 walks
   // the tile row-major, 4 columns per thread (fp32 master, natural 16-bit
@@ -520,7 +647,7 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
       for (int q = 0; q < 4; ++q) {
 #pragma clang fp contract(off)
         const float a = cr[q];
-        const float x = PRE ? pre[PRE ? c0 + u : 0][q] : 0.0f;
+        const float x = PREF ? pre[PREF ? c0 + u : 0][q] : 0.0f;
         if (MODE == WIDE_PRED) {
           v[q] = x - a;                                              // eps
           hv[q] = cvt<OT>(v[q]);
@@ -626,7 +753,8 @@ inline bool problem_ok(int mode, int split, bool a32, const WideProblem& q) {
 template <typename OT, int MODE, int SPLIT, int ACT, bool BREG, int BM, int BN, int S, int WGM, int WGN,
           bool A32 = false>
 struct Cfg {
-  static constexpr int smem = smem_bytes(BM, BN, S, SPLIT == 2);
+  static constexpr int smem = smem_bytes(BM, BN, S, SPLIT == 2, is_s16(MODE));
+  static_assert(smem <= 160 * 1024, "a configuration's LDS exceeds the CU's 160 KB");
   static constexpr int BM_ = BM, BN_ = BN;
   static const void* fn() {
     return reinterpret_cast<const void*>(&dma_gemm_kernel<OT, MODE, SPLIT, ACT, BREG, BM, BN, S, WGM, WGN, A32>);

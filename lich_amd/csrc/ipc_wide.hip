@@ -18,18 +18,21 @@ using dma::Cfg;
 //   split-2 prediction: 128 x 256 (2 stages, waves 2 x 4): 281 us per launch on the wide
 //       configuration against 317 us for 128 x 128 (3 stages, 4 x 2), the alternative;
 //       256 x 128 (2 stages) measured 349 us
-//   inference: 128 x 256 (3 stages, 16 waves 4 x 4: 32 x 64 per wave, four waves per SIMD
-//       to hide the LDS and barrier latency): 180 us against 188 us for 128 x 256 with
-//       waves 2 x 4 and 183-188 us for 256 x 128 (3, 4 x 2)
-//   weight update: 128 x 256 (3, 4 x 4): 325 us against 337 us for 128 x 256 (3, 2 x 4),
-//       353 us for 256 x 128 (3, 4 x 2) and more for 128 x 128 (4 stages, 4 x 2)
+//   inference and weight update: 256 x 256 (2 stages, 8 waves 2 x 4: 128 x 64 per wave),
+//       finished from the registers (their fp32 tile exceeds the LDS): 170 and 268 us
+//       against 199 and 298 us for 128 x 256 (3 stages, 16 waves 4 x 4, LDS-staged
+//       epilogue), the previous defaults, in the same process; the wide step's main loops
+//       read half the LDS bytes per MFMA on 128 x 64 wave tiles.  Alternatives: 128 x 256
+//       with waves 4 x 4 or 2 x 4, 256 x 128 (3, 4 x 2) and, for the weight update,
+//       128 x 128 (4 stages, 4 x 2)
 #define WIDE_PRED1_CFGS(X) X(256, 128, 3, 4, 2) X(128, 256, 3, 2, 4)
 #define WIDE_PRED2_CFGS(X) X(128, 256, 2, 2, 4) X(128, 128, 3, 4, 2)
 // the split-2 prediction reading the fp32 W (a32): waves 4 x 2, so that each
 // wave splits its 32-row A fragment for 4 column blocks (two waves share it)
 #define WIDE_PRED2A_CFGS(X) X(128, 256, 2, 4, 2) X(128, 128, 3, 4, 2)
-#define WIDE_INFER_CFGS(X) X(128, 256, 3, 4, 4) X(128, 256, 3, 2, 4) X(256, 128, 3, 4, 2)
-#define WIDE_WEIGHT_CFGS(X) X(128, 256, 3, 4, 4) X(128, 256, 3, 2, 4) X(256, 128, 3, 4, 2) X(128, 128, 4, 4, 2)
+#define WIDE_INFER_CFGS(X) X(256, 256, 2, 2, 4) X(128, 256, 3, 4, 4) X(128, 256, 3, 2, 4) X(256, 128, 3, 4, 2)
+#define WIDE_WEIGHT_CFGS(X) \
+  X(256, 256, 2, 2, 4) X(128, 256, 3, 4, 4) X(128, 256, 3, 2, 4) X(256, 128, 3, 4, 2) X(128, 128, 4, 4, 2)
 #define IPC_COUNT1(...) +1
 constexpr int kPred1Cfgs = 0 WIDE_PRED1_CFGS(IPC_COUNT1), kPred2Cfgs = 0 WIDE_PRED2_CFGS(IPC_COUNT1);
 constexpr int kInferCfgs = 0 WIDE_INFER_CFGS(IPC_COUNT1), kWeightCfgs = 0 WIDE_WEIGHT_CFGS(IPC_COUNT1);

@@ -57,7 +57,7 @@ def test_wide_tuner_gates_candidates_and_configs_agree_bitwise(tmp_path):
     x_in = torch.randn((dims[-1], B), generator=g).to(DEV)
     y = torch.nn.functional.one_hot(torch.randint(0, dims[0], (B,), generator=g), dims[0]).float().T.contiguous().to(DEV)
     outs = []
-    for wc in ((-1, -1, -1, -1), (1, 1, 1, -1), (0, 0, 2, -1)):
+    for wc in ((-1, -1, -1, -1), (1, 1, 1, -1), (0, 0, 2, -1), (0, 3, 4, -1)):
         m = HipIPC(IPCConfig(dims=dims, activation="tanh", dtype=torch.bfloat16, fused="wide", wide_config=wc,
                              hierarchical_policy_auto=False), device=DEV, weights=w0)
         m.initialize_batch(x_in, y)
