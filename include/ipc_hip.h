@@ -62,13 +62,17 @@ extern "C" {
 /* tile configurations of the MFMA GEMM family; IPC_TILE_AUTO picks by shape.
  * IPC_TILE_DMA_* are the LDS-DMA kernel (operands streamed HBM -> LDS without
  * VGPR staging, transposed operands read with the LDS transpose read) in
- * three tile configurations: 256 x 128 (the automatic choice), 128 x 256 and
- * 128 x 128 (more tiles for small shapes).  They give bit-identical results
+ * four tile configurations: 256 x 128, 128 x 256,
+ * 128 x 128 (more tiles for small shapes) and 256 x 256 (8 waves of 128 x 64,
+ * half the LDS reads per MFMA, an epilogue from the registers; for large
+ * shapes).  They give bit-identical results
  * (the same k order) and serve 16-bit storage (storage == operand ==
  * fp16/bf16) with a contraction that is a multiple of 64, 16-byte aligned
  * tensors and, for operands read transposed, a contiguous extent that is a
- * multiple of 8; IPC_TILE_AUTO picks the 256 x 128 one whenever those hold,
- * and asking for a DMA tile otherwise is IPC_ERR_CONFIG.  The autotuner
+ * multiple of 8; IPC_TILE_AUTO picks the 256 x 256 one whenever those hold
+ * and its tiles fill every CU at least once (256 tiles or more over the
+ * groups), the 256 x 128 one when they hold otherwise; asking for a DMA tile
+ * where they do not hold is IPC_ERR_CONFIG.  The autotuner
  * searches all of them per shape. */
 #define IPC_TILE_AUTO (-1)
 #define IPC_TILE_32x32 0
@@ -77,7 +81,8 @@ extern "C" {
 #define IPC_TILE_DMA_256x128 3
 #define IPC_TILE_DMA_128x256 4
 #define IPC_TILE_DMA_128x128 5
-#define IPC_TILE_COUNT 6
+#define IPC_TILE_DMA_256x256 6
+#define IPC_TILE_COUNT 7
 
 /* weight-update backends of a plan */
 #define IPC_WMODE_GEMM 0

@@ -24,8 +24,8 @@ DT_F32, DT_F16, DT_BF16 = 0, 1, 2
 ACT_CODES = {"identity": 0, "linear": 0, "relu": 1, "tanh": 2, "sigmoid": 3, "silu": 4, "gelu": 5}
 TILE_AUTO = -1
 TILE_DMA = 3
-TILE_DMA_TILES = (3, 4, 5)  # LDS-DMA kernel: 256 x 128, 128 x 256, 128 x 128
-TILE_COUNT = 6
+TILE_DMA_TILES = (3, 4, 5, 6)  # LDS-DMA kernel: 256 x 128, 128 x 256, 128 x 128, 256 x 256
+TILE_COUNT = 7
 WMODE = {"gemm": 0, "outer": 1, "auto": 2}
 SPLIT_NONE, SPLIT_W, SPLIT_WX = 1, 2, 3
 PATH_AUTO, PATH_PHASED, PATH_NARROW, PATH_WIDE, PATH_RESIDENT = -1, 0, 1, 2, 3

@@ -24,8 +24,8 @@ this library's choices), every candidate gated on correctness.
   choices through the reference's precedence.
 
 * Standalone kernels with 16-bit storage (the per-kernel sweep's operator
-  calls, ``tune_standalone``): the generic tiles and the three LDS-DMA tile
-  configurations (256x128, 128x256, 128x128) per (kind, M, K, B), under the
+  calls, ``tune_standalone``): the generic tiles and the four LDS-DMA tile
+  configurations (256x128, 128x256, 128x128, 256x256) per (kind, M, K, B), under the
   same probe.
 * Layer-resident plans: the top layer's row-block size (16, 32 or 64 rows,
   ``ipc_plan_set_resident_rows``) is part of the execution search; every
@@ -56,7 +56,7 @@ from .reference import get_activation
 from .trainer import HipIPC, IPCConfig, init_weights_cpu
 from .tuning import TuningEntry, TuningKey, TuningTable, config_to_dict
 
-TILES = (0, 1, 2, 3, 4, 5)  # generic 32x32, 64x64, 128x128; LDS-DMA 256x128, 128x256, 128x128
+TILES = (0, 1, 2, 3, 4, 5, 6)  # generic 32x32, 64x64, 128x128; LDS-DMA 256x128, 128x256, 128x128, 256x256
 RESIDENT_ROWS = (16, 32, 64)
 RTOL = ATOL = 2e-2
 MAX_BAD = 0.01
@@ -184,7 +184,7 @@ def tune_standalone(points, activation: str, dtype: torch.dtype, *, reps: int = 
     """The operator calls with 16-bit storage (``dtype`` both storage and
     operand type), as the per-kernel sweep makes them: for every (M, K, B) of
     ``points`` the prediction, inference and weight kernels over every tile
-    (the three LDS-DMA configurations where the shape allows them), gated and
+    (the four LDS-DMA configurations where the shape allows them), gated and
     timed like ``tune_kernels``."""
     entries = []
     for M, K, B in points:

@@ -154,16 +154,20 @@ struct Buf {
   __device__ __forceinline__ void st16(unsigned short x, unsigned v, unsigned s) const {
     __builtin_amdgcn_raw_buffer_store_b16(x, r, v, s, 0);
   }
+  __device__ __forceinline__ unsigned short ld16(unsigned v, unsigned s) const {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, v, s, 0);
+  }
 };
 
 // Dynamic LDS of a configuration: the pipeline stages, reused by the fp32
 // epilogue tile (BM rows of BN + 1 floats) when that tile fits the CU's
-// 160 KB; a wide configuration whose tile does not (256 x 256) finishes from
-// the registers and stages only its 16-bit transposed copy (reg_epilogue).
+// 160 KB; a configuration whose tile does not (256 x 256) finishes from the
+// registers and stages only the wide path's 16-bit transposed copy
+// (reg_epilogue).
 // (LO: the A_lo block, or A stored as fp32 rows of twice the bytes.)
 constexpr int stage_bytes(int BM, int BN, int S, bool LO) { return S * (BM * 128 * (LO ? 2 : 1) + BN * 128); }
 constexpr bool reg_epilogue(int BM, int BN, int S, bool LO, bool s16) {
-  return !s16 && BM * (BN + 1) * 4 > 160 * 1024 && stage_bytes(BM, BN, S, LO) <= 160 * 1024;
+  return BM * (BN + 1) * 4 > 160 * 1024 && stage_bytes(BM, BN, S, LO) <= 160 * 1024;
 }
 constexpr int smem_bytes(int BM, int BN, int S, bool LO, bool s16 = true) {
   return reg_epilogue(BM, BN, S, LO, s16) || stage_bytes(BM, BN, S, LO) > BM * (BN + 1) * 4
@@ -524,16 +528,23 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
     // step.  The 16-bit transposed copy is staged in LDS as a [BN][BM] tile
     // (16-byte chunk c of row n at chunk c ^ (n % 32): conflict-free for both
     // passes, BM >= 256) and then written row by row, 16 bytes per lane.
+    // The standalone kernels' inputs and outputs are 16-bit (their rounding
+    // steps are those of the LDS path) and they have no transposed copy.
     static_assert(BM >= 256 && BN * BM * (int)sizeof(OT) <= stage_bytes(BM, BN, S, LO), "transposed tile");
     const int elr = lane & 31, elk = lane >> 5;
-    constexpr bool EIN = MODE == WIDE_INFER;
+    constexpr bool EIN = MODE == WIDE_INFER || MODE == S16_INFER;
+    constexpr unsigned ES = S16 ? (unsigned)sizeof(OT) : 4u;  // bytes of an input, output or out2 element
     const long long xld = pre_from_aux ? p.ldx : p.ldo;
-    const Buf bx(pre_from_aux ? p.aux : p.out, PRE ? (long long)M * xld * 4 : 0);
-    const Buf be(p.aux, EIN ? (long long)M * p.ldx * 4 : 0);
-    const Buf bo(p.out, (long long)M * p.ldo * 4);
-    const Buf bh(p.h, p.h ? (long long)M * p.ldh * (long long)sizeof(OT) : 0);
-    const Buf bl(p.hl, p.hl ? (long long)M * p.ldhl * (long long)sizeof(OT) : 0);
-    const Buf b2(p.out2, p.out2 ? (long long)M * p.ld2 * 4 : 0);
+    const Buf bx(pre_from_aux ? p.aux : p.out, PRE ? (long long)M * xld * ES : 0);
+    const Buf be(p.aux, EIN ? (long long)M * p.ldx * ES : 0);
+    const Buf bo(p.out, (long long)M * p.ldo * ES);
+    const Buf bh(p.h, !S16 && p.h ? (long long)M * p.ldh * (long long)sizeof(OT) : 0);
+    const Buf bl(p.hl, !S16 && p.hl ? (long long)M * p.ldhl * (long long)sizeof(OT) : 0);
+    const Buf b2(p.out2, p.out2 ? (long long)M * p.ld2 * ES : 0);
+    auto ldin = [&](const Buf& b, unsigned v, unsigned s) -> float {
+      if constexpr (S16) return to_f32(__builtin_bit_cast(OT, b.ld16(v, s)));
+      else return b.ld32(v, s);
+    };
     unsigned short* tl = reinterpret_cast<unsigned short*>(smem);
     wait_vmcnt<0>();
     __syncthreads();  // every wave is done with the pipeline stages
@@ -546,14 +557,14 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
         const int ml0 = wm * WTM + i * 32 + 4 * elk, mb = m0 + ml0;
         const bool ncol = n < N;
         float xin[PRE ? 16 : 1], ein[EIN ? 16 : 1];
-        const unsigned vx = (unsigned)(mb * xld + n) * 4u, ve = (unsigned)(mb * p.ldx + n) * 4u;
+        const unsigned vx = (unsigned)(mb * xld + n) * ES, ve = (unsigned)(mb * p.ldx + n) * ES;
 #pragma unroll
         for (int q = 0; q < 16; ++q) {
-          if constexpr (PRE) xin[PRE ? q : 0] = ncol ? bx.ld32(vx, (unsigned)(qrow(q) * xld) * 4u) : 0.0f;
-          if constexpr (EIN) ein[EIN ? q : 0] = ncol ? be.ld32(ve, (unsigned)(qrow(q) * p.ldx) * 4u) : 0.0f;
+          if constexpr (PRE) xin[PRE ? q : 0] = ncol ? ldin(bx, vx, (unsigned)(qrow(q) * xld) * ES) : 0.0f;
+          if constexpr (EIN) ein[EIN ? q : 0] = ncol ? ldin(be, ve, (unsigned)(qrow(q) * p.ldx) * ES) : 0.0f;
         }
-        const unsigned vo = (unsigned)(mb * p.ldo + n) * 4u, vh = (unsigned)(mb * p.ldh + n) * (unsigned)sizeof(OT),
-                       vl = (unsigned)(mb * p.ldhl + n) * (unsigned)sizeof(OT), v2 = (unsigned)(mb * p.ld2 + n) * 4u;
+        const unsigned vo = (unsigned)(mb * p.ldo + n) * ES, vh = (unsigned)(mb * p.ldh + n) * (unsigned)sizeof(OT),
+                       vl = (unsigned)(mb * p.ldhl + n) * (unsigned)sizeof(OT), v2 = (unsigned)(mb * p.ld2 + n) * ES;
         unsigned short hs[16];
 #pragma unroll
         for (int q = 0; q < 16; ++q) {
@@ -573,20 +584,38 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
             v = a;                                                    // x = W f(x_upper)
             fv = act_t<ACT>(v);
             hv = cvt<OT>(fv);
-          } else {
+          } else if (MODE == WIDE_WEIGHT) {
             v = x + p.scal * a;                                       // W_new
             hv = cvt<OT>(v);
             lv = cvt<OT>(v - to_f32(hv));
+          } else if (MODE == S16_PRED) {
+            // tilelang_kernels.py:173: E = cast(X_lower) - cast(acc) in storage precision
+            hv = cvt<OT>(x - to_f32(cvt<OT>(a)));
+          } else if (MODE == S16_FWD) {
+            hv = cvt<OT>(a);
+          } else if (MODE == S16_INFER) {
+            const float xn = x + p.scal * (-ein[EIN ? q : 0] + dact_t<ACT>(x) * a);
+            hv = cvt<OT>(xn);
+            lv = cvt<OT>(act_t<ACT>(xn));                              // A_out
+          } else {
+            // tilelang_kernels.py:319-320: W = cast(float(W) + alpha * acc)
+            hv = cvt<OT>(x + p.scal * a);
           }
           const unsigned r = (unsigned)qrow(q);
           if (ncol) {
-            bo.st32(v, vo, r * (unsigned)p.ldo * 4u);
-            if (MODE != WIDE_WEIGHT || p.h) bh.st16(__builtin_bit_cast(unsigned short, hv), vh, r * (unsigned)p.ldh * (unsigned)sizeof(OT));
-            if (MODE == WIDE_WEIGHT && p.hl) bl.st16(__builtin_bit_cast(unsigned short, lv), vl, r * (unsigned)p.ldhl * (unsigned)sizeof(OT));
-            if (MODE == WIDE_INFER && p.out2) b2.st32(fv, v2, r * (unsigned)p.ld2 * 4u);
+            if constexpr (S16) {
+              bo.st16(__builtin_bit_cast(unsigned short, hv), vo, r * (unsigned)p.ldo * ES);
+              if (MODE == S16_INFER && p.out2) b2.st16(__builtin_bit_cast(unsigned short, lv), v2, r * (unsigned)p.ld2 * ES);
+            } else {
+              bo.st32(v, vo, r * (unsigned)p.ldo * 4u);
+              if (MODE != WIDE_WEIGHT || p.h) bh.st16(__builtin_bit_cast(unsigned short, hv), vh, r * (unsigned)p.ldh * (unsigned)sizeof(OT));
+              if (MODE == WIDE_WEIGHT && p.hl) bl.st16(__builtin_bit_cast(unsigned short, lv), vl, r * (unsigned)p.ldhl * (unsigned)sizeof(OT));
+              if (MODE == WIDE_INFER && p.out2) b2.st32(fv, v2, r * (unsigned)p.ld2 * 4u);
+            }
           }
           hs[q] = mb + (int)r < M ? __builtin_bit_cast(unsigned short, hv) : (unsigned short)0;  // padding stays zero
         }
+        if constexpr (S16) continue;
         // rows 8 g + 4 elk + (0, 1) and (2, 3): two 4-byte LDS stores per group
 #pragma unroll
         for (int q = 0; q < 16; q += 2) {
@@ -595,7 +624,7 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
               (unsigned)hs[q] | ((unsigned)hs[q + 1] << 16);
         }
       }
-    if (!p.t) return;
+    if (S16 || !p.t) return;
     __syncthreads();
     OT* tcopy = reinterpret_cast<OT*>(p.t);
 #pragma unroll 4
@@ -613,7 +642,7 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
   // the tile row-major, 4 columns per thread (fp32 master, natural 16-bit
   // copy), pass 2 column-major (the transposed 16-bit copy of the wide path).
   constexpr int CS = BN + 1;  // fp32 row stride: conflict-free column walk in pass 2
-  static_assert(BM * CS * 4 <= smem_bytes(BM, BN, S, LO), "epilogue tile exceeds the LDS");
+  static_assert(REG || BM * CS * 4 <= smem_bytes(BM, BN, S, LO), "epilogue tile exceeds the LDS");
   float* cs = reinterpret_cast<float*>(smem);
   wait_vmcnt<0>();
   __syncthreads();

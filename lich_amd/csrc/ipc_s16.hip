@@ -84,6 +84,7 @@ hipError_t launch_s16(int mode, const WideProblem* probs, int count, int operand
     case 0: return Tiles0::launch(mode, probs, count, operand, act, s);
     case 1: return s16::launch_tiles1(mode, probs, count, operand, act, s);
     case 2: return s16::launch_tiles2(mode, probs, count, operand, act, s);
+    case 3: return s16::launch_tiles3(mode, probs, count, operand, act, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -1,7 +1,7 @@
 // ipc_s16_tiles.h - the tile configurations of the standalone 16-bit-storage
 // kernels (operator API, src/ipc_tilelang/tilelang_kernels.py:114-349) on the
 // LDS-DMA MFMA kernel of ipc_dma_gemm.h.  Each configuration is compiled in a
-// translation unit of its own (ipc_s16.hip, ipc_s16_t1.hip, ipc_s16_t2.hip)
+// translation unit of its own (ipc_s16.hip, ipc_s16_t1.hip .. ipc_s16_t3.hip)
 // and chosen per call by its tile id, which is what the autotuner searches.
 // The k order, and so every result bit, does not depend on the configuration.
 #pragma once
@@ -48,8 +48,11 @@ struct Tiles {
 // of 64 x 64), 3 stages.  Configuration 2: 128 x 128 tiles, 4 waves of
 // 64 x 64, 2 stages (66 KB of LDS: two workgroups per CU), for shapes with
 // few tiles.
+// Configuration 3: 256 x 256 tiles, 8 waves of 128 x 64, 2 stages, finished
+// from the registers (the fp32 tile exceeds the LDS).
 hipError_t launch_tiles1(int mode, const WideProblem* probs, int count, int operand, int act, hipStream_t s);
 hipError_t launch_tiles2(int mode, const WideProblem* probs, int count, int operand, int act, hipStream_t s);
+hipError_t launch_tiles3(int mode, const WideProblem* probs, int count, int operand, int act, hipStream_t s);
 
 }  // namespace s16
 }  // namespace ipc

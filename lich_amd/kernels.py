@@ -36,8 +36,8 @@ class KernelConfig:
 
     ``tile`` selects one of the CDNA4 MFMA tile shapes of the library
     (generic kernel 0: 32x32, 1: 64x64, 2: 128x128; LDS-DMA kernel for 16-bit
-    storage 3: 256x128, 4: 128x256, 5: 128x128; -1: chosen from the problem
-    shape).  When
+    storage 3: 256x128, 4: 128x256, 5: 128x128, 6: 256x256; -1: chosen from
+    the problem shape).  When
     ``tile`` is None the reference's ``block_m``/``block_n`` pick the closest
     shape; with neither given the choice is automatic.
     """

@@ -507,7 +507,7 @@ def test_noalloc_entry_point_validates_on_the_host():
 def test_wide_tile_configurations_are_selectable_before_bind():
     lib = _lib()
     assert lib.ipc_plan_wide_config_count(0, nat.SPLIT_W) == 2 and lib.ipc_plan_wide_config_count(0, 1) == 2
-    assert lib.ipc_plan_wide_config_count(1, 1) == 3 and lib.ipc_plan_wide_config_count(2, 1) == 4
+    assert lib.ipc_plan_wide_config_count(1, 1) == 4 and lib.ipc_plan_wide_config_count(2, 1) == 5
     assert lib.ipc_plan_wide_config_count(0, nat.SPLIT_WX) == 0 and lib.ipc_plan_wide_config_count(7, 1) == 0
     assert lib.ipc_plan_set_wide_config(None, 0, 0, 0, -1) == nat.ERR_NULL
     dims = (ctypes.c_int * 4)(10, 64, 64, 784)
@@ -522,7 +522,7 @@ def test_wide_tile_configurations_are_selectable_before_bind():
     try:
         base = lib.ipc_plan_workspace_bytes(h)
         assert lib.ipc_plan_set_wide_config(h, 2, 0, 0, -1) == nat.ERR_CONFIG   # split-2 prediction has 0..1
-        assert lib.ipc_plan_set_wide_config(h, 0, 0, 4, -1) == nat.ERR_CONFIG   # weight has 0..3
+        assert lib.ipc_plan_set_wide_config(h, 0, 0, 5, -1) == nat.ERR_CONFIG   # weight has 0..4
         assert lib.ipc_plan_set_wide_config(h, 0, 0, 0, 3) == nat.ERR_CONFIG    # not a power of two
         assert lib.ipc_plan_set_wide_config(h, -1, 1, 2, 8) == nat.IPC_OK
         assert lib.ipc_plan_workspace_bytes(h) == base                          # same prediction tile
@@ -625,7 +625,7 @@ def test_resident_row_blocks_are_a_plan_option():
 
 
 def test_dma_tile_ids_are_refused_where_the_dma_kernel_cannot_run():
-    """The three LDS-DMA tile ids need 16-bit storage and a contraction of
+    """The LDS-DMA tile ids need 16-bit storage and a contraction of
     whole 64-k steps; asked for otherwise they are an error, never a silent
     fallback; an id past the table is unknown."""
     lib = _lib()

@@ -88,7 +88,7 @@ def test_wide_tuner_gates_candidates_and_configs_agree_bitwise(tmp_path):
 
 def test_standalone_tuner_searches_the_dma_tiles_and_the_choice_reaches_the_builders():
     """The operator calls with bf16 storage at a per-kernel sweep shape: the
-    three LDS-DMA tile configurations are candidates; one that fails the probe
+    LDS-DMA tile configurations are candidates; one that fails the probe
     is never selected (however fast), and the chosen tile is what a builder
     given the table's config runs."""
     from lich_amd.kernels import build_prediction_error

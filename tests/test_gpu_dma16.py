@@ -281,7 +281,7 @@ def test_default_standalone_calls_allocate_no_device_memory():
 @pytest.mark.parametrize("act", ["relu", "tanh", "identity"])
 @pytest.mark.parametrize("M,K,B", [(296, 192, 136), (1000, 256, 264), (64, 128, 8)])
 def test_dma_tile_configurations_agree(M, K, B, act, op):
-    """The three LDS-DMA tile configurations (the autotuner's search space
+    """The LDS-DMA tile configurations (the autotuner's search space
     for the standalone calls) add the contraction in the same k order with
     the same epilogue: prediction, forward, inference (with A_out) and both
     weight updates agree with the default configuration bit for bit for relu
@@ -296,7 +296,9 @@ def test_dma_tile_configurations_agree(M, K, B, act, op):
     Bw = 128
     ew, xw, w0 = _t(randn((M, Bw), g), dt), _t(randn((K, Bw), g), dt), _t(randn((M, K), g, 1 / math.sqrt(K)), dt)
     res = {}
-    for tile in (3, 4, 5):
+    from lich_amd import _native as nat
+
+    for tile in nat.TILE_DMA_TILES:
         cfg = KernelConfig(tile=tile)
         ep = torch.empty((M, B), device=DEV, dtype=dt)
         fp = torch.empty((M, B), device=DEV, dtype=dt)
@@ -311,6 +313,6 @@ def test_dma_tile_configurations_agree(M, K, B, act, op):
         build_weight_update(M, K, Bw, act, dt, cfg, 0.01, False)(ws, ew, xw)
         res[tile] = (ep, fp, x, a, wr, ws)
     torch.cuda.synchronize()
-    for tile in (4, 5):
+    for tile in nat.TILE_DMA_TILES[1:]:
         for i, (u, v) in enumerate(zip(res[3], res[tile])):
             assert _same(v, u, act), (tile, i)
