@@ -68,3 +68,27 @@ def test_whole_step_plan_replays_of_a_torch_graph_equal_direct_launches(path, di
             assert torch.equal(a, b), (r, i, float((a - b).abs().max()))
     graphed.check_steps()
     del g
+
+
+def test_stream_handle_follows_the_current_stream_and_the_capture_stream():
+    """The handle every library call launches on is torch's current stream,
+    read at call time: the default stream, a side stream inside its context
+    manager, and the capture stream inside torch.cuda.graph."""
+    from lich_amd import _native as nat
+
+    report("stream-handle")
+    assert nat.current_stream_handle() == torch.cuda.current_stream().cuda_stream
+    assert nat.current_stream_handle(DEV) == torch.cuda.current_stream(DEV).cuda_stream
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        assert nat.current_stream_handle(DEV) == side.cuda_stream
+        assert nat.current_stream_handle() == side.cuda_stream
+    seen = []
+    g = torch.cuda.CUDAGraph()
+    x = torch.zeros(4, device=DEV)
+    with torch.cuda.graph(g):
+        seen.append((nat.current_stream_handle(DEV), torch.cuda.current_stream(DEV).cuda_stream))
+        x.add_(1.0)
+    g.replay()
+    torch.cuda.synchronize()
+    assert seen[0][0] == seen[0][1] and seen[0][0] != torch.cuda.current_stream(DEV).cuda_stream
