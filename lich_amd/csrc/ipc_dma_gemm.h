@@ -169,6 +169,13 @@ constexpr int stage_bytes(int BM, int BN, int S, bool LO) { return S * (BM * 128
 constexpr bool reg_epilogue(int BM, int BN, int S, bool LO, bool s16) {
   return BM * (BN + 1) * 4 > 160 * 1024 && stage_bytes(BM, BN, S, LO) <= 160 * 1024;
 }
+// The split-2 prediction reading the fp32 W (A32) with 2 stages takes a third
+// A stage when the LDS holds it (128 x 256: 3 x 32 + 2 x 32 KB = 160 KB): in
+// the wide configuration's steady state 299-304 us per launch against
+// 311-314 us, bit-identical.
+constexpr bool a32_extra_stage(int BM, int BN, int S, bool a32) {
+  return a32 && S == 2 && (S + 1) * BM * 256 + S * BN * 128 <= 160 * 1024;
+}
 constexpr int smem_bytes(int BM, int BN, int S, bool LO, bool s16 = true) {
   return reg_epilogue(BM, BN, S, LO, s16) || stage_bytes(BM, BN, S, LO) > BM * (BN + 1) * 4
              ? stage_bytes(BM, BN, S, LO)
@@ -218,6 +225,11 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
   constexpr int STAGE = A_BYTES * A_BLOCKS + B_BYTES;
   constexpr int IA = A_BYTES / 1024 / NW, IB = B_BYTES / 1024 / NW;  // DMA instructions per wave and stage
   constexpr int LPS = IA * A_BLOCKS + (BREG ? 0 : IB);
+  // A32 with 2 stages: the fp32 W, which each row block's few column tiles
+  // read from far, takes a third stage where the LDS holds it, so its loads
+  // lead by two k-steps, while the 16-bit B block (shared by every row tile,
+  // an L2 hit) keeps two: the A ring first in the LDS, then the B ring.
+  constexpr int AX = a32_extra_stage(BM, BN, S, A32) ? 1 : 0, SA = S + AX;
   constexpr int RB = B_BYTES / 16 / NT;                               // register-path chunks per thread
   constexpr int WTM = BM / WGM, WTN = BN / WGN, RM = WTM / 32, RN = WTN / 32;
   using MF = Mfma32<OT>;
@@ -259,8 +271,12 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
   const int alim = p.a_lim, blim = p.b_lim;
   const int nk = kslice / WIDE_BK, kbase = slice * kslice;
 
-  auto issue_dma = [&](int kt, int stage) {
-    unsigned char* st = smem + stage * STAGE;
+  // stage i's A block (its A_lo block follows it) and B block
+  auto a_stage = [&](int i) -> unsigned char* { return AX ? smem + i * A_BYTES : smem + i * STAGE; };
+  auto b_stage = [&](int i) -> unsigned char* {
+    return AX ? smem + SA * A_BYTES + i * B_BYTES : smem + i * STAGE + A_BYTES * A_BLOCKS;
+  };
+  auto issue_a = [&](int kt, unsigned char* st) {
     const int k0 = kbase + kt * WIDE_BK;
 #pragma unroll
     for (int q = 0; q < IA; ++q) {
@@ -277,15 +293,19 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
         }
       }
     }
-    if (!BREG) {
+  };
+  auto issue_b = [&](int kt, unsigned char* st) {
+    const int k0 = kbase + kt * WIDE_BK;
 #pragma unroll
-      for (int q = 0; q < IB; ++q) {
-        const int blk = q * NW + w;
-        const OT* src = slot_src<OT, BMN, BN>(Bg, ldb, n0, blim, k0, blk * 64 + lane);
-        __builtin_amdgcn_global_load_lds((glb_void*)src, (lds_void*)(st + A_BYTES * A_BLOCKS + blk * 1024),
-                                         16, 0, 0);
-      }
+    for (int q = 0; q < IB; ++q) {
+      const int blk = q * NW + w;
+      const OT* src = slot_src<OT, BMN, BN>(Bg, ldb, n0, blim, k0, blk * 64 + lane);
+      __builtin_amdgcn_global_load_lds((glb_void*)src, (lds_void*)(st + blk * 1024), 16, 0, 0);
     }
+  };
+  auto issue_dma = [&](int kt, int stage) {
+    issue_a(kt, a_stage(stage));
+    if (!BREG) issue_b(kt, b_stage(stage));
   };
   // register path of the B operand: 16-byte chunks of the stage's B block
   uint4 breg[BREG ? RB : 1];
@@ -377,6 +397,7 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
       }
     }
   }
+  if (AX && S - 1 < nk) issue_a(S - 1, a_stage(S - 1));  // the extra A stage's first fill
 
   // lane-constant parts of the fragment addresses
   const int lr = lane & 31, lk = lane >> 5;         // k-contiguous reads: row, 8-k half
@@ -419,22 +440,32 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
     return frag_kc(blk, wn * WTN + j * 32, kk);
   };
 
-  int stage = 0, fill = S - 1;
+  int stage = 0, fill = S - 1, astage = 0;
 #pragma unroll 1
   for (int kt = 0; kt < nk; ++kt) {
-    // this wave's DMA loads of step kt are done once at most S-2 later steps are in flight
-    if (kt + S - 2 < nk) wait_vmcnt<(S - 2) * LPS>();
-    else wait_vmcnt<0>();
+    if constexpr (AX) {
+      // issue order per step: B(kt + 1), then A(kt + 2); step kt's A and B are
+      // done once at most the last A fill, A(kt + 1), is in flight
+      if (kt + 1 < nk) wait_vmcnt<IA>();
+      else wait_vmcnt<0>();
+    } else {
+      // this wave's DMA loads of step kt are done once at most S-2 later steps are in flight
+      if (kt + S - 2 < nk) wait_vmcnt<(S - 2) * LPS>();
+      else wait_vmcnt<0>();
+    }
     wg_barrier();
     const bool refill = kt + S - 1 < nk;
-    if (refill) {
+    if constexpr (AX) {
+      if (refill) issue_b(kt + S - 1, b_stage(fill));
+      if (kt + SA - 1 < nk) issue_a(kt + SA - 1, a_stage(astage == 0 ? SA - 1 : astage - 1));
+    } else if (refill) {
       issue_breg(kt + S - 1);
       issue_dma(kt + S - 1, fill);
     }
 
-    const unsigned char* sa = smem + stage * STAGE;
+    const unsigned char* sa = a_stage(AX ? astage : stage);
     const unsigned char* sal = sa + A_BYTES;
-    const unsigned char* sb = sa + A_BYTES * A_BLOCKS;
+    const unsigned char* sb = b_stage(stage);
     V af[2][RM], bf[2][RN], alf[2][LO ? RM : 1];
     // Software pipeline over the 16-k slices of the stage: the reads of
     // slice kk+1 go out while slice kk's MFMAs run.  A scheduling barrier
@@ -498,6 +529,7 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
     }
     stage = stage + 1 == S ? 0 : stage + 1;
     fill = fill + 1 == S ? 0 : fill + 1;
+    astage = astage + 1 == SA ? 0 : astage + 1;
   }
 
   // ------------------------------------------------------------ epilogue
@@ -841,7 +873,11 @@ inline bool problem_ok(int mode, int split, bool a32, const WideProblem& q) {
 template <typename OT, int MODE, int SPLIT, int ACT, bool BREG, int BM, int BN, int S, int WGM, int WGN,
           bool A32 = false>
 struct Cfg {
-  static constexpr int smem = smem_bytes(BM, BN, S, SPLIT == 2, is_s16(MODE));
+  static constexpr int smem = a32_extra_stage(BM, BN, S, A32)
+                                  ? (S + 1) * BM * 256 + S * BN * 128 > smem_bytes(BM, BN, S, true, false)
+                                        ? (S + 1) * BM * 256 + S * BN * 128
+                                        : smem_bytes(BM, BN, S, true, false)
+                                  : smem_bytes(BM, BN, S, SPLIT == 2, is_s16(MODE));
   static_assert(smem <= 160 * 1024, "a configuration's LDS exceeds the CU's 160 KB");
   static constexpr int BM_ = BM, BN_ = BN;
   static const void* fn() {

@@ -28,7 +28,9 @@ using dma::Cfg;
 #define WIDE_PRED1_CFGS(X) X(256, 128, 3, 4, 2) X(128, 256, 3, 2, 4)
 #define WIDE_PRED2_CFGS(X) X(128, 256, 2, 2, 4) X(128, 128, 3, 4, 2)
 // the split-2 prediction reading the fp32 W (a32): waves 4 x 2, so that each
-// wave splits its 32-row A fragment for 4 column blocks (two waves share it)
+// wave splits its 32-row A fragment for 4 column blocks (two waves share it);
+// on 128 x 256 tiles the W block has three stages and the B block two
+// (a32_extra_stage)
 #define WIDE_PRED2A_CFGS(X) X(128, 256, 2, 4, 2) X(128, 128, 3, 4, 2)
 #define WIDE_INFER_CFGS(X) X(256, 256, 2, 2, 4) X(128, 256, 3, 4, 4) X(128, 256, 3, 2, 4) X(256, 128, 3, 4, 2)
 #define WIDE_WEIGHT_CFGS(X) \
