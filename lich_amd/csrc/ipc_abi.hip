@@ -277,9 +277,20 @@ int run_s16(int mode, const WideProblem& q, int groups, long long a_gs, long lon
   hipStream_t s = (hipStream_t)stream;
   const long long need = s16_workspace_need(mode, act, q.M, b_gs, groups);
   if (need > 0 && workspace && ws_bytes >= need) {
-    const long long n = (long long)groups * b_gs;  // the groups' B operands are contiguous, b_gs apart
     WideProblem qa = q;
     qa.b = workspace;
+    if (mode == S16_PRED || mode == S16_FWD) {
+      // f(X_upper [K][B])^T into the workspace: the GEMM then reads both
+      // operands k-contiguous (plain 16-byte fragment reads instead of the
+      // transposing ones), with the same values in the same k order
+      qa.ldb = q.K;
+      qa.b_lim = q.N;
+      const std::vector<WideProblem> v = s16_groups(qa, groups, a_gs, b_gs, o_gs, x_gs, o2_gs);
+      TRY(launch_rc(launch_s16_activate_t(q.b, workspace, q.K, q.N, groups, b_gs, operand, act, s), what));
+      return launch_rc(launch_s16(mode == S16_PRED ? S16_PREDT : S16_FWDT, v.data(), groups, operand,
+                                  IPC_ACT_IDENTITY, cfg, s), what);
+    }
+    const long long n = (long long)groups * b_gs;  // the groups' B operands are contiguous, b_gs apart
     const std::vector<WideProblem> v = s16_groups(qa, groups, a_gs, b_gs, o_gs, x_gs, o2_gs);
     TRY(launch_rc(launch_s16_activate(q.b, workspace, n, operand, act, s), what));
     return launch_rc(launch_s16(mode, v.data(), groups, operand, IPC_ACT_IDENTITY, cfg, s), what);

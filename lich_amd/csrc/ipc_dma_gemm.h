@@ -72,12 +72,16 @@ __device__ __forceinline__ void wg_barrier() {
 // Operand layouts: A is m-contiguous (read transposed) for the standalone
 // inference update (W_lower [K][M]), k-contiguous otherwise; B is
 // n-contiguous for the standalone prediction / forward / inference kernels
-// (X_upper, E_lower [K][B]), k-contiguous for the weight update.  The wide
+// (X_upper, E_lower [K][B]), k-contiguous for the weight update and for the
+// prediction / forward given f(X_upper)^T (S16_PREDT / S16_FWDT).  The wide
 // path keeps k-contiguous copies of every operand (WT, FT, ET next to W, F,
 // E), so all of its reads are plain 16-byte fragment reads.
 constexpr bool a_mn(int mode) { return mode == S16_INFER; }
 constexpr bool b_mn(int mode) { return mode == S16_PRED || mode == S16_FWD || mode == S16_INFER; }
 constexpr bool is_s16(int mode) { return mode >= S16_PRED; }
+// the standalone prediction / forward, with B as given or as f(X_upper)^T
+constexpr bool s16_pred(int mode) { return mode == S16_PRED || mode == S16_PREDT; }
+constexpr bool s16_fwd(int mode) { return mode == S16_FWD || mode == S16_FWDT; }
 
 // chunk position of chunk c in row r
 __device__ __forceinline__ int kc_swz(int r, int c) { return c ^ ((r >> 1) & 7); }
@@ -364,9 +368,9 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
       }
     }
   };
-  constexpr bool PRE = MODE != WIDE_FWD && MODE != S16_FWD;
+  constexpr bool PRE = MODE != WIDE_FWD && !s16_fwd(MODE);
   constexpr bool REG = reg_epilogue(BM, BN, S, LO, S16);
-  const bool pre_from_aux = MODE == WIDE_PRED || MODE == S16_PRED;
+  const bool pre_from_aux = MODE == WIDE_PRED || s16_pred(MODE);
   // the register epilogue loads its input block by block after the main loop
   // (fetched here, IT groups of 4 would take the accumulators' registers)
   constexpr bool PREF = PRE && !REG;
@@ -620,10 +624,10 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
           const float a = acc[i][j][q];
           const float x = PRE ? xin[cur][PRE ? q : 0] : 0.0f;
           OT hv, lv;
-          if (MODE == S16_PRED) {
+          if (s16_pred(MODE)) {
             // tilelang_kernels.py:173: E = cast(X_lower) - cast(acc) in storage precision
             hv = cvt<OT>(x - to_f32(cvt<OT>(a)));
-          } else if (MODE == S16_FWD) {
+          } else if (s16_fwd(MODE)) {
             hv = cvt<OT>(a);
           } else if (MODE == S16_INFER) {
             const float xn = x + s_scal * (-ein[cur][EIN ? q : 0] + dact_t<ACT>(x) * a);
@@ -679,10 +683,10 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
             v = x + p.scal * a;                                       // W_new
             hv = cvt<OT>(v);
             lv = cvt<OT>(v - to_f32(hv));
-          } else if (MODE == S16_PRED) {
+          } else if (s16_pred(MODE)) {
             // tilelang_kernels.py:173: E = cast(X_lower) - cast(acc) in storage precision
             hv = cvt<OT>(x - to_f32(cvt<OT>(a)));
-          } else if (MODE == S16_FWD) {
+          } else if (s16_fwd(MODE)) {
             hv = cvt<OT>(a);
           } else if (MODE == S16_INFER) {
             const float xn = x + p.scal * (-ein[EIN ? q : 0] + dact_t<ACT>(x) * a);
@@ -783,10 +787,10 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
           v[q] = x + p.scal * a;                                     // W_new
           hv[q] = cvt<OT>(v[q]);
           lv[q] = cvt<OT>(v[q] - to_f32(hv[q]));
-        } else if (MODE == S16_PRED) {
+        } else if (s16_pred(MODE)) {
           // tilelang_kernels.py:173: E = cast(X_lower) - cast(acc) in storage precision
           hv[q] = cvt<OT>(x - to_f32(cvt<OT>(a)));
-        } else if (MODE == S16_FWD) {
+        } else if (s16_fwd(MODE)) {
           hv[q] = cvt<OT>(a);
         } else if (MODE == S16_INFER) {
           const float xn = x + p.scal * (-ein[u][q] + dact_t<ACT>(x) * a);

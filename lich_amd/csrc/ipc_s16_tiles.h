@@ -25,6 +25,16 @@ struct Tiles {
           case S16_PRED: return dma::Cfg<OT, S16_PRED, 1, ACT, R, BM, BN, S, PM, PN>::launch(probs, count, s);
           case S16_FWD: return dma::Cfg<OT, S16_FWD, 1, ACT, R, BM, BN, S, PM, PN>::launch(probs, count, s);
           case S16_INFER: return dma::Cfg<OT, S16_INFER, 1, ACT, false, BM, BN, S, PM, PN>::launch(probs, count, s);
+          case S16_PREDT:
+          case S16_FWDT:
+            // f(X_upper)^T from a caller workspace: the activation is applied
+            if constexpr (ACT == ACT_IDENTITY) {
+              if (mode == S16_PREDT)
+                return dma::Cfg<OT, S16_PREDT, 1, ACT, false, BM, BN, S, PM, PN>::launch(probs, count, s);
+              return dma::Cfg<OT, S16_FWDT, 1, ACT, false, BM, BN, S, PM, PN>::launch(probs, count, s);
+            } else {
+              return hipErrorInvalidValue;
+            }
           default: return dma::Cfg<OT, S16_WEIGHT, 1, ACT, R, BM, BN, S, WM, WN>::launch(probs, count, s);
         }
       }

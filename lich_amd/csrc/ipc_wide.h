@@ -48,6 +48,9 @@ constexpr int WIDE_MAX_BATCH = 16;  // problems per launch
 enum {
   WIDE_PRED = 0, WIDE_INFER = 1, WIDE_WEIGHT = 2, WIDE_FWD = 3,
   S16_PRED = 4, S16_FWD = 5, S16_INFER = 6, S16_WEIGHT = 7,
+  // S16_PRED / S16_FWD whose B operand is f(X_upper)^T [N][K] (k-contiguous,
+  // ldb = K): the copy a caller workspace holds after launch_s16_activate_t
+  S16_PREDT = 8, S16_FWDT = 9,
 };
 
 inline long long wide_pad(long long v, long long m) { return (v + m - 1) / m * m; }
@@ -126,6 +129,11 @@ hipError_t launch_s16(int mode, const WideProblem* probs, int count, int operand
 // S16_PRED / S16_FWD / recomputing S16_WEIGHT call evaluated once, so that the
 // call then runs with ACT_IDENTITY on the LDS-DMA path for that operand.
 hipError_t launch_s16_activate(const void* in, void* out, long long n, int operand, int act, hipStream_t s);
+// The same values transposed: out[g][b][k] = cvt(f(in[g][k][b])) for `groups`
+// [K][B] operands gstride elements apart (the copies gstride apart as well):
+// the B operand of S16_PREDT / S16_FWDT.
+hipError_t launch_s16_activate_t(const void* in, void* out, int K, int B, int groups, long long gstride,
+                                 int operand, int act, hipStream_t s);
 
 // Refresh of the 16-bit copies from the fp32 masters (after the masters were
 // written outside a step):

@@ -204,6 +204,46 @@ def test_preactivated_operand_gives_the_register_path_bits(M, K, B, G, act, op):
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("op", ["f16", "bf16"])
+@pytest.mark.parametrize("act", ["relu", "tanh"])
+@pytest.mark.parametrize("M,K,B,G", [(296, 192, 136, 1), (512, 256, 520, 1), (256, 256, 72, 3)])
+def test_transposed_preactivation_matches_the_loader_on_every_tile(M, K, B, G, act, op):
+    """With a workspace, the prediction and forward evaluate f(X_upper) once
+    and store it transposed ([B][K]), so that the GEMM reads both operands
+    k-contiguous: on every LDS-DMA tile configuration (256 x 256 finishes from
+    the registers), for ragged batch widths (the transposing pass's edges)
+    and grouped calls, the results equal the loader path's bit for bit."""
+    from lich_amd import _native as nat
+
+    report("dma16-preact-t", M=M, K=K, B=B, G=G, act=act, op=op)
+    dt = OPS[op]
+    g = gen(5 * M + 3 * K + B + G)
+    xu, w, xl = _t(randn((G, K, B), g), dt), _t(randn((G, M, K), g, 1 / math.sqrt(K)), dt), _t(randn((G, M, B), g), dt)
+    try:
+        _preact(1)
+        for tile in nat.TILE_DMA_TILES:
+            cfg = KernelConfig(tile=tile)
+            out = {}
+            for use_ws in (False, True):
+                ep = torch.empty((G, M, B), device=DEV, dtype=dt)
+                fp = torch.empty((M, B), device=DEV, dtype=dt)
+                if G == 1:
+                    kp = build_prediction_error(M, K, B, act, dt, cfg)
+                    kp(xu[0], w[0], xl[0], ep[0], workspace=kp.new_workspace() if use_ws else None)
+                    kf = build_forward(M, K, B, act, dt, cfg)
+                    kf(xu[0], w[0], fp, workspace=kf.new_workspace() if use_ws else None)
+                else:
+                    kp = build_prediction_error_batched(M, K, B, G, act, dt, cfg)
+                    kp(xu, w, xl, ep, workspace=kp.new_workspace() if use_ws else None)
+                out[use_ws] = (ep, fp)
+            torch.cuda.synchronize()
+            assert torch.equal(out[False][0], out[True][0]), tile
+            if G == 1:
+                assert torch.equal(out[False][1], out[True][1]), tile
+    finally:
+        _preact(-1)
+
+
 def test_preactivation_into_a_caller_workspace_under_graph_capture():
     """A captured standalone call with a caller workspace records its
     activation launch and its GEMM (nothing is allocated, so nothing keeps it
