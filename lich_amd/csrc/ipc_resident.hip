@@ -208,6 +208,17 @@ struct Resident {
   static constexpr bool S3 = SPLIT >= 3;
   static constexpr int KSTEP = Op<OT>::KSTEP, KL = Op<OT>::KL;
 
+  // a * b for the kernel's small non-negative index products (LDS element
+  // offsets and tile counts, all well below 2^23): the full-rate 24-bit
+  // multiply, where the compiler, unable to bound lane-varying operands times
+  // a layout stride, issues the quarter-rate 32-bit one (the fp16 launch of
+  // the depth-6 profile: 33.8 -> 32.9 us).  The split-3 instantiations keep
+  // the 32-bit multiply: with it they measured 0.35 us faster per launch.
+  __device__ __forceinline__ static int m24(int a, int b) {
+    if constexpr (S3) return a * b;
+    else return __mul24(a, b);
+  }
+
   const ResidentArgs& p;
   OT* lds;
   ResidentLds lay;
@@ -291,9 +302,9 @@ struct Resident {
     const float f = act_t<ACT>(v);
     if (k < K && b < B) {
       const OT hi = cvt<OT>(f);
-      lds[lay.fh + b * lay.ldf + k] = hi;
-      if (S3) lds[lay.fl + b * lay.ldf + k] = cvt<OT>(f - to_f32(hi));
-      lds[lay.ft + k * lay.ldft + b] = hi;
+      lds[lay.fh + m24(b, lay.ldf) + k] = hi;
+      if (S3) lds[lay.fl + m24(b, lay.ldf) + k] = cvt<OT>(f - to_f32(hi));
+      lds[lay.ft + m24(k, lay.ldft) + b] = hi;
     }
     return f;
   }
@@ -318,17 +329,17 @@ struct Resident {
     }
     if (b < B) {
       if (r0 + 4 <= K) {
-        *reinterpret_cast<V4*>(lds + lay.fh + b * lay.ldf + r0) = V4{hi[0], hi[1], hi[2], hi[3]};
-        if (S3) *reinterpret_cast<V4*>(lds + lay.fl + b * lay.ldf + r0) = V4{lo[0], lo[1], lo[2], lo[3]};
+        *reinterpret_cast<V4*>(lds + lay.fh + m24(b, lay.ldf) + r0) = V4{hi[0], hi[1], hi[2], hi[3]};
+        if (S3) *reinterpret_cast<V4*>(lds + lay.fl + m24(b, lay.ldf) + r0) = V4{lo[0], lo[1], lo[2], lo[3]};
 #pragma unroll
-        for (int q = 0; q < 4; ++q) lds[lay.ft + (r0 + q) * lay.ldft + b] = hi[q];
+        for (int q = 0; q < 4; ++q) lds[lay.ft + m24(r0 + q, lay.ldft) + b] = hi[q];
       } else {
 #pragma unroll
         for (int q = 0; q < 4; ++q)
           if (r0 + q < K) {
-            lds[lay.fh + b * lay.ldf + r0 + q] = hi[q];
-            if (S3) lds[lay.fl + b * lay.ldf + r0 + q] = lo[q];
-            lds[lay.ft + (r0 + q) * lay.ldft + b] = hi[q];
+            lds[lay.fh + m24(b, lay.ldf) + r0 + q] = hi[q];
+            if (S3) lds[lay.fl + m24(b, lay.ldf) + r0 + q] = lo[q];
+            lds[lay.ft + m24(r0 + q, lay.ldft) + b] = hi[q];
           }
       }
     }
@@ -343,15 +354,15 @@ struct Resident {
 #pragma unroll
     for (int q = 0; q < 4; ++q) eo[q] = cvt<OT>(e[q]);
     if (r0 + 4 <= M) {
-      *reinterpret_cast<V4*>(lds + lay.eb + b * lay.lde + r0) = V4{eo[0], eo[1], eo[2], eo[3]};
+      *reinterpret_cast<V4*>(lds + lay.eb + m24(b, lay.lde) + r0) = V4{eo[0], eo[1], eo[2], eo[3]};
 #pragma unroll
-      for (int q = 0; q < 4; ++q) lds[lay.ea + (r0 + q) * lay.lda + b] = eo[q];
+      for (int q = 0; q < 4; ++q) lds[lay.ea + m24(r0 + q, lay.lda) + b] = eo[q];
     } else {
 #pragma unroll
       for (int q = 0; q < 4; ++q)
         if (r0 + q < M) {
-          lds[lay.eb + b * lay.lde + r0 + q] = eo[q];
-          lds[lay.ea + (r0 + q) * lay.lda + b] = eo[q];
+          lds[lay.eb + m24(b, lay.lde) + r0 + q] = eo[q];
+          lds[lay.ea + m24(r0 + q, lay.lda) + b] = eo[q];
         }
     }
   }
@@ -366,17 +377,17 @@ struct Resident {
     for (int q = 0; q < 4; ++q) {
       hi[q] = cvt<OT>(w[q]);
       if (m0 + q < M) {
-        lds[lay.wh + (m0 + q) * lay.ldw + k] = hi[q];
-        if (S3) lds[lay.wl + (m0 + q) * lay.ldw + k] = cvt<OT>(w[q] - to_f32(hi[q]));
+        lds[lay.wh + m24(m0 + q, lay.ldw) + k] = hi[q];
+        if (S3) lds[lay.wl + m24(m0 + q, lay.ldw) + k] = cvt<OT>(w[q] - to_f32(hi[q]));
       }
     }
     if (hidden) {
       if (m0 + 4 <= M) {
-        *reinterpret_cast<V4*>(lds + lay.wt + k * lay.ldwt + m0) = V4{hi[0], hi[1], hi[2], hi[3]};
+        *reinterpret_cast<V4*>(lds + lay.wt + m24(k, lay.ldwt) + m0) = V4{hi[0], hi[1], hi[2], hi[3]};
       } else {
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-          if (m0 + q < M) lds[lay.wt + k * lay.ldwt + m0 + q] = hi[q];
+          if (m0 + q < M) lds[lay.wt + m24(k, lay.ldwt) + m0 + q] = hi[q];
       }
     }
   }
@@ -384,24 +395,24 @@ struct Resident {
   // W element (m, k) of the block into its operand copies.
   __device__ __forceinline__ void stage_w(int m, int k, float w) {
     const OT hi = cvt<OT>(w);
-    lds[lay.wh + m * lay.ldw + k] = hi;
-    if (S3) lds[lay.wl + m * lay.ldw + k] = cvt<OT>(w - to_f32(hi));
-    if (hidden) lds[lay.wt + k * lay.ldwt + m] = hi;
+    lds[lay.wh + m24(m, lay.ldw) + k] = hi;
+    if (S3) lds[lay.wl + m24(m, lay.ldw) + k] = cvt<OT>(w - to_f32(hi));
+    if (hidden) lds[lay.wt + m24(k, lay.ldwt) + m] = hi;
   }
 
   // Tile t of a [rows][B] matrix: row of result element i of this lane, and its column.
   __device__ __forceinline__ int trow(int t, int i) const { return qdiv(t, inv_nbt) * 16 + 4 * lg + i; }
-  __device__ __forceinline__ int tcol(int t) const { return (t - qdiv(t, inv_nbt) * nbt) * 16 + lr; }
+  __device__ __forceinline__ int tcol(int t) const { return (t - m24(qdiv(t, inv_nbt), nbt)) * 16 + lr; }
   // update tile t: row tile over M, column tile over K
   __device__ __forceinline__ int urt(int t) const { return qdiv(t, inv_ktl); }
-  __device__ __forceinline__ int uct(int t) const { return t - qdiv(t, inv_ktl) * ktl; }
+  __device__ __forceinline__ int uct(int t) const { return t - m24(qdiv(t, inv_ktl), ktl); }
   __device__ __forceinline__ int rec(int t) const { return t * RES_TILE + lane * 4; }
 
   // acc = W_block f(x upper) for prediction tile t
   __device__ __forceinline__ f32x4 pred_tile(int t) const {
-    const int rt = qdiv(t, inv_nbt), ct = t - rt * nbt;
-    const int a0 = (rt * 16 + lr) * lay.ldw + lg * KL;
-    const int b0 = (ct * 16 + lr) * lay.ldf + lg * KL;
+    const int rt = qdiv(t, inv_nbt), ct = t - m24(rt, nbt);
+    const int a0 = m24(rt * 16 + lr, lay.ldw) + lg * KL;
+    const int b0 = m24(ct * 16 + lr, lay.ldf) + lg * KL;
     f32x4 c = zero4();
     for (int ks = 0; ks < ks_k; ++ks) {
       const V8 ah = ld8(lay.wh + a0 + ks * KSTEP);
@@ -419,9 +430,9 @@ struct Resident {
 
   // acc = W^T eps for inference tile t (rows over K)
   __device__ __forceinline__ f32x4 infer_tile(int t) const {
-    const int rt = qdiv(t, inv_nbt), ct = t - rt * nbt;
-    const int a0 = lay.wt + (rt * 16 + lr) * lay.ldwt + lg * KL;
-    const int b0 = lay.eb + (ct * 16 + lr) * lay.lde + lg * KL;
+    const int rt = qdiv(t, inv_nbt), ct = t - m24(rt, nbt);
+    const int a0 = lay.wt + m24(rt * 16 + lr, lay.ldwt) + lg * KL;
+    const int b0 = lay.eb + m24(ct * 16 + lr, lay.lde) + lg * KL;
     f32x4 c = zero4();
     for (int ks = 0; ks < ks_m; ++ks) c = Op<OT>::mma(ld8(a0 + ks * KSTEP), ld8(b0 + ks * KSTEP), c);
     return c;
@@ -433,12 +444,12 @@ struct Resident {
   // column kernel's rank-B update does.
   __device__ __forceinline__ f32x4 outer_tile(int t) const {
     const int c = uct(t) * 16 + lr, r0 = urt(t) * 16 + 4 * lg;
-    const OT* fr = lds + lay.ft + c * lay.ldft;
+    const OT* fr = lds + lay.ft + m24(c, lay.ldft);
     f32x4 acc = zero4();
     for (int b = 0; b < B; ++b) {
       const float f = to_f32(fr[b]);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) acc[q] = __builtin_fmaf(to_f32(lds[lay.ea + (r0 + q) * lay.lda + b]), f, acc[q]);
+      for (int q = 0; q < 4; ++q) acc[q] = __builtin_fmaf(to_f32(lds[lay.ea + m24(r0 + q, lay.lda) + b]), f, acc[q]);
     }
     return acc;
   }
@@ -447,8 +458,8 @@ struct Resident {
   __device__ __forceinline__ f32x4 update_tile(int t) const {
     if (p.outer) return outer_tile(t);
     const int rt = urt(t), ct = uct(t);
-    const int a0 = lay.ea + (rt * 16 + lr) * lay.lda + lg * KL;
-    const int b0 = lay.ft + (ct * 16 + lr) * lay.ldft + lg * KL;
+    const int a0 = lay.ea + m24(rt * 16 + lr, lay.lda) + lg * KL;
+    const int b0 = lay.ft + m24(ct * 16 + lr, lay.ldft) + lg * KL;
     f32x4 c = zero4();
     for (int ks = 0; ks < ks_b; ++ks) c = Op<OT>::mma(ld8(a0 + ks * KSTEP), ld8(b0 + ks * KSTEP), c);
     return c;
@@ -464,9 +475,9 @@ struct Resident {
   __device__ __forceinline__ void pred_tiles(int n, f32x4 (&c)[MAXT]) const {
     const int t0 = wave, t1 = wave + NWV;
     if (t1 < n && NWV % nbt == 0) {
-      const int rt0 = qdiv(t0, inv_nbt), ct = t0 - rt0 * nbt, rt1 = rt0 + NWV / nbt;
-      const int a0 = (rt0 * 16 + lr) * lay.ldw + lg * KL, a1 = (rt1 * 16 + lr) * lay.ldw + lg * KL;
-      const int b0 = (ct * 16 + lr) * lay.ldf + lg * KL;
+      const int rt0 = qdiv(t0, inv_nbt), ct = t0 - m24(rt0, nbt), rt1 = rt0 + NWV / nbt;
+      const int a0 = m24(rt0 * 16 + lr, lay.ldw) + lg * KL, a1 = m24(rt1 * 16 + lr, lay.ldw) + lg * KL;
+      const int b0 = m24(ct * 16 + lr, lay.ldf) + lg * KL;
       f32x4 c0 = zero4(), c1 = zero4();
       for (int ks = 0; ks < ks_k; ++ks) {
         const V8 bh = ld8(lay.fh + b0 + ks * KSTEP);
@@ -493,9 +504,9 @@ struct Resident {
   __device__ __forceinline__ void infer_tiles(int n, f32x4 (&c)[MAXT]) const {
     const int t0 = wave, t1 = wave + NWV;
     if (t1 < n && NWV % nbt == 0) {
-      const int rt0 = qdiv(t0, inv_nbt), ct = t0 - rt0 * nbt, rt1 = rt0 + NWV / nbt;
-      const int a0 = lay.wt + (rt0 * 16 + lr) * lay.ldwt + lg * KL, a1 = lay.wt + (rt1 * 16 + lr) * lay.ldwt + lg * KL;
-      const int b0 = lay.eb + (ct * 16 + lr) * lay.lde + lg * KL;
+      const int rt0 = qdiv(t0, inv_nbt), ct = t0 - m24(rt0, nbt), rt1 = rt0 + NWV / nbt;
+      const int a0 = lay.wt + m24(rt0 * 16 + lr, lay.ldwt) + lg * KL, a1 = lay.wt + m24(rt1 * 16 + lr, lay.ldwt) + lg * KL;
+      const int b0 = lay.eb + m24(ct * 16 + lr, lay.lde) + lg * KL;
       f32x4 c0 = zero4(), c1 = zero4();
       for (int ks = 0; ks < ks_m; ++ks) {
         const V8 b = ld8(b0 + ks * KSTEP);
@@ -513,9 +524,9 @@ struct Resident {
   __device__ __forceinline__ void update_tiles(int n, f32x4 (&c)[MAXT]) const {
     const int t0 = wave, t1 = wave + NWV;
     if (!p.outer && t1 < n && NWV % ktl == 0) {
-      const int rt0 = urt(t0), ct = t0 - rt0 * ktl, rt1 = rt0 + NWV / ktl;
-      const int a0 = lay.ea + (rt0 * 16 + lr) * lay.lda + lg * KL, a1 = lay.ea + (rt1 * 16 + lr) * lay.lda + lg * KL;
-      const int b0 = lay.ft + (ct * 16 + lr) * lay.ldft + lg * KL;
+      const int rt0 = urt(t0), ct = t0 - m24(rt0, ktl), rt1 = rt0 + NWV / ktl;
+      const int a0 = lay.ea + m24(rt0 * 16 + lr, lay.lda) + lg * KL, a1 = lay.ea + m24(rt1 * 16 + lr, lay.lda) + lg * KL;
+      const int b0 = lay.ft + m24(ct * 16 + lr, lay.ldft) + lg * KL;
       f32x4 c0 = zero4(), c1 = zero4();
       for (int ks = 0; ks < ks_b; ++ks) {
         const V8 b = ld8(b0 + ks * KSTEP);
@@ -1099,7 +1110,7 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, ResidentArg
         for (int q = 0; q < 4; ++q) {
           const int r = k.trow(t, q);
           if (r < k.M && b < B) {
-            k.lds[k.lay.ea + r * k.lay.lda + b] = cvt<OT>(ev4[i][q]);
+            k.lds[k.lay.ea + k.m24(r, k.lay.lda) + b] = cvt<OT>(ev4[i][q]);
             if (last && j == 0) gbl(p.e[l])[(long long)(r0 + r) * B + b] = ev4[i][q];
           }
         }
