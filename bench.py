@@ -316,15 +316,17 @@ def kernel_sweep(sizes=(1024, 4096, 8192), batches=(256, 2048, 8192), acts=("tan
                     if kind == "pred":
                         return lambda: kern(xu, w, xl, e, workspace=ws)
                     if kind == "infer":
-                        return lambda: kern(xl, e, wl, el, aout if save else None)
+                        return lambda: kern(xl, e, wl, el, aout if save else None, workspace=ws)
                     return lambda: kern(w, e, xu, workspace=ws)
 
                 for kind, save, kern in cases:
                     # the default call (no workspace: f(X) in every row tile's
-                    # loader; the library allocates nothing) and, where the call
-                    # would evaluate f(X) once given one, the caller-workspace call
+                    # loader, the inference update's operands read transposed;
+                    # the library allocates nothing) and, where the call would
+                    # use one (f(X) evaluated once, or the inference update's
+                    # operands copied transposed), the caller-workspace call
                     us = time_launch(call(kind, save, kern), reps)
-                    need = kern.workspace_bytes if kind != "infer" else 0
+                    need = kern.workspace_bytes
                     us_ws = None
                     if need > 0:
                         if ws_buf is None or ws_buf.numel() < need:

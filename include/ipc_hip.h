@@ -415,7 +415,8 @@ int ipc_set_coresident_limit(int blocks);
 
 /*
  * Caller workspace of the standalone 16-bit-storage calls on the LDS-DMA
- * kernel (ipc_pred_err, ipc_forward, ipc_weight_update with recompute).
+ * kernel (ipc_pred_err, ipc_forward, ipc_weight_update with recompute,
+ * ipc_infer_update).
  * Their B operand f(X_upper) is activated in the loader of every row tile,
  * which for the exponential activations costs more VALU work than the tile's
  * MFMAs once there are many row tiles.  The _ws variants take a device
@@ -431,14 +432,17 @@ int ipc_set_coresident_limit(int blocks);
  *
  * ipc_s16_workspace_bytes gives the bytes a call of `kind` (IPC_PHASE_PRED
  * for ipc_pred_err_ws / ipc_forward_ws, IPC_PHASE_WEIGHT for a recomputing
- * ipc_weight_update_ws) with M rows, contraction K, batch B and `groups`
- * groups uses: groups * K * B * 2 when it pre-activates under the current
- * mode, else 0.  The automatic rule: exp-based activations from M >= 1024 and
- * K * B >= 2^20, relu from M >= 4096 and K * B >= 2^22, never identity or the
- * inference update.  ipc_s16_preactivates(kind, act, M, K, B) reports the
- * same decision (1 / 0).  ipc_set_s16_preactivate, a tuning hook, sets the
- * mode: -1 (default) the rule, 0 never, 1 whenever a workspace is given.
- * Not thread-safe.
+ * ipc_weight_update_ws, IPC_PHASE_INFER for ipc_infer_update_ws) with M rows,
+ * contraction K, batch B and `groups` groups uses: groups * K * B * 2 when it
+ * pre-activates under the current mode (groups * (M * K + K * B) * 2 for the
+ * inference update, which copies W_lower and E_lower transposed into the
+ * workspace so that its GEMM reads both operands k-contiguous), else 0.  The
+ * automatic rule: exp-based activations from M >= 1024 and K * B >= 2^20,
+ * relu from M >= 4096 and K * B >= 2^22, never identity; the inference
+ * update from M * K >= 2^26 and K * B >= 2^26.  ipc_s16_preactivates(kind,
+ * act, M, K, B) reports the same decision (1 / 0).  ipc_set_s16_preactivate,
+ * a tuning hook, sets the mode: -1 (default) the rule, 0 never, 1 whenever a
+ * workspace is given.  Not thread-safe.
  */
 int ipc_pred_err_ws(const void* x_upper, const void* w, const void* x_lower, void* e,
                     int M, int K, int B, int groups,
@@ -451,6 +455,10 @@ int ipc_forward_ws(const void* x_upper, const void* w, void* out,
 int ipc_weight_update_ws(void* w, const void* e, const void* x_upper, int M, int K, int B, int groups,
                          float alpha, int recompute, int storage, int operand, int act, int tile,
                          void* workspace, long long workspace_bytes, void* stream);
+int ipc_infer_update_ws(void* x, const void* e, const void* w_lower, const void* e_lower, void* a_out,
+                        int M, int K, int B, int groups, float gamma,
+                        int storage, int operand, int act, int tile,
+                        void* workspace, long long workspace_bytes, void* stream);
 long long ipc_s16_workspace_bytes(int kind, int act, int M, int K, int B, int groups);
 int ipc_set_s16_preactivate(int mode);
 int ipc_s16_preactivates(int kind, int act, int M, int K, int B);

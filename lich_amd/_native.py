@@ -80,6 +80,7 @@ def _declare(lib):
         "ipc_pred_err_ws": ([vp, vp, vp, vp, i, i, i, i, i, i, i, i, i, vp, c_longlong, vp], i),
         "ipc_forward_ws": ([vp, vp, vp, i, i, i, i, i, i, i, i, i, vp, c_longlong, vp], i),
         "ipc_weight_update_ws": ([vp, vp, vp, i, i, i, i, f, i, i, i, i, i, vp, c_longlong, vp], i),
+        "ipc_infer_update_ws": ([vp, vp, vp, vp, vp, i, i, i, i, f, i, i, i, i, vp, c_longlong, vp], i),
         "ipc_s16_workspace_bytes": ([i, i, i, i, i, i], c_longlong),
         "ipc_plan_create": ([POINTER(vp), i, POINTER(c_int), i, i, i, i, i, f, f, i, i, i], i),
         "ipc_plan_fused": ([vp], i),

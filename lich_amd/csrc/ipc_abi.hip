@@ -251,33 +251,57 @@ int g_s16_preact = -1;
 // operand).  The automatic rule, from the per-kernel sweep on MI355X: the
 // exponential activations pay for the extra pass from 4 row tiles of 256
 // (M >= 1024) and a 2^20-element operand; relu, cheap in the loader, from 16
-// row tiles and 2^22 elements.
-bool s16_preact_rule(int mode, int act, int M, long long kb) {
-  if (act == IPC_ACT_IDENTITY || mode == S16_INFER || g_s16_preact == 0) return false;
+// row tiles and 2^22 elements.  The inference update has no activated
+// operand; given a workspace it stores W_lower and E_lower transposed
+// instead, which pays only for the largest calls (W and E_lower of at least
+// 2^26 elements each): at 8192^3 3-8 % faster, at 8192 x 8192 x 2048 and
+// 4096^2 x 8192 3-9 % slower, the two copying passes outweighing the GEMM's
+// gain.
+bool s16_preact_rule(int mode, int act, int M, int K, long long kb) {
+  if (g_s16_preact == 0) return false;
+  if (mode == S16_INFER) return g_s16_preact > 0 || ((long long)M * K >= (1LL << 26) && kb >= (1LL << 26));
+  if (act == IPC_ACT_IDENTITY) return false;
   if (g_s16_preact > 0) return true;
   if (act == IPC_ACT_RELU) return M >= 4096 && kb >= (1LL << 22);
   return M >= 1024 && kb >= (1LL << 20);
 }
 
-// Bytes of caller workspace a pre-activating call uses: the groups' activated
-// B operands, 16-bit, contiguous (0 when the rule says the call does not
-// pre-activate).
-long long s16_workspace_need(int mode, int act, int M, long long kb, int groups) {
-  return s16_preact_rule(mode, act, M, kb) ? (long long)groups * kb * 2 : 0;
+// Bytes of caller workspace a call uses (0 when the rule says it does not
+// use one): the groups' activated B operands, 16-bit, contiguous; for the
+// inference update the groups' W_lower^T blocks [M][K], then their
+// E_lower^T blocks [B][K].
+long long s16_workspace_need(int mode, int act, int M, int K, long long kb, int groups) {
+  if (!s16_preact_rule(mode, act, M, K, kb)) return 0;
+  return mode == S16_INFER ? (long long)groups * ((long long)M * K + kb) * 2 : (long long)groups * kb * 2;
 }
 
 // A standalone call on the LDS-DMA kernel.  With a caller workspace of at
 // least s16_workspace_need bytes the B operand is activated once into it
-// (an elementwise launch) and the GEMM reads it like the other operands;
-// otherwise every row tile activates its B block in its loader.  The library
+// (an elementwise launch) and the GEMM reads it like the other operands, or,
+// for the inference update, both operands are copied transposed into it;
+// otherwise every row tile activates its B block in its loader and the
+// inference update reads its operands transposed from LDS.  The library
 // allocates nothing either way.
 int run_s16(int mode, const WideProblem& q, int groups, long long a_gs, long long b_gs, long long o_gs,
             long long x_gs, long long o2_gs, int operand, int act, int cfg, void* workspace, long long ws_bytes,
             void* stream, const char* what) {
   hipStream_t s = (hipStream_t)stream;
-  const long long need = s16_workspace_need(mode, act, q.M, b_gs, groups);
+  const long long need = s16_workspace_need(mode, act, q.M, q.K, b_gs, groups);
   if (need > 0 && workspace && ws_bytes >= need) {
     WideProblem qa = q;
+    if (mode == S16_INFER) {
+      // W_lower [K][M] -> [M][K] and E_lower [K][B] -> [B][K] (identity
+      // "activation"): both GEMM operands k-contiguous, the same values in
+      // the same k order
+      char* wt = static_cast<char*>(workspace);
+      char* et = wt + (long long)groups * a_gs * 2;
+      qa.a = wt; qa.lda = q.K; qa.a_lim = q.M;
+      qa.b = et; qa.ldb = q.K; qa.b_lim = q.N;
+      const std::vector<WideProblem> v = s16_groups(qa, groups, a_gs, b_gs, o_gs, x_gs, o2_gs);
+      TRY(launch_rc(launch_s16_activate_t(q.a, wt, q.K, q.M, groups, a_gs, operand, IPC_ACT_IDENTITY, s), what));
+      TRY(launch_rc(launch_s16_activate_t(q.b, et, q.K, q.N, groups, b_gs, operand, IPC_ACT_IDENTITY, s), what));
+      return launch_rc(launch_s16(S16_INFERT, v.data(), groups, operand, act, cfg, s), what);
+    }
     qa.b = workspace;
     if (mode == S16_PRED || mode == S16_FWD) {
       // f(X_upper [K][B])^T into the workspace: the GEMM then reads both
@@ -404,6 +428,14 @@ int ipc_forward_ws(const void* x_upper, const void* w, void* out, int M, int K, 
 int ipc_infer_update(void* x, const void* e, const void* w_lower, const void* e_lower, void* a_out, int M,
                      int K, int B, int groups, float gamma, int storage, int operand, int act, int tile,
                      void* stream) {
+  return ipc_infer_update_ws(x, e, w_lower, e_lower, a_out, M, K, B, groups, gamma, storage, operand, act, tile,
+                             nullptr, 0, stream);
+}
+
+int ipc_infer_update_ws(void* x, const void* e, const void* w_lower, const void* e_lower, void* a_out, int M,
+                        int K, int B, int groups, float gamma, int storage, int operand, int act, int tile,
+                        void* workspace, long long workspace_bytes, void* stream) {
+  TRY(check_workspace(workspace, workspace_bytes));
   TRY(check_dtypes(storage, operand));
   TRY(check_act(act));
   TRY(check_dims(M, K, B, groups));
@@ -426,7 +458,8 @@ int ipc_infer_update(void* x, const void* e, const void* w_lower, const void* e_
     q.scal = gamma;
     q.vec = B % 4 == 0 && al8(x) && al8(e) && al8(a_out);
     return run_s16(S16_INFER, q, groups, (long long)K * M, (long long)K * B, (long long)M * B, (long long)M * B,
-                   (long long)M * B, operand, act, use_dma - 1, nullptr, 0, stream, "ipc_infer_update");
+                   (long long)M * B, operand, act, use_dma - 1, workspace, workspace_bytes, stream,
+                   "ipc_infer_update");
   }
   GemmProblem p = make_inf(x, e, w_lower, e_lower, a_out, M, K, B, groups, gamma, act, es);
   return launch_rc(launch_gemm(&p, 1, storage, operand, IPC_SPLIT_NONE, tile, (hipStream_t)stream),
@@ -1527,13 +1560,13 @@ int ipc_wide_problem_check(int phase, int split, int fp32_w, int has_lo, int K, 
 
 int ipc_s16_preactivates(int kind, int act, int M, int K, int B) {
   const int mode = kind == IPC_PHASE_PRED ? S16_PRED : kind == IPC_PHASE_WEIGHT ? S16_WEIGHT : S16_INFER;
-  return s16_preact_rule(mode, act, M, (long long)K * B) ? 1 : 0;
+  return s16_preact_rule(mode, act, M, K, (long long)K * B) ? 1 : 0;
 }
 
 long long ipc_s16_workspace_bytes(int kind, int act, int M, int K, int B, int groups) {
   if (M < 1 || K < 1 || B < 1 || groups < 1) return 0;
   const int mode = kind == IPC_PHASE_PRED ? S16_PRED : kind == IPC_PHASE_WEIGHT ? S16_WEIGHT : S16_INFER;
-  return s16_workspace_need(mode, act, M, (long long)K * B, groups);
+  return s16_workspace_need(mode, act, M, K, (long long)K * B, groups);
 }
 
 int ipc_set_s16_preactivate(int mode) {

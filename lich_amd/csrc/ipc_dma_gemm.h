@@ -82,6 +82,8 @@ constexpr bool is_s16(int mode) { return mode >= S16_PRED; }
 // the standalone prediction / forward, with B as given or as f(X_upper)^T
 constexpr bool s16_pred(int mode) { return mode == S16_PRED || mode == S16_PREDT; }
 constexpr bool s16_fwd(int mode) { return mode == S16_FWD || mode == S16_FWDT; }
+// the standalone inference update, with W_lower / E_lower as given or transposed
+constexpr bool s16_infer(int mode) { return mode == S16_INFER || mode == S16_INFERT; }
 
 // chunk position of chunk c in row r
 __device__ __forceinline__ int kc_swz(int r, int c) { return c ^ ((r >> 1) & 7); }
@@ -568,7 +570,7 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
     // steps are those of the LDS path) and they have no transposed copy.
     static_assert(BM >= 256 && BN * BM * (int)sizeof(OT) <= stage_bytes(BM, BN, S, LO), "transposed tile");
     const int elr = lane & 31, elk = lane >> 5;
-    constexpr bool EIN = MODE == WIDE_INFER || MODE == S16_INFER;
+    constexpr bool EIN = MODE == WIDE_INFER || s16_infer(MODE);
     constexpr unsigned ES = S16 ? (unsigned)sizeof(OT) : 4u;  // bytes of an input, output or out2 element
     const long long xld = pre_from_aux ? p.ldx : p.ldo;
     const Buf bx(pre_from_aux ? p.aux : p.out, PRE ? (long long)M * xld * ES : 0);
@@ -598,7 +600,7 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
       constexpr int NBK = RM * RN;
       const long long s_ldo = p.ldo, s_ld2 = p.ld2;
       const float s_scal = p.scal;
-      const bool s_out2 = MODE == S16_INFER && p.out2 != nullptr;
+      const bool s_out2 = s16_infer(MODE) && p.out2 != nullptr;
       float xin[2][PRE ? 16 : 1], ein[2][EIN ? 16 : 1];
       auto load_block = [&](int bk, float (&xo)[PRE ? 16 : 1], float (&eo)[EIN ? 16 : 1]) {
         const int n = n0 + wn * WTN + (bk % RN) * 32 + elr, nn = n < N ? n : 0;
@@ -629,7 +631,7 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
             hv = cvt<OT>(x - to_f32(cvt<OT>(a)));
           } else if (s16_fwd(MODE)) {
             hv = cvt<OT>(a);
-          } else if (MODE == S16_INFER) {
+          } else if (s16_infer(MODE)) {
             const float xn = x + s_scal * (-ein[cur][EIN ? q : 0] + dact_t<ACT>(x) * a);
             hv = cvt<OT>(xn);
             lv = cvt<OT>(act_t<ACT>(xn));                              // A_out
@@ -688,7 +690,7 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
             hv = cvt<OT>(x - to_f32(cvt<OT>(a)));
           } else if (s16_fwd(MODE)) {
             hv = cvt<OT>(a);
-          } else if (MODE == S16_INFER) {
+          } else if (s16_infer(MODE)) {
             const float xn = x + p.scal * (-ein[EIN ? q : 0] + dact_t<ACT>(x) * a);
             hv = cvt<OT>(xn);
             lv = cvt<OT>(act_t<ACT>(xn));                              // A_out
@@ -700,7 +702,7 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
           if (ncol) {
             if constexpr (S16) {
               bo.st16(__builtin_bit_cast(unsigned short, hv), vo, r * (unsigned)p.ldo * ES);
-              if (MODE == S16_INFER && p.out2) b2.st16(__builtin_bit_cast(unsigned short, lv), v2, r * (unsigned)p.ld2 * ES);
+              if (s16_infer(MODE) && p.out2) b2.st16(__builtin_bit_cast(unsigned short, lv), v2, r * (unsigned)p.ld2 * ES);
             } else {
               bo.st32(v, vo, r * (unsigned)p.ldo * 4u);
               if (MODE != WIDE_WEIGHT || p.h) bh.st16(__builtin_bit_cast(unsigned short, hv), vh, r * (unsigned)p.ldh * (unsigned)sizeof(OT));
@@ -753,7 +755,7 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
 #pragma unroll
   for (int c0 = 0; c0 < IT; c0 += CH) {
     float ein[CH][4];
-    if (MODE == WIDE_INFER || MODE == S16_INFER) {
+    if (MODE == WIDE_INFER || s16_infer(MODE)) {
 #pragma unroll
       for (int u = 0; u < CH; ++u) load_group(p.aux, p.ldx, c0 + u, ein[u]);
     }
@@ -792,7 +794,7 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
           hv[q] = cvt<OT>(x - to_f32(cvt<OT>(a)));
         } else if (s16_fwd(MODE)) {
           hv[q] = cvt<OT>(a);
-        } else if (MODE == S16_INFER) {
+        } else if (s16_infer(MODE)) {
           const float xn = x + p.scal * (-ein[u][q] + dact_t<ACT>(x) * a);
           hv[q] = cvt<OT>(xn);
           lv[q] = cvt<OT>(act_t<ACT>(xn));                            // A_out
@@ -826,7 +828,7 @@ __global__ void __launch_bounds__(WGM * WGN * 64) dma_gemm_kernel(const Batch bt
         }
       } else {
         OT* op = reinterpret_cast<OT*>(p.out) + (long long)m * p.ldo + n;
-        OT* o2 = MODE == S16_INFER && p.out2 ? reinterpret_cast<OT*>(p.out2) + (long long)m * p.ld2 + n : nullptr;
+        OT* o2 = s16_infer(MODE) && p.out2 ? reinterpret_cast<OT*>(p.out2) + (long long)m * p.ld2 + n : nullptr;
         if (vec && nv == 4) {
           uint2 hh; hh.x = pack2(hv[0], hv[1]); hh.y = pack2(hv[2], hv[3]);
           *reinterpret_cast<uint2*>(op) = hh;

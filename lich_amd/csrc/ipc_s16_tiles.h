@@ -25,6 +25,7 @@ struct Tiles {
           case S16_PRED: return dma::Cfg<OT, S16_PRED, 1, ACT, R, BM, BN, S, PM, PN>::launch(probs, count, s);
           case S16_FWD: return dma::Cfg<OT, S16_FWD, 1, ACT, R, BM, BN, S, PM, PN>::launch(probs, count, s);
           case S16_INFER: return dma::Cfg<OT, S16_INFER, 1, ACT, false, BM, BN, S, PM, PN>::launch(probs, count, s);
+          case S16_INFERT: return dma::Cfg<OT, S16_INFERT, 1, ACT, false, BM, BN, S, PM, PN>::launch(probs, count, s);
           case S16_PREDT:
           case S16_FWDT:
             // f(X_upper)^T from a caller workspace: the activation is applied

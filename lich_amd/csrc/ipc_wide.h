@@ -51,6 +51,9 @@ enum {
   // S16_PRED / S16_FWD whose B operand is f(X_upper)^T [N][K] (k-contiguous,
   // ldb = K): the copy a caller workspace holds after launch_s16_activate_t
   S16_PREDT = 8, S16_FWDT = 9,
+  // S16_INFER reading W_lower^T [M][K] and E_lower^T [B][K] (both
+  // k-contiguous, lda = ldb = K): the transposed copies of a caller workspace
+  S16_INFERT = 10,
 };
 
 inline long long wide_pad(long long v, long long m) { return (v + m - 1) / m * m; }

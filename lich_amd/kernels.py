@@ -118,7 +118,8 @@ class _Kernel:
     @property
     def workspace_bytes(self) -> int:
         """Bytes of caller workspace that let a call evaluate f(X_upper) once
-        instead of in every row tile's loader (0: the call never uses one).
+        instead of in every row tile's loader, or, for the inference update,
+        copy its operands transposed (0: the call never uses one).
         Only 16-bit storage on the LDS-DMA kernel uses it; the library itself
         allocates nothing."""
         if self._ws_kind < 0 or self.storage == nat.DT_F32:
@@ -180,15 +181,20 @@ class ForwardKernel(_Kernel):
 
 
 class InferenceUpdateKernel(_Kernel):
-    """``k(X[M,B], E[M,B], W_lower[K,M], E_lower[K,B][, A_out[M,B]])``:
-    ``X += gamma(-E + f'(X) W_lower^T E_lower)`` (and ``A_out = f(X_new)``)."""
+    """``k(X[M,B], E[M,B], W_lower[K,M], E_lower[K,B][, A_out[M,B]], *, workspace=None)``:
+    ``X += gamma(-E + f'(X) W_lower^T E_lower)`` (and ``A_out = f(X_new)``).
+    ``workspace`` (optional, caller-owned, ``new_workspace()``) lets a large
+    16-bit call copy W_lower and E_lower transposed, so that its GEMM reads
+    both operands k-contiguous (same bits)."""
+
+    _ws_kind = 1
 
     def __init__(self, *a, gamma: float, save_activation: bool, **kw):
         super().__init__(*a, **kw)
         self.gamma = float(gamma)
         self.save_activation = bool(save_activation)
 
-    def __call__(self, x, e, w_lower, e_lower, a_out=None):
+    def __call__(self, x, e, w_lower, e_lower, a_out=None, *, workspace=None):
         M, K, B, dt = self.M, self.K, self.B, self.dtype
         _check(x, "X", self._shape(M, B), dt)
         _check(e, "E", self._shape(M, B), dt)
@@ -200,10 +206,11 @@ class InferenceUpdateKernel(_Kernel):
             _check(a_out, "A_out", self._shape(M, B), dt)
         elif a_out is not None:
             raise ValueError("A_out given to a kernel built with save_activation=False")
-        nat.check(nat.lib().ipc_infer_update(
+        ws, nbytes = self._ws(workspace)
+        nat.check(nat.lib().ipc_infer_update_ws(
             x.data_ptr(), e.data_ptr(), w_lower.data_ptr(), e_lower.data_ptr(),
             a_out.data_ptr() if a_out is not None else None, M, K, B, self.groups, self.gamma,
-            self.storage, self.operand, self.act, self.tile, nat.current_stream_handle(x.device)))
+            self.storage, self.operand, self.act, self.tile, ws, nbytes, nat.current_stream_handle(x.device)))
 
 
 class WeightUpdateKernel(_Kernel):

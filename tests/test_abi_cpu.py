@@ -543,8 +543,10 @@ def test_s16_preactivate_hook_validates_its_mode():
 
 def test_s16_preactivation_rule():
     """The automatic rule: exp-based activations from M >= 1024 and K*B >= 2^20,
-    relu from M >= 4096 and K*B >= 2^22, never for the inference update or
-    identity; mode 0 turns it off, mode 1 on."""
+    relu from M >= 4096 and K*B >= 2^22, never identity; the inference update
+    (which copies its operands transposed) from M*K >= 2^26 and K*B >= 2^26,
+    whatever the activation; mode 0 turns it off, mode 1 on.  The workspace
+    sizes follow: K*B*2 per group, (M*K + K*B)*2 for the inference update."""
     lib = _lib()
     tanh, relu, ident = nat.act_code("tanh"), nat.act_code("relu"), nat.act_code("identity")
     q = lib.ipc_s16_preactivates
@@ -552,7 +554,13 @@ def test_s16_preactivation_rule():
     assert q(0, tanh, 1023, 1024, 1024) == 0 and q(0, tanh, 1024, 1024, 512) == 0
     assert q(0, relu, 4096, 4096, 1024) == 1 and q(0, relu, 2048, 4096, 2048) == 0
     assert q(0, relu, 4096, 1024, 2048) == 0
-    assert q(1, tanh, 8192, 8192, 8192) == 0 and q(0, ident, 8192, 8192, 8192) == 0
+    assert q(0, ident, 8192, 8192, 8192) == 0
+    assert q(1, tanh, 8192, 8192, 8192) == 1 and q(1, ident, 8192, 8192, 8192) == 1
+    assert q(1, relu, 8192, 8192, 4096) == 0 and q(1, tanh, 4096, 8192, 8192) == 0
+    wb = lib.ipc_s16_workspace_bytes
+    assert wb(0, tanh, 1024, 1024, 1024, 3) == 3 * 1024 * 1024 * 2
+    assert wb(1, relu, 8192, 8192, 8192, 2) == 2 * (8192 * 8192 + 8192 * 8192) * 2
+    assert wb(1, relu, 4096, 4096, 2048, 1) == 0 and wb(0, ident, 8192, 8192, 8192, 1) == 0
     try:
         assert lib.ipc_set_s16_preactivate(0) == nat.IPC_OK and q(0, tanh, 8192, 8192, 8192) == 0
         assert lib.ipc_set_s16_preactivate(1) == nat.IPC_OK and q(0, relu, 8, 64, 8) == 1

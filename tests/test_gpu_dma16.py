@@ -21,7 +21,8 @@ import torch
 
 from lich_amd.kernels import (KernelConfig, build_forward, build_inference_update, build_prediction_error,
                               build_weight_update)
-from lich_amd.layer_batching import build_prediction_error_batched, build_weight_update_batched
+from lich_amd.layer_batching import (build_inference_update_batched, build_prediction_error_batched,
+                                     build_weight_update_batched)
 from oracle import ipc_oracle as O
 from tests.helpers import ACTS, DEV, OPS, gen, randn, rel_err, report
 
@@ -239,6 +240,49 @@ def test_transposed_preactivation_matches_the_loader_on_every_tile(M, K, B, G, a
             torch.cuda.synchronize()
             assert torch.equal(out[False][0], out[True][0]), tile
             if G == 1:
+                assert torch.equal(out[False][1], out[True][1]), tile
+    finally:
+        _preact(-1)
+
+
+@pytest.mark.parametrize("op", ["f16", "bf16"])
+@pytest.mark.parametrize("act", ["relu", "tanh", "identity"])
+@pytest.mark.parametrize("M,K,B,G,save", [(296, 192, 136, 1, True), (512, 256, 520, 1, False),
+                                          (256, 256, 72, 3, True)])
+def test_inference_update_with_transposed_operands_matches_on_every_tile(M, K, B, G, save, act, op):
+    """With a workspace, the inference update copies W_lower and E_lower
+    transposed ([M][K], [B][K]) and its GEMM reads both operands k-contiguous:
+    on every LDS-DMA tile configuration, for ragged shapes and grouped calls,
+    X and A_out equal the transposing-read path's bit for bit, and the
+    workspace holds (M*K + K*B)*2 bytes per group."""
+    from lich_amd import _native as nat
+
+    report("dma16-infer-ws", M=M, K=K, B=B, G=G, save=save, act=act, op=op)
+    dt = OPS[op]
+    g = gen(11 * M + 5 * K + B + G)
+    x0, e = _t(randn((G, M, B), g), dt), _t(randn((G, M, B), g), dt)
+    wl, el = _t(randn((G, K, M), g, 1 / math.sqrt(K)), dt), _t(randn((G, K, B), g), dt)
+    try:
+        _preact(1)
+        for tile in nat.TILE_DMA_TILES:
+            cfg = KernelConfig(tile=tile)
+            out = {}
+            for use_ws in (False, True):
+                x = x0.clone()
+                a = torch.empty((G, M, B), device=DEV, dtype=dt) if save else None
+                if G == 1:
+                    k = build_inference_update(M, K, B, act, dt, cfg, 0.5, save)
+                    k(x[0], e[0], wl[0], el[0], a[0] if save else None,
+                      workspace=k.new_workspace() if use_ws else None)
+                else:
+                    k = build_inference_update_batched(M, K, B, G, act, dt, cfg, 0.5, save)
+                    k(x, e, wl, el, a, workspace=k.new_workspace() if use_ws else None)
+                if use_ws:
+                    assert k.workspace_bytes == G * (M * K + K * B) * 2
+                out[use_ws] = (x, a)
+            torch.cuda.synchronize()
+            assert torch.equal(out[False][0], out[True][0]), tile
+            if save:
                 assert torch.equal(out[False][1], out[True][1]), tile
     finally:
         _preact(-1)
