@@ -16,19 +16,21 @@
 // A step, per workgroup:
 //   1. P = W f(x[l+1]) with 16-bit MFMA (one product with unsplit operands,
 //      three with split 3: hi*hi + lo*hi + hi*lo), or fp32 MFMA;
-//      eps[l] = x[l] - P; g = W[l]^T eps[l] (the inference term of layer l+1).
-//      Top chunks publish their partial P instead.
-//   2. publish eps[l] and g (16x16 result tiles, one 16-byte record per
-//      lane) and raise the workgroup's flag; wait for the flags of the
-//      workgroups it exchanges with (the same set both ways, so a
+//      eps[l] = x[l] - P; g = W[l]^T eps[l] (the inference term of layer l+1)
+//      and its product with f'(x[l+1]) of the old state.  Top chunks publish
+//      their partial P instead.
+//   2. publish eps[l] and f'(x[l+1]) g (16x16 result tiles, one 16-byte
+//      record per lane) and raise the workgroup's flag; wait for the flags of
+//      the workgroups it exchanges with (the same set both ways, so a
 //      double-buffered exchange is safe).
-//   3. x[l] += gamma(-eps[l] + f'(x[l]) g[l]) with g[l] from workgroup l-1 and
-//      x[l+1] += gamma(-eps[l+1] + f'(x[l+1]) g) with eps[l+1] from workgroup
-//      l+1.  eps[L-1] = x[L-1] minus the top chunks' partials summed in chunk
-//      order (per row block); each block's chunk 0 hands its rows to workgroup
-//      L-2 as one record under a flag of its own.  The top workgroups apply
-//      x[L-1]'s update one step late (with workgroup L-2's g of the previous
-//      step), so they never wait for workgroup L-2's current step.  Both
+//   3. x[l] += gamma(-eps[l] + f'(x[l]) g[l]) with that product from
+//      workgroup l-1 and x[l+1] += gamma(-eps[l+1] + f'(x[l+1]) g) with
+//      eps[l+1] from workgroup l+1.  eps[L-1] = x[L-1] minus the top chunks'
+//      partials summed in chunk order (per row block); each block's chunk 0
+//      hands its rows to workgroup L-2 as one record under a flag of its own.
+//      The top workgroups apply x[L-1]'s update one step late (with workgroup
+//      L-2's product of the previous step), so they never wait for workgroup
+//      L-2's current step.  Both
 //      neighbours evaluate every shared state with the same operands in the
 //      same order, so their copies stay bit-identical without a second
 //      exchange.
@@ -176,23 +178,24 @@ __device__ __forceinline__ f32x4 sum_partials(const float* base, long long strid
   return sum;
 }
 
-// x + gamma(-e + d g) with d = f'(x), evaluated without contraction so that
-// every workgroup holding a copy of the state computes the same bits.  d
-// depends on the old state only and is evaluated before the exchange.
-__device__ __forceinline__ float state_update(float x, float e, float g, float d, float gamma) {
+// x + gamma(-e + dg) with dg = f'(x) g, evaluated without contraction so that
+// every workgroup holding a copy of the state computes the same bits.  f'(x)
+// depends on the old state only: the workgroup that computes g = W^T eps holds
+// f(x) of that state as well, forms the product (one rounded fp32 multiply)
+// and exchanges it in place of g, so its receivers evaluate no f'.
+__device__ __forceinline__ float state_update(float x, float e, float dg, float gamma) {
 #pragma clang fp contract(off)
-  return x + gamma * (-e + d * g);
+  return x + gamma * (-e + dg);
 }
 
-template <int ACT>
-__device__ __forceinline__ f32x4 dact4(f32x4 x) {
-  f32x4 d;
+__device__ __forceinline__ f32x4 mul4(f32x4 a, f32x4 b) {
+  f32x4 c;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) d[q] = dact_t<ACT>(x[q]);
-  return d;
+  for (int q = 0; q < 4; ++q) c[q] = a[q] * b[q];
+  return c;
 }
 
-// dact4 given f(x) as well (the value staged for the MFMAs)
+// f'(x) given f(x) as well (the value staged for the MFMAs)
 template <int ACT>
 __device__ __forceinline__ f32x4 dact4_from(f32x4 x, f32x4 f) {
   f32x4 d;
@@ -802,24 +805,24 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, Resident
       }
     }
     __syncthreads();
-    // next to the top layer the chunks read g one step later: three buffers
+    // gb = f'(x[l+1]) (W^T eps[l]) of the old state x[l+1], kept for this
+    // workgroup's copy of x[l+1] and sent to workgroup l+1 (or the top chunks,
+    // which read it one step later: three buffers)
     float* xg = p.xg[l] + (long long)(from_top ? s % 3 : buf) * ninf * RES_TILE;
+    f32x4 db[MAXT];
+#pragma unroll
+    for (int i = 0; i < MAXT; ++i) db[i] = dact4_from<ACT>(xb[i], fb[i]);
     k.infer_tiles(ninf, gb);
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) {
       const int t = wave + NWV * i;
+      gb[i] = mul4(db[i], gb[i]);
       if (t < ninf) st_rec(xg + k.rec(t), gb[i]);
     }
-    // ---- 2. exchange; f'(x[l]) and f'(x[l+1]) of the old states meanwhile
+    // ---- 2. exchange
     publish(&p.flags[k.wg], ep.base + (unsigned)(s + 1));
-    f32x4 da[MAXT], db[MAXT];
-#pragma unroll
-    for (int i = 0; i < MAXT; ++i) {
-      da[i] = l >= 1 ? dact4<ACT>(xa[i]) : zero4();
-      db[i] = dact4_from<ACT>(xb[i], fb[i]);
-    }
     wait_peers(p, peers, npeers, ep.base + (unsigned)(s + 1));
-    // ---- 3. x[l] with g[l] from workgroup l-1; x[l+1] with eps[l+1] from above
+    // ---- 3. x[l] with f'(x[l]) g[l] from workgroup l-1; x[l+1] with eps[l+1] from above
     // (every exchange load of the phase is issued before the first use)
     f32x4 gl[MAXT], eu[MAXT];
     const float* xgl = l >= 1 ? p.xg[l - 1] + (long long)buf * npr * RES_TILE : nullptr;
@@ -845,7 +848,7 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, Resident
         const int t = wave + NWV * i;
         if (t < npr)
 #pragma unroll
-          for (int q = 0; q < 4; ++q) xa[i][q] = state_update(xa[i][q], ea[i][q], gl[i][q], da[i][q], gamma);
+          for (int q = 0; q < 4; ++q) xa[i][q] = state_update(xa[i][q], ea[i][q], gl[i][q], gamma);
       }
     }
 #pragma unroll
@@ -853,7 +856,7 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, Resident
       const int t = wave + NWV * i;
       if (t < ninf) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) xb[i][q] = state_update(xb[i][q], eu[i][q], gb[i][q], db[i][q], gamma);
+        for (int q = 0; q < 4; ++q) xb[i][q] = state_update(xb[i][q], eu[i][q], gb[i][q], gamma);
         fb[i] = k.stage_f4(k.trow(t, 0), k.tcol(t), xb[i]);
       }
     }
@@ -1045,14 +1048,11 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, ResidentArg
         if (t < npr) st_rec(xp + (long long)j * nrec * RES_TILE + k.rec(k.toff + t), cp[i]);
       }
     }
-    // ---- 2. exchange: the siblings' partials of this step, workgroup L-2's g
-    // of the previous one; f'(x[L-1]) of the state the late update starts from
-    // meanwhile (nothing to wait for in a first step from xn: its flag goes up
-    // once the step has read xn, below)
+    // ---- 2. exchange: the siblings' partials of this step, workgroup L-2's
+    // f'(x[L-1]) g of the previous one (f' of the state the late update starts
+    // from; nothing to wait for in a first step from xn: its flag goes up once
+    // the step has read xn, below)
     if (!pre) publish(&p.flags[k.wg], ep.base + (unsigned)(s + 1));
-    f32x4 da[MAXT];
-#pragma unroll
-    for (int i = 0; i < MAXT; ++i) da[i] = dact4<ACT>(xa[i]);
     if (!pre) wait_peers(p, peers, npeers, ep.base + (unsigned)(s + 1), 1);
     f32x4 g[MAXT];
 #pragma unroll
@@ -1079,7 +1079,7 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, ResidentArg
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const int r = k.trow(t, q);
-          if (s >= 1) xa[i][q] = state_update(xa[i][q], ev_prev[i][q], g[i][q], da[i][q], gamma);
+          if (s >= 1) xa[i][q] = state_update(xa[i][q], ev_prev[i][q], g[i][q], gamma);
           ev4[i][q] = (r < k.M && b < B) ? xa[i][q] - sum[q] : 0.0f;
         }
       }
