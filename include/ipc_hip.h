@@ -188,7 +188,7 @@ typedef struct ipc_plan ipc_plan;
  *   IPC_PATH_RESIDENT  multi-step launches on the layer-resident whole-step
  *                    kernel (every workgroup keeps one layer's W, or a column
  *                    chunk of the top layer's, on chip for all steps and
- *                    exchanges only eps and W^T eps with its neighbours): a
+ *                    exchanges only eps and f'(x) W^T eps with its neighbours): a
  *                    narrow net with fp16/bf16 operands, split 1 or 3, L >= 2,
  *                    d_0..d_{L-1} <= 64, B <= 128 and the GEMM weight update
  *                    (weight mode GEMM, or AUTO with B > 16); IPC_ERR_CONFIG
@@ -225,7 +225,7 @@ int ipc_plan_path(const ipc_plan* plan);
  * the weight update after them.  A layer-resident plan then keeps, after
  * those: its per-workgroup step flags, which count steps across launches
  * (they are never cleared), the cache generation and one cache slot per
- * workgroup; the double-buffered eps / W^T eps exchange; and caches tied to
+ * workgroup; the double-buffered eps / f'(x) W^T eps exchange; and caches tied to
  * the bound buffers (the top chunks' 16-bit images of f(x[L]), the hidden
  * f(x) values and the next launch's first-step partial products), which a
  * launch reuses while their generation is current.  ipc_plan_bind and

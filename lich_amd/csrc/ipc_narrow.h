@@ -91,7 +91,7 @@ __host__ __device__ inline void narrow_lds_layout(const int* dims, int L, int KS
 // whole-step kernel in which every workgroup owns one layer's W for all steps
 // (the top layer's W, with its long input-width contraction, is split into
 // column chunks owned by one workgroup each) and exchanges only eps and
-// W^T eps with its neighbours: 16-bit operands with the GEMM weight update
+// f'(x) W^T eps with its neighbours: 16-bit operands with the GEMM weight update
 // (B <= 128), and fp32 operands with either weight update while the operand
 // blocks fit the LDS (B <= 64 at width 64).
 constexpr int RES_MAX_WIDTH = 64;   // d_0 .. d_{L-1}
@@ -113,7 +113,7 @@ struct ResidentArgs {
   float* w[NARROW_MAX_L];
   float* fx[NARROW_MAX_L + 1];  // f(x[l]) written at the end (a[l] in save mode)
   float* xe[NARROW_MAX_L];      // eps[l], l = 1..L-2:        [2][tiles(d_l)][RES_TILE]
-  float* xg[NARROW_MAX_L];      // W[l]^T eps[l], l = 0..L-2: [2][tiles(d_{l+1})][RES_TILE]
+  float* xg[NARROW_MAX_L];      // f'(x[l+1]) W[l]^T eps[l], l = 0..L-2: [2][tiles(d_{l+1})][RES_TILE]
   float* xp;                    // top-layer partial products: [2][chunks][tiles(d_{L-1})][RES_TILE]
   float* xs;                    // eps[L-1] as summed by each row block's chunk 0: [2][tiles(d_{L-1})][RES_TILE]
   float* xn;                    // the top-layer partial products of the next launch's first step, computed
