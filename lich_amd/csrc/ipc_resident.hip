@@ -954,6 +954,20 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, ResidentArg
 #pragma unroll
     for (int u = 0; u < CB; ++u) img[u] = bi.u128((threadIdx.x + u * NT) * 16u);
   }
+  // A warm launch's first step sums the partial products the previous launch
+  // left in xn.  Those of the wave's first prediction tile are loaded here,
+  // with the image, and summed once they arrive (the same loads and chunk
+  // order as sum_partials), so that the first eps[L-1] does not wait for a
+  // memory round trip after the prologue; a second tile loads its own in the
+  // step.  A cold launch drops them.
+  const int nrec_pf = k.npr_full, npr_pf = k.n_pred;
+  const bool pf = C <= PBATCH && wave < npr_pf;
+  f32x4 pv[PBATCH];
+  if (pf) {
+    const float* xn0 = k.p.xn + k.rec(k.toff + wave);
+#pragma unroll
+    for (int u = 0; u < PBATCH; ++u) pv[u] = u < C ? ld_rec(xn0 + (long long)u * nrec_pf * RES_TILE) : zero4();
+  }
   setup(k);
   if (warm) {
     const gu32x4* src = isrc;
@@ -1014,6 +1028,15 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, ResidentArg
   }
   end_prologue(k, p, aword, peers, npeers_lds);
   const int npeers = npeers_lds;
+  f32x4 pre_sum = zero4();
+  if (pf) {
+    pre_sum = pv[0];
+#pragma unroll
+    for (int u = 1; u < PBATCH; ++u)
+      if (u < C)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) pre_sum[q] = pre_sum[q] + pv[u][q];
+  }
 
   // The chunks apply each step's x[L-1] update one step late, just before the
   // next step's eps[L-1]: their own chain (partial product, partial sums,
@@ -1028,9 +1051,11 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, ResidentArg
   // product (at the start of a launch the top chunks are not yet a step
   // ahead of it).
   float* xn = p.xn + (long long)j * nrec * RES_TILE;
+  // ev_prev: the previous step's eps[L-1], read from the second step on; before
+  // the first, tile 0's prefetched partial sum
   f32x4 ev_prev[MAXT];
 #pragma unroll
-  for (int i = 0; i < MAXT; ++i) ev_prev[i] = zero4();
+  for (int i = 0; i < MAXT; ++i) ev_prev[i] = i == 0 ? pre_sum : zero4();
   for (int s = 0; s < p.steps; ++s) {
     k.refresh();
     const int lg = k.lg, lr = k.lr;
@@ -1074,7 +1099,7 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, ResidentArg
       const int t = wave + NWV * i;
       ev4[i] = zero4();
       if (t < npr) {
-        const f32x4 sum = sum_partials(xp, (long long)nrec * RES_TILE, C, k.rec(k.toff + t));
+        const f32x4 sum = i == 0 && pre && pf ? ev_prev[0] : sum_partials(xp, (long long)nrec * RES_TILE, C, k.rec(k.toff + t));
         const int b = k.tcol(t);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
