@@ -112,15 +112,25 @@ typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(1))) u32x4 gu32x4;
 __device__ __forceinline__ gf32* gbl(float* p) { return (gf32*)p; }
 __device__ __forceinline__ const gf32* gbl(const float* p) { return (const gf32*)p; }
+typedef __attribute__((address_space(1))) char gchar;
+// v at byte `off` (32-bit) of a uniform base: the store takes the scalar base
+// and the lane's 32-bit offset
+__device__ __forceinline__ void st_at(gf32* base, unsigned off, float v) { *(gf32*)((gchar*)base + off) = v; }
+// the four values of a result-tile lane (rows `stride` bytes apart) from byte `off`
+__device__ __forceinline__ void st4_rows(gf32* base, unsigned off, unsigned stride, f32x4 v) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) st_at(base, off + q * stride, v[q]);
+}
 
 // A pointer every lane holds the same value of, moved to scalar registers
-// (loads through it then take a 32-bit per-lane offset instead of a 64-bit
+// (accesses through it then take a 32-bit per-lane offset instead of a 64-bit
 // per-lane address).
-__device__ __forceinline__ const float* uniform(const float* p) {
+template <typename T>
+__device__ __forceinline__ T* uniform(T* p) {
   const unsigned long long v = reinterpret_cast<unsigned long long>(p);
   const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)v);
   const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(v >> 32));
-  return reinterpret_cast<const float*>(((unsigned long long)hi << 32) | lo);
+  return reinterpret_cast<T*>(((unsigned long long)hi << 32) | lo);
 }
 
 // Element idx of a state or weight matrix (a uniform pointer) when `in`,
@@ -673,36 +683,50 @@ __device__ __forceinline__ void end_prologue(const Resident<OT, SPLIT, ACT>& k, 
 template <typename OT, int SPLIT, int ACT>
 __device__ __forceinline__ void write_states(Resident<OT, SPLIT, ACT>& k, const ResidentArgs& p,
                                              const f32x4* ea, const f32x4* xa, const f32x4* xb, const f32x4* fb) {
+  // (uniform base pointers and 32-bit byte offsets, so that each store takes
+  // the lane's offset and the scalar base: one offset per tile, the rows a
+  // uniform stride apart; rows are checked one by one only where a tile's
+  // four rows do not all exist)
+  // (x[l] is written for l >= 1, x[l+1] next to the top layer; the flags are
+  // uniform, the pointers always valid)
   const int l = k.l, B = k.B, wave = k.wave;
-  float* E = p.e[l];
-  float* X = l >= 1 ? p.x[l] : nullptr;
-  float* XU = l + 1 == k.L - 1 ? p.x[l + 1] : nullptr;
-  float* FU = p.fx[l + 1];
+  const bool wx = l >= 1, wxu = l + 1 == k.L - 1, wfu = p.fx[l + 1] != nullptr;
+  gf32* E = gbl(uniform(p.e[l]));
+  gf32* X = gbl(uniform(p.x[l]));
+  gf32* XU = gbl(uniform(p.x[l + 1]));
+  gf32* FU = gbl(uniform(p.fx[l + 1]));
+  const unsigned rs = (unsigned)B * 4u;  // bytes between rows
 #pragma unroll
   for (int i = 0; i < MAXT; ++i) {
     const int t = wave + NWV * i;
     if (t < k.n_pred) {
-      const int b = k.tcol(t);
+      const int b = k.tcol(t), r0 = k.trow(t, 0);
+      const unsigned o = (unsigned)(r0 * B + b) * 4u;
+      if (r0 + 4 <= k.M && b < B) {
+        st4_rows(E, o, rs, ea[i]);
+        if (wx) st4_rows(X, o, rs, xa[i]);
+      } else {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int r = k.trow(t, q);
-        if (r < k.M && b < B) {
-          const long long o = (long long)r * B + b;
-          gbl(E)[o] = ea[i][q];
-          if (X) gbl(X)[o] = xa[i][q];
-        }
+        for (int q = 0; q < 4; ++q)
+          if (r0 + q < k.M && b < B) {
+            st_at(E, o + q * rs, ea[i][q]);
+            if (wx) st_at(X, o + q * rs, xa[i][q]);
+          }
       }
     }
     if (t < k.n_inf) {
-      const int b = k.tcol(t);
+      const int b = k.tcol(t), r0 = k.trow(t, 0);
+      const unsigned o = (unsigned)(r0 * B + b) * 4u;
+      if (r0 + 4 <= k.K && b < B) {
+        if (wfu) st4_rows(FU, o, rs, fb[i]);
+        if (wxu) st4_rows(XU, o, rs, xb[i]);
+      } else {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int r = k.trow(t, q);
-        if (r < k.K && b < B) {
-          const long long o = (long long)r * B + b;
-          if (FU) gbl(FU)[o] = fb[i][q];
-          if (XU) gbl(XU)[o] = xb[i][q];
-        }
+        for (int q = 0; q < 4; ++q)
+          if (r0 + q < k.K && b < B) {
+            if (wfu) st_at(FU, o + q * rs, fb[i][q]);
+            if (wxu) st_at(XU, o + q * rs, xb[i][q]);
+          }
       }
     }
   }
@@ -883,15 +907,19 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, Resident
   }
 
   // ---- results: W[l] (the states went out before the last weight update)
+  gf32* WG = gbl(uniform(p.w[l]));
 #pragma unroll
   for (int i = 0; i < MU; ++i) {
     const int t = wave + NWV * i;
     if (t < k.n_upd) {
-      const int c = k.uct(t) * 16 + lr;
+      const int c = k.uct(t) * 16 + lr, r0 = k.urt(t) * 16 + 4 * lg;
+      const unsigned o = (unsigned)(r0 * k.ldw_g + c) * 4u, rs = (unsigned)k.ldw_g * 4u;
+      if (r0 + 4 <= k.M && c < k.K) {
+        st4_rows(WG, o, rs, wr[i]);
+      } else {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int r = k.urt(t) * 16 + 4 * lg + q;
-        if (r < k.M && c < k.K) gbl(p.w[l])[(long long)r * k.ldw_g + c] = wr[i][q];
+        for (int q = 0; q < 4; ++q)
+          if (r0 + q < k.M && c < k.K) st_at(WG, o + q * rs, wr[i][q]);
       }
     }
   }
