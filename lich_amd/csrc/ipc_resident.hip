@@ -573,7 +573,7 @@ __device__ __forceinline__ void publish(unsigned* flag, unsigned value) {
 // fences).  The flags count steps across launches, so they are compared as a
 // difference, which stays right when the count wraps around.
 __device__ __forceinline__ void wait_peers(const ResidentArgs& p, const int* peers, int npeers, unsigned value,
-                                           int n_prev = 0) {
+                                           int n_prev = 0, bool acquire = true) {
   if (threadIdx.x < 64) {
     const int lane = threadIdx.x;
     const unsigned* f = lane < npeers ? &p.flags[peers[lane]] : nullptr;
@@ -589,9 +589,29 @@ __device__ __forceinline__ void wait_peers(const ResidentArgs& p, const int* pee
         break;
       }
     }
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    if (acquire) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
   __syncthreads();
+}
+
+// Four exchange records (16 bytes per lane each) read coherently at agent
+// scope: SC1 loads are served from the device's coherence point, never from a
+// line the reader's L2 may hold from before, the same coherence the flag polls
+// rely on.  The writer's release fence has written its records back before its
+// flag went up, and these loads leave only after the flag was seen, so no
+// acquire fence (an invalidation of the whole L2) is needed before them.  One
+// block that waits for all four: no load stays in flight past it.
+__device__ __forceinline__ void ld_rec4_sc1(const float* a0, const float* a1, const float* a2, const float* a3,
+                                            f32x4& v0, f32x4& v1, f32x4& v2, f32x4& v3) {
+  asm volatile(
+      "global_load_dwordx4 %0, %4, off sc1\n\t"
+      "global_load_dwordx4 %1, %5, off sc1\n\t"
+      "global_load_dwordx4 %2, %6, off sc1\n\t"
+      "global_load_dwordx4 %3, %7, off sc1\n\t"
+      "s_waitcnt vmcnt(0)"
+      : "=&v"(v0), "=&v"(v1), "=&v"(v2), "=&v"(v3)
+      : "v"(a0), "v"(a1), "v"(a2), "v"(a3)
+      : "memory");
 }
 
 // The flags area across launches.  Step flags are never cleared: every
@@ -845,26 +865,27 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, Resident
     }
     // ---- 2. exchange
     publish(&p.flags[k.wg], ep.base + (unsigned)(s + 1));
-    wait_peers(p, peers, npeers, ep.base + (unsigned)(s + 1));
+    wait_peers(p, peers, npeers, ep.base + (unsigned)(s + 1), 0, false);
     // ---- 3. x[l] with f'(x[l]) g[l] from workgroup l-1; x[l+1] with eps[l+1] from above
     // (every exchange load of the phase is issued before the first use)
+    // (f'(x[l]) g[l] of workgroup l-1, absent for l = 0; eps[l+1] from workgroup
+    // l+1, or eps[L-1] as summed by the row blocks' chunk 0; a tile past the
+    // counts, or an absent record, reads tile 0 of eps[l+1], in range, and is
+    // zeroed)
     f32x4 gl[MAXT], eu[MAXT];
+    static_assert(MAXT == 2, "four records per wave");
     const float* xgl = l >= 1 ? p.xg[l - 1] + (long long)buf * npr * RES_TILE : nullptr;
-    if (xgl) {
-#pragma unroll
-      for (int i = 0; i < MAXT; ++i) {
-        const int t = wave + NWV * i;
-        gl[i] = t < npr ? ld_rec(xgl + k.rec(t)) : zero4();
-      }
-    }
+    const float* xeu = (from_top ? p.xs : p.xe[l + 1]) + (long long)buf * ninf * RES_TILE;
     {
-      // eps[l+1] from workgroup l+1, or eps[L-1] as summed by the row blocks' chunk 0
-      const float* xeu = (from_top ? p.xs : p.xe[l + 1]) + (long long)buf * ninf * RES_TILE;
-#pragma unroll
-      for (int i = 0; i < MAXT; ++i) {
-        const int t = wave + NWV * i;
-        eu[i] = t < ninf ? ld_rec(xeu + k.rec(t)) : zero4();
-      }
+      const int t0 = wave, t1 = wave + NWV;
+      const float* fallback = xeu + k.rec(0);
+      const bool g0 = xgl && t0 < npr, g1 = xgl && t1 < npr, e0 = t0 < ninf, e1 = t1 < ninf;
+      ld_rec4_sc1(g0 ? xgl + k.rec(t0) : fallback, g1 ? xgl + k.rec(t1) : fallback,
+                  e0 ? xeu + k.rec(t0) : fallback, e1 ? xeu + k.rec(t1) : fallback, gl[0], gl[1], eu[0], eu[1]);
+      if (!g0) gl[0] = zero4();
+      if (!g1) gl[1] = zero4();
+      if (!e0) eu[0] = zero4();
+      if (!e1) eu[1] = zero4();
     }
     if (xgl) {
 #pragma unroll
