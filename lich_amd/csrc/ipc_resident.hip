@@ -474,7 +474,22 @@ struct Resident {
     const int a0 = lay.ea + m24(rt * 16 + lr, lay.lda) + lg * KL;
     const int b0 = lay.ft + m24(ct * 16 + lr, lay.ldft) + lg * KL;
     f32x4 c = zero4();
-    for (int ks = 0; ks < ks_b; ++ks) c = Op<OT>::mma(ld8(a0 + ks * KSTEP), ld8(b0 + ks * KSTEP), c);
+    int ks = 0;
+    if constexpr (!S3) {
+      // four k-steps' fragments read before their MFMAs (one LDS latency
+      // instead of four; the same MFMA sequence)
+      for (; ks + 4 <= ks_b; ks += 4) {
+        V8 a[4], b[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          a[u] = ld8(a0 + (ks + u) * KSTEP);
+          b[u] = ld8(b0 + (ks + u) * KSTEP);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) c = Op<OT>::mma(a[u], b[u], c);
+      }
+    }
+    for (; ks < ks_b; ++ks) c = Op<OT>::mma(ld8(a0 + ks * KSTEP), ld8(b0 + ks * KSTEP), c);
     return c;
   }
 
@@ -492,7 +507,25 @@ struct Resident {
       const int a0 = m24(rt0 * 16 + lr, lay.ldw) + lg * KL, a1 = m24(rt1 * 16 + lr, lay.ldw) + lg * KL;
       const int b0 = m24(ct * 16 + lr, lay.ldf) + lg * KL;
       f32x4 c0 = zero4(), c1 = zero4();
-      for (int ks = 0; ks < ks_k; ++ks) {
+      int ks = 0;
+      if constexpr (!S3) {
+        // two k-steps' fragments read before their MFMAs (the same sequence)
+        for (; ks + 2 <= ks_k; ks += 2) {
+          V8 bh[2], ah0[2], ah1[2];
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            bh[u] = ld8(lay.fh + b0 + (ks + u) * KSTEP);
+            ah0[u] = ld8(lay.wh + a0 + (ks + u) * KSTEP);
+            ah1[u] = ld8(lay.wh + a1 + (ks + u) * KSTEP);
+          }
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            c0 = Op<OT>::mma(ah0[u], bh[u], c0);
+            c1 = Op<OT>::mma(ah1[u], bh[u], c1);
+          }
+        }
+      }
+      for (; ks < ks_k; ++ks) {
         const V8 bh = ld8(lay.fh + b0 + ks * KSTEP);
         const V8 ah0 = ld8(lay.wh + a0 + ks * KSTEP), ah1 = ld8(lay.wh + a1 + ks * KSTEP);
         c0 = Op<OT>::mma(ah0, bh, c0);
@@ -521,7 +554,24 @@ struct Resident {
       const int a0 = lay.wt + m24(rt0 * 16 + lr, lay.ldwt) + lg * KL, a1 = lay.wt + m24(rt1 * 16 + lr, lay.ldwt) + lg * KL;
       const int b0 = lay.eb + m24(ct * 16 + lr, lay.lde) + lg * KL;
       f32x4 c0 = zero4(), c1 = zero4();
-      for (int ks = 0; ks < ks_m; ++ks) {
+      int ks = 0;
+      if constexpr (!S3) {
+        for (; ks + 2 <= ks_m; ks += 2) {
+          V8 b[2], x0[2], x1[2];
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            b[u] = ld8(b0 + (ks + u) * KSTEP);
+            x0[u] = ld8(a0 + (ks + u) * KSTEP);
+            x1[u] = ld8(a1 + (ks + u) * KSTEP);
+          }
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            c0 = Op<OT>::mma(x0[u], b[u], c0);
+            c1 = Op<OT>::mma(x1[u], b[u], c1);
+          }
+        }
+      }
+      for (; ks < ks_m; ++ks) {
         const V8 b = ld8(b0 + ks * KSTEP);
         c0 = Op<OT>::mma(ld8(a0 + ks * KSTEP), b, c0);
         c1 = Op<OT>::mma(ld8(a1 + ks * KSTEP), b, c1);
