@@ -651,16 +651,17 @@ __device__ __forceinline__ void wait_peers(const ResidentArgs& p, const int* pee
 // flag went up, and these loads leave only after the flag was seen, so no
 // acquire fence (an invalidation of the whole L2) is needed before them.  One
 // block that waits for all four: no load stays in flight past it.
-__device__ __forceinline__ void ld_rec4_sc1(const float* a0, const float* a1, const float* a2, const float* a3,
-                                            f32x4& v0, f32x4& v1, f32x4& v2, f32x4& v3) {
+// (Two scalar bases, each with two 32-bit byte offsets.)
+__device__ __forceinline__ void ld_rec4_sc1(const float* b0, unsigned o0, unsigned o1, const float* b1, unsigned o2,
+                                            unsigned o3, f32x4& v0, f32x4& v1, f32x4& v2, f32x4& v3) {
   asm volatile(
-      "global_load_dwordx4 %0, %4, off sc1\n\t"
-      "global_load_dwordx4 %1, %5, off sc1\n\t"
-      "global_load_dwordx4 %2, %6, off sc1\n\t"
-      "global_load_dwordx4 %3, %7, off sc1\n\t"
+      "global_load_dwordx4 %0, %4, %8 sc1\n\t"
+      "global_load_dwordx4 %1, %5, %8 sc1\n\t"
+      "global_load_dwordx4 %2, %6, %9 sc1\n\t"
+      "global_load_dwordx4 %3, %7, %9 sc1\n\t"
       "s_waitcnt vmcnt(0)"
       : "=&v"(v0), "=&v"(v1), "=&v"(v2), "=&v"(v3)
-      : "v"(a0), "v"(a1), "v"(a2), "v"(a3)
+      : "v"(o0), "v"(o1), "v"(o2), "v"(o3), "s"(b0), "s"(b1)
       : "memory");
 }
 
@@ -919,23 +920,20 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, Resident
     // ---- 3. x[l] with f'(x[l]) g[l] from workgroup l-1; x[l+1] with eps[l+1] from above
     // (every exchange load of the phase is issued before the first use)
     // (f'(x[l]) g[l] of workgroup l-1, absent for l = 0; eps[l+1] from workgroup
-    // l+1, or eps[L-1] as summed by the row blocks' chunk 0; a tile past the
-    // counts, or an absent record, reads tile 0 of eps[l+1], in range, and is
-    // zeroed)
+    // l+1, or eps[L-1] as summed by the row blocks' chunk 0; through scalar
+    // bases and 32-bit byte offsets.  A tile past the counts, or an absent
+    // record, reads tile 0 of eps[l+1], in range; such values are never used:
+    // every use of gl and eu is under the same tile test)
     f32x4 gl[MAXT], eu[MAXT];
     static_assert(MAXT == 2, "four records per wave");
-    const float* xgl = l >= 1 ? p.xg[l - 1] + (long long)buf * npr * RES_TILE : nullptr;
-    const float* xeu = (from_top ? p.xs : p.xe[l + 1]) + (long long)buf * ninf * RES_TILE;
+    const bool xgl = l >= 1;
     {
+      const float* ebase = uniform((from_top ? p.xs : p.xe[l + 1]) + (long long)buf * ninf * RES_TILE);
+      const float* gbase = xgl ? uniform(p.xg[l - 1] + (long long)buf * npr * RES_TILE) : ebase;
       const int t0 = wave, t1 = wave + NWV;
-      const float* fallback = xeu + k.rec(0);
+      const unsigned r0 = (unsigned)k.rec(t0) * 4u, r1 = (unsigned)k.rec(t1) * 4u, f = (unsigned)k.rec(0) * 4u;
       const bool g0 = xgl && t0 < npr, g1 = xgl && t1 < npr, e0 = t0 < ninf, e1 = t1 < ninf;
-      ld_rec4_sc1(g0 ? xgl + k.rec(t0) : fallback, g1 ? xgl + k.rec(t1) : fallback,
-                  e0 ? xeu + k.rec(t0) : fallback, e1 ? xeu + k.rec(t1) : fallback, gl[0], gl[1], eu[0], eu[1]);
-      if (!g0) gl[0] = zero4();
-      if (!g1) gl[1] = zero4();
-      if (!e0) eu[0] = zero4();
-      if (!e1) eu[1] = zero4();
+      ld_rec4_sc1(gbase, g0 ? r0 : f, g1 ? r1 : f, ebase, e0 ? r0 : f, e1 ? r1 : f, gl[0], gl[1], eu[0], eu[1]);
     }
     if (xgl) {
 #pragma unroll
