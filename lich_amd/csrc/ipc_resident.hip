@@ -889,13 +889,15 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, Resident
       const int t = wave + NWV * i;
       if (t < npr) {
         const f32x4 c = cp[i];
-        const int b = k.tcol(t);
+        const int b = k.tcol(t), r0 = k.trow(t, 0);
+        if (r0 + 4 <= k.M && b < B) {  // (the lane's four rows and its column all exist)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int r = k.trow(t, q);
-          ea[i][q] = r < k.M && b < B ? xa[i][q] - c[q] : 0.0f;
+          for (int q = 0; q < 4; ++q) ea[i][q] = xa[i][q] - c[q];
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) ea[i][q] = r0 + q < k.M && b < B ? xa[i][q] - c[q] : 0.0f;
         }
-        k.stage_e4(k.trow(t, 0), b, ea[i]);
+        k.stage_e4(r0, b, ea[i]);
         if (xe) st_rec(xe + k.rec(t), ea[i]);
       }
     }
