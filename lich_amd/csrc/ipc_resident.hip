@@ -359,6 +359,34 @@ struct Resident {
     return f;
   }
 
+  // stage_f4 for a lane whose four rows (r0 + 4 <= K) and column (b < B) all
+  // exist: the same values and stores, without the tests.
+  __device__ __forceinline__ f32x4 stage_f4_full(int r0, int b, f32x4 v) {
+    f32x4 f;
+    OT hi[4], lo[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      f[q] = act_t<ACT>(v[q]);
+      hi[q] = cvt<OT>(f[q]);
+      if (S3) lo[q] = cvt<OT>(f[q] - to_f32(hi[q]));
+    }
+    *reinterpret_cast<V4*>(lds + lay.fh + m24(b, lay.ldf) + r0) = V4{hi[0], hi[1], hi[2], hi[3]};
+    if (S3) *reinterpret_cast<V4*>(lds + lay.fl + m24(b, lay.ldf) + r0) = V4{lo[0], lo[1], lo[2], lo[3]};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) lds[lay.ft + m24(r0 + q, lay.ldft) + b] = hi[q];
+    return f;
+  }
+
+  // stage_e4 for a lane whose four rows (r0 + 4 <= M) and column (b < B) all exist.
+  __device__ __forceinline__ void stage_e4_full(int r0, int b, f32x4 e) {
+    OT eo[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) eo[q] = cvt<OT>(e[q]);
+    *reinterpret_cast<V4*>(lds + lay.eb + m24(b, lay.lde) + r0) = V4{eo[0], eo[1], eo[2], eo[3]};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) lds[lay.ea + m24(r0 + q, lay.lda) + b] = eo[q];
+  }
+
   // eps rows r0 .. r0 + 3 of column b (zero outside M x B) into the inference
   // B operand [b][m] (contiguous) and the weight-update A operand [m][b].
   __device__ __forceinline__ void stage_e4(int r0, int b, f32x4 e) {
@@ -893,11 +921,12 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, Resident
         if (r0 + 4 <= k.M && b < B) {  // (the lane's four rows and its column all exist)
 #pragma unroll
           for (int q = 0; q < 4; ++q) ea[i][q] = xa[i][q] - c[q];
+          k.stage_e4_full(r0, b, ea[i]);
         } else {
 #pragma unroll
           for (int q = 0; q < 4; ++q) ea[i][q] = r0 + q < k.M && b < B ? xa[i][q] - c[q] : 0.0f;
+          k.stage_e4(r0, b, ea[i]);
         }
-        k.stage_e4(r0, b, ea[i]);
         if (xe) st_rec(xe + k.rec(t), ea[i]);
       }
     }
@@ -952,7 +981,9 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, Resident
       if (t < ninf) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) xb[i][q] = state_update(xb[i][q], eu[i][q], gb[i][q], gamma);
-        fb[i] = k.stage_f4(k.trow(t, 0), k.tcol(t), xb[i]);
+        const int b = k.tcol(t), r0 = k.trow(t, 0);
+        if (r0 + 4 <= k.K && b < B) fb[i] = k.stage_f4_full(r0, b, xb[i]);
+        else fb[i] = k.stage_f4(r0, b, xb[i]);
       }
     }
     if (s + 1 == p.steps) write_states(k, p, ea, xa, xb, fb);  // overlaps the last weight update
