@@ -433,6 +433,19 @@ struct Resident {
     }
   }
 
+  // stage_w4 of a hidden workgroup for a lane whose four rows (m0 + 4 <= M)
+  // and column (k < K) all exist: the same values and stores, without the tests.
+  __device__ __forceinline__ void stage_w4_full(int m0, int k, f32x4 w) {
+    OT hi[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      hi[q] = cvt<OT>(w[q]);
+      lds[lay.wh + m24(m0 + q, lay.ldw) + k] = hi[q];
+      if (S3) lds[lay.wl + m24(m0 + q, lay.ldw) + k] = cvt<OT>(w[q] - to_f32(hi[q]));
+    }
+    *reinterpret_cast<V4*>(lds + lay.wt + m24(k, lay.ldwt) + m0) = V4{hi[0], hi[1], hi[2], hi[3]};
+  }
+
   // W element (m, k) of the block into its operand copies.
   __device__ __forceinline__ void stage_w(int m, int k, float w) {
     const OT hi = cvt<OT>(w);
@@ -995,14 +1008,23 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, Resident
       if (t < k.n_upd) {
         const f32x4 c = k.update_tile(t);
         const int col = k.uct(t) * 16 + lr, r0 = k.urt(t) * 16 + 4 * lg;
+        if (r0 + 4 <= k.M && col < k.K) {  // (the lane's four rows and its column all exist)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          if (r0 + q < k.M && col < k.K) {
+          for (int q = 0; q < 4; ++q) {
 #pragma clang fp contract(off)
             wr[i][q] = wr[i][q] + alpha * c[q];
           }
+          k.stage_w4_full(r0, col, wr[i]);
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            if (r0 + q < k.M && col < k.K) {
+#pragma clang fp contract(off)
+              wr[i][q] = wr[i][q] + alpha * c[q];
+            }
+          }
+          k.stage_w4(r0, col, wr[i]);
         }
-        k.stage_w4(r0, col, wr[i]);
       }
     }
     __syncthreads();
