@@ -308,6 +308,20 @@ struct Resident {
 
   __device__ __forceinline__ V8 ld8(int off) const { return *reinterpret_cast<const V8*>(lds + off); }
 
+  // Four values rounded to the operand type as one vector (two packed
+  // conversions).  The vector is pinned, so the 2-byte stores of single
+  // elements take their halves from these registers instead of converting
+  // the values a second time.
+  __device__ __forceinline__ static V4 cvt4(f32x4 v) {
+    V4 h = V4{cvt<OT>(v[0]), cvt<OT>(v[1]), cvt<OT>(v[2]), cvt<OT>(v[3])};
+    asm("" : "+v"(h));
+    return h;
+  }
+  // the lo terms cvt(v - hi) of a split operand
+  __device__ __forceinline__ static V4 cvt4_lo(f32x4 v, V4 h) {
+    return cvt4(f32x4{v[0] - to_f32(h[0]), v[1] - to_f32(h[1]), v[2] - to_f32(h[2]), v[3] - to_f32(h[3])});
+  }
+
   // f(v) as 16-bit hi (and lo) terms into the prediction B operand [b][k] and
   // hi into the weight-update B operand [k][b]; (k, b) outside K x B is left
   // zero.  Returns f(v).
@@ -334,16 +348,13 @@ struct Resident {
 
   // The same with f(v) given (its operand terms only).
   __device__ __forceinline__ f32x4 stage_fv4(int r0, int b, f32x4 f) {
-    OT hi[4], lo[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      hi[q] = cvt<OT>(f[q]);
-      if (S3) lo[q] = cvt<OT>(f[q] - to_f32(hi[q]));
-    }
+    const V4 hi = cvt4(f);
+    V4 lo;
+    if (S3) lo = cvt4_lo(f, hi);
     if (b < B) {
       if (r0 + 4 <= K) {
-        *reinterpret_cast<V4*>(lds + lay.fh + m24(b, lay.ldf) + r0) = V4{hi[0], hi[1], hi[2], hi[3]};
-        if (S3) *reinterpret_cast<V4*>(lds + lay.fl + m24(b, lay.ldf) + r0) = V4{lo[0], lo[1], lo[2], lo[3]};
+        *reinterpret_cast<V4*>(lds + lay.fh + m24(b, lay.ldf) + r0) = hi;
+        if (S3) *reinterpret_cast<V4*>(lds + lay.fl + m24(b, lay.ldf) + r0) = lo;
 #pragma unroll
         for (int q = 0; q < 4; ++q) lds[lay.ft + m24(r0 + q, lay.ldft) + b] = hi[q];
       } else {
@@ -363,15 +374,11 @@ struct Resident {
   // exist: the same values and stores, without the tests.
   __device__ __forceinline__ f32x4 stage_f4_full(int r0, int b, f32x4 v) {
     f32x4 f;
-    OT hi[4], lo[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      f[q] = act_t<ACT>(v[q]);
-      hi[q] = cvt<OT>(f[q]);
-      if (S3) lo[q] = cvt<OT>(f[q] - to_f32(hi[q]));
-    }
-    *reinterpret_cast<V4*>(lds + lay.fh + m24(b, lay.ldf) + r0) = V4{hi[0], hi[1], hi[2], hi[3]};
-    if (S3) *reinterpret_cast<V4*>(lds + lay.fl + m24(b, lay.ldf) + r0) = V4{lo[0], lo[1], lo[2], lo[3]};
+    for (int q = 0; q < 4; ++q) f[q] = act_t<ACT>(v[q]);
+    const V4 hi = cvt4(f);
+    *reinterpret_cast<V4*>(lds + lay.fh + m24(b, lay.ldf) + r0) = hi;
+    if (S3) *reinterpret_cast<V4*>(lds + lay.fl + m24(b, lay.ldf) + r0) = cvt4_lo(f, hi);
 #pragma unroll
     for (int q = 0; q < 4; ++q) lds[lay.ft + m24(r0 + q, lay.ldft) + b] = hi[q];
     return f;
@@ -379,10 +386,8 @@ struct Resident {
 
   // stage_e4 for a lane whose four rows (r0 + 4 <= M) and column (b < B) all exist.
   __device__ __forceinline__ void stage_e4_full(int r0, int b, f32x4 e) {
-    OT eo[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) eo[q] = cvt<OT>(e[q]);
-    *reinterpret_cast<V4*>(lds + lay.eb + m24(b, lay.lde) + r0) = V4{eo[0], eo[1], eo[2], eo[3]};
+    const V4 eo = cvt4(e);
+    *reinterpret_cast<V4*>(lds + lay.eb + m24(b, lay.lde) + r0) = eo;
 #pragma unroll
     for (int q = 0; q < 4; ++q) lds[lay.ea + m24(r0 + q, lay.lda) + b] = eo[q];
   }
@@ -391,11 +396,9 @@ struct Resident {
   // B operand [b][m] (contiguous) and the weight-update A operand [m][b].
   __device__ __forceinline__ void stage_e4(int r0, int b, f32x4 e) {
     if (b >= B) return;
-    OT eo[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) eo[q] = cvt<OT>(e[q]);
+    const V4 eo = cvt4(e);
     if (r0 + 4 <= M) {
-      *reinterpret_cast<V4*>(lds + lay.eb + m24(b, lay.lde) + r0) = V4{eo[0], eo[1], eo[2], eo[3]};
+      *reinterpret_cast<V4*>(lds + lay.eb + m24(b, lay.lde) + r0) = eo;
 #pragma unroll
       for (int q = 0; q < 4; ++q) lds[lay.ea + m24(r0 + q, lay.lda) + b] = eo[q];
     } else {
@@ -413,18 +416,19 @@ struct Resident {
   // 8-byte store when all four rows exist.
   __device__ __forceinline__ void stage_w4(int m0, int k, f32x4 w) {
     if (k >= K) return;
-    OT hi[4];
+    const V4 hi = cvt4(w);
+    V4 lo;
+    if (S3) lo = cvt4_lo(w, hi);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      hi[q] = cvt<OT>(w[q]);
       if (m0 + q < M) {
         lds[lay.wh + m24(m0 + q, lay.ldw) + k] = hi[q];
-        if (S3) lds[lay.wl + m24(m0 + q, lay.ldw) + k] = cvt<OT>(w[q] - to_f32(hi[q]));
+        if (S3) lds[lay.wl + m24(m0 + q, lay.ldw) + k] = lo[q];
       }
     }
     if (hidden) {
       if (m0 + 4 <= M) {
-        *reinterpret_cast<V4*>(lds + lay.wt + m24(k, lay.ldwt) + m0) = V4{hi[0], hi[1], hi[2], hi[3]};
+        *reinterpret_cast<V4*>(lds + lay.wt + m24(k, lay.ldwt) + m0) = hi;
       } else {
 #pragma unroll
         for (int q = 0; q < 4; ++q)
@@ -436,14 +440,15 @@ struct Resident {
   // stage_w4 of a hidden workgroup for a lane whose four rows (m0 + 4 <= M)
   // and column (k < K) all exist: the same values and stores, without the tests.
   __device__ __forceinline__ void stage_w4_full(int m0, int k, f32x4 w) {
-    OT hi[4];
+    const V4 hi = cvt4(w);
+    V4 lo;
+    if (S3) lo = cvt4_lo(w, hi);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      hi[q] = cvt<OT>(w[q]);
       lds[lay.wh + m24(m0 + q, lay.ldw) + k] = hi[q];
-      if (S3) lds[lay.wl + m24(m0 + q, lay.ldw) + k] = cvt<OT>(w[q] - to_f32(hi[q]));
+      if (S3) lds[lay.wl + m24(m0 + q, lay.ldw) + k] = lo[q];
     }
-    *reinterpret_cast<V4*>(lds + lay.wt + m24(k, lay.ldwt) + m0) = V4{hi[0], hi[1], hi[2], hi[3]};
+    *reinterpret_cast<V4*>(lds + lay.wt + m24(k, lay.ldwt) + m0) = hi;
   }
 
   // W element (m, k) of the block into its operand copies.
