@@ -1007,6 +1007,9 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, Resident
     if (s + 1 == p.steps) write_states(k, p, ea, xa, xb, fb);  // overlaps the last weight update
     __syncthreads();
     // ---- 4. W[l] += alpha eps[l] f(x_new[l+1])^T
+    // (after the last step W only leaves from the registers: no operand
+    // copies, no barrier)
+    const bool more = s + 1 < p.steps;
 #pragma unroll
     for (int i = 0; i < MU; ++i) {
       const int t = wave + NWV * i;
@@ -1019,7 +1022,7 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, Resident
 #pragma clang fp contract(off)
             wr[i][q] = wr[i][q] + alpha * c[q];
           }
-          k.stage_w4_full(r0, col, wr[i]);
+          if (more) k.stage_w4_full(r0, col, wr[i]);
         } else {
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
@@ -1028,11 +1031,11 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, Resident
               wr[i][q] = wr[i][q] + alpha * c[q];
             }
           }
-          k.stage_w4(r0, col, wr[i]);
+          if (more) k.stage_w4(r0, col, wr[i]);
         }
       }
     }
-    __syncthreads();
+    if (more) __syncthreads();
   }
 
   // ---- results: W[l] (the states went out before the last weight update)
