@@ -155,11 +155,15 @@ __host__ __device__ inline void resident_lds_layout(int M, int K, int B, bool hi
   o.wh = at; at += M16 * o.ldw;
   o.wl = at; if (split3) at += M16 * o.ldw;
   o.wt = at; if (hidden) at += K16 * o.ldwt;
-  o.fh = at; at += B16 * o.ldf;
+  // 16-bit hidden workgroups read the weight update's operands from fh and eb
+  // with transposing LDS loads and keep no ft or ea; fh and eb then hold the
+  // update's BP contraction rows (those past B zero)
+  const bool trh = hidden && esize == 2;
+  o.fh = at; at += (trh ? BP : B16) * o.ldf;
   o.fl = at; if (split3) at += B16 * o.ldf;
-  o.ft = at; at += K16 * o.ldft;
-  o.eb = at; if (hidden) at += B16 * o.lde;
-  o.ea = at; at += M16 * o.lda;
+  o.ft = at; if (!trh) at += K16 * o.ldft;
+  o.eb = at; if (hidden) at += (trh ? BP : B16) * o.lde;
+  o.ea = at; if (!trh) at += M16 * o.lda;
   o.bytes = at * esize;
 }
 

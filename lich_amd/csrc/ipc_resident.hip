@@ -220,6 +220,10 @@ struct Resident {
   typedef typename Op<OT>::V4 V4;
   static constexpr bool S3 = SPLIT >= 3;
   static constexpr int KSTEP = Op<OT>::KSTEP, KL = Op<OT>::KL;
+  // 16-bit hidden workgroups: the weight update reads eps and f(x) from the
+  // inference and prediction operands (eb, fh) with transposing loads, so
+  // their staging writes no [m][b] / [k][b] copies (ea, ft)
+  static constexpr bool TRH = sizeof(OT) == 2;
 
   // a * b for the kernel's small non-negative index products (LDS element
   // offsets and tile counts, all well below 2^23): the full-rate 24-bit
@@ -355,15 +359,16 @@ struct Resident {
       if (r0 + 4 <= K) {
         *reinterpret_cast<V4*>(lds + lay.fh + m24(b, lay.ldf) + r0) = hi;
         if (S3) *reinterpret_cast<V4*>(lds + lay.fl + m24(b, lay.ldf) + r0) = lo;
+        if (!TRH)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) lds[lay.ft + m24(r0 + q, lay.ldft) + b] = hi[q];
+          for (int q = 0; q < 4; ++q) lds[lay.ft + m24(r0 + q, lay.ldft) + b] = hi[q];
       } else {
 #pragma unroll
         for (int q = 0; q < 4; ++q)
           if (r0 + q < K) {
             lds[lay.fh + m24(b, lay.ldf) + r0 + q] = hi[q];
             if (S3) lds[lay.fl + m24(b, lay.ldf) + r0 + q] = lo[q];
-            lds[lay.ft + m24(r0 + q, lay.ldft) + b] = hi[q];
+            if (!TRH) lds[lay.ft + m24(r0 + q, lay.ldft) + b] = hi[q];
           }
       }
     }
@@ -379,8 +384,9 @@ struct Resident {
     const V4 hi = cvt4(f);
     *reinterpret_cast<V4*>(lds + lay.fh + m24(b, lay.ldf) + r0) = hi;
     if (S3) *reinterpret_cast<V4*>(lds + lay.fl + m24(b, lay.ldf) + r0) = cvt4_lo(f, hi);
+    if (!TRH)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) lds[lay.ft + m24(r0 + q, lay.ldft) + b] = hi[q];
+      for (int q = 0; q < 4; ++q) lds[lay.ft + m24(r0 + q, lay.ldft) + b] = hi[q];
     return f;
   }
 
@@ -388,8 +394,9 @@ struct Resident {
   __device__ __forceinline__ void stage_e4_full(int r0, int b, f32x4 e) {
     const V4 eo = cvt4(e);
     *reinterpret_cast<V4*>(lds + lay.eb + m24(b, lay.lde) + r0) = eo;
+    if (!TRH)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) lds[lay.ea + m24(r0 + q, lay.lda) + b] = eo[q];
+      for (int q = 0; q < 4; ++q) lds[lay.ea + m24(r0 + q, lay.lda) + b] = eo[q];
   }
 
   // eps rows r0 .. r0 + 3 of column b (zero outside M x B) into the inference
@@ -399,14 +406,15 @@ struct Resident {
     const V4 eo = cvt4(e);
     if (r0 + 4 <= M) {
       *reinterpret_cast<V4*>(lds + lay.eb + m24(b, lay.lde) + r0) = eo;
+      if (!TRH)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) lds[lay.ea + m24(r0 + q, lay.lda) + b] = eo[q];
+        for (int q = 0; q < 4; ++q) lds[lay.ea + m24(r0 + q, lay.lda) + b] = eo[q];
     } else {
 #pragma unroll
       for (int q = 0; q < 4; ++q)
         if (r0 + q < M) {
           lds[lay.eb + m24(b, lay.lde) + r0 + q] = eo[q];
-          lds[lay.ea + m24(r0 + q, lay.lda) + b] = eo[q];
+          if (!TRH) lds[lay.ea + m24(r0 + q, lay.lda) + b] = eo[q];
         }
     }
   }
@@ -537,6 +545,54 @@ struct Resident {
     }
     for (; ks < ks_b; ++ks) c = Op<OT>::mma(ld8(a0 + ks * KSTEP), ld8(b0 + ks * KSTEP), c);
     return c;
+  }
+
+  // Eight consecutive contraction rows b0 .. b0 + 7 of column c of a [b][c]
+  // 16-bit block (row stride ld elements) as one MFMA fragment, through two
+  // transposing loads: each 16-lane group reads a 4 x 16 block, lane i the
+  // 8-byte piece of row i / 4 and columns 4 (i % 4) .. 4 (i % 4) + 3, and
+  // gets column i of it back.  `off`: the lane's piece in rows b0 .. b0 + 3
+  // (rows b0 + 4 .. b0 + 7 are 4 ld further).
+  __device__ __forceinline__ V8 ld8_tr(int off, int ld) const {
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+    const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds + off));
+    const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds + off + 4 * ld));
+    return __builtin_bit_cast(V8, __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
+  }
+
+  // update_tile of a hidden workgroup.  16-bit operands: eps from eb [b][m]
+  // and f(x) from fh [b][k] through transposing loads, the same fragment
+  // values and MFMA sequence as from ea and ft (lane (g, r) gets rows
+  // 8g .. 8g + 7 of column r in both forms).
+  __device__ __forceinline__ f32x4 update_tile_h(int t) const {
+    if constexpr (!TRH) {
+      return update_tile(t);
+    } else {
+      const int rt = urt(t), ct = uct(t);
+      const int brow = 8 * lg + (lr >> 2), col = 4 * (lr & 3);
+      const int a0 = lay.eb + m24(brow, lay.lde) + rt * 16 + col;
+      const int b0 = lay.fh + m24(brow, lay.ldf) + ct * 16 + col;
+      const int sa = KSTEP * lay.lde, sb = KSTEP * lay.ldf;  // one k-step further
+      f32x4 c = zero4();
+      int ks = 0;
+      if constexpr (!S3) {
+        // two k-steps' fragments read before their MFMAs (four need more
+        // registers than the loop has)
+        for (; ks + 2 <= ks_b; ks += 2) {
+          V8 a[2], b[2];
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            a[u] = ld8_tr(a0 + (ks + u) * sa, lay.lde);
+            b[u] = ld8_tr(b0 + (ks + u) * sb, lay.ldf);
+          }
+#pragma unroll
+          for (int u = 0; u < 2; ++u) c = Op<OT>::mma(a[u], b[u], c);
+        }
+      }
+      for (; ks < ks_b; ++ks) c = Op<OT>::mma(ld8_tr(a0 + ks * sa, lay.lde), ld8_tr(b0 + ks * sb, lay.ldf), c);
+      return c;
+    }
   }
 
   // The wave's tiles t = wave and wave + NWV of a [rows][cols] tiling with
@@ -1014,7 +1070,7 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, Resident
     for (int i = 0; i < MU; ++i) {
       const int t = wave + NWV * i;
       if (t < k.n_upd) {
-        const f32x4 c = k.update_tile(t);
+        const f32x4 c = k.update_tile_h(t);
         const int col = k.uct(t) * 16 + lr, r0 = k.urt(t) * 16 + 4 * lg;
         if (r0 + 4 <= k.M && col < k.K) {  // (the lane's four rows and its column all exist)
 #pragma unroll
