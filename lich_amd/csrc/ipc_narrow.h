@@ -134,6 +134,8 @@ struct ResidentArgs {
 // output extents to 16; every row is padded by KP / 4 elements (16 bytes).
 //   wh, wl  [M16][KkP+pad]  W hi / lo          (prediction A)
 //   wt      [K16][MkP+pad]  W^T hi             (inference A, hidden only)
+// (16-bit hidden workgroups: no wh; wt holds KkP rows and is read transposed
+// as the prediction A as well; wl is W^T lo in wt's layout; no ft or ea, below)
 //   fh, fl  [B16][KkP+pad]  f(x upper) hi / lo (prediction B)
 //   ft      [K16][BkP+pad]  f(x upper) hi      (weight-update B)
 //   eb      [B16][MkP+pad]  eps                (inference B, hidden only)
@@ -151,14 +153,16 @@ __host__ __device__ inline void resident_lds_layout(int M, int K, int B, bool hi
   const int M16 = res_round(M, 16), MP = res_round(M, KP), K16 = res_round(K, 16), KK = res_round(K, KP);
   const int B16 = res_round(B, 16), BP = res_round(B, KP);
   o.ldw = KK + pad; o.ldwt = MP + pad; o.ldf = KK + pad; o.ldft = BP + pad; o.lde = MP + pad; o.lda = BP + pad;
-  int at = 0;
-  o.wh = at; at += M16 * o.ldw;
-  o.wl = at; if (split3) at += M16 * o.ldw;
-  o.wt = at; if (hidden) at += K16 * o.ldwt;
-  // 16-bit hidden workgroups read the weight update's operands from fh and eb
-  // with transposing LDS loads and keep no ft or ea; fh and eb then hold the
-  // update's BP contraction rows (those past B zero)
+  // 16-bit hidden workgroups read the prediction's W operand from wt and the
+  // weight update's operands from fh and eb with transposing LDS loads, and
+  // keep no wh, ft or ea; wt (and wl, W^T lo in wt's layout) then hold the
+  // prediction's KK contraction rows, fh and eb the update's BP (rows past
+  // the matrix zero)
   const bool trh = hidden && esize == 2;
+  int at = 0;
+  o.wh = at; if (!trh) at += M16 * o.ldw;
+  o.wl = at; if (split3) at += trh ? KK * o.ldwt : M16 * o.ldw;
+  o.wt = at; if (hidden) at += (trh ? KK : K16) * o.ldwt;
   o.fh = at; at += (trh ? BP : B16) * o.ldf;
   o.fl = at; if (split3) at += B16 * o.ldf;
   o.ft = at; if (!trh) at += K16 * o.ldft;

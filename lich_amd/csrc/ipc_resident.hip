@@ -221,8 +221,10 @@ struct Resident {
   static constexpr bool S3 = SPLIT >= 3;
   static constexpr int KSTEP = Op<OT>::KSTEP, KL = Op<OT>::KL;
   // 16-bit hidden workgroups: the weight update reads eps and f(x) from the
-  // inference and prediction operands (eb, fh) with transposing loads, so
-  // their staging writes no [m][b] / [k][b] copies (ea, ft)
+  // inference and prediction operands (eb, fh), and the prediction reads W
+  // from the inference operand W^T (wt; split 3: its lo half in wl), all with
+  // transposing loads, so their staging writes no [m][b], [k][b] or [m][k]
+  // copies (ea, ft, wh)
   static constexpr bool TRH = sizeof(OT) == 2;
 
   // a * b for the kernel's small non-negative index products (LDS element
@@ -427,20 +429,26 @@ struct Resident {
     const V4 hi = cvt4(w);
     V4 lo;
     if (S3) lo = cvt4_lo(w, hi);
+    const bool tr = TRH && hidden;  // (W^T copies only; lo in wt's layout)
+    if (!tr)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      if (m0 + q < M) {
-        lds[lay.wh + m24(m0 + q, lay.ldw) + k] = hi[q];
-        if (S3) lds[lay.wl + m24(m0 + q, lay.ldw) + k] = lo[q];
+      for (int q = 0; q < 4; ++q) {
+        if (m0 + q < M) {
+          lds[lay.wh + m24(m0 + q, lay.ldw) + k] = hi[q];
+          if (S3) lds[lay.wl + m24(m0 + q, lay.ldw) + k] = lo[q];
+        }
       }
-    }
     if (hidden) {
       if (m0 + 4 <= M) {
         *reinterpret_cast<V4*>(lds + lay.wt + m24(k, lay.ldwt) + m0) = hi;
+        if (S3 && tr) *reinterpret_cast<V4*>(lds + lay.wl + m24(k, lay.ldwt) + m0) = lo;
       } else {
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-          if (m0 + q < M) lds[lay.wt + m24(k, lay.ldwt) + m0 + q] = hi[q];
+          if (m0 + q < M) {
+            lds[lay.wt + m24(k, lay.ldwt) + m0 + q] = hi[q];
+            if (S3 && tr) lds[lay.wl + m24(k, lay.ldwt) + m0 + q] = lo[q];
+          }
       }
     }
   }
@@ -451,12 +459,14 @@ struct Resident {
     const V4 hi = cvt4(w);
     V4 lo;
     if (S3) lo = cvt4_lo(w, hi);
+    if (!TRH)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      lds[lay.wh + m24(m0 + q, lay.ldw) + k] = hi[q];
-      if (S3) lds[lay.wl + m24(m0 + q, lay.ldw) + k] = lo[q];
-    }
+      for (int q = 0; q < 4; ++q) {
+        lds[lay.wh + m24(m0 + q, lay.ldw) + k] = hi[q];
+        if (S3) lds[lay.wl + m24(m0 + q, lay.ldw) + k] = lo[q];
+      }
     *reinterpret_cast<V4*>(lds + lay.wt + m24(k, lay.ldwt) + m0) = hi;
+    if (S3 && TRH) *reinterpret_cast<V4*>(lds + lay.wl + m24(k, lay.ldwt) + m0) = lo;
   }
 
   // W element (m, k) of the block into its operand copies.
@@ -592,6 +602,85 @@ struct Resident {
       }
       for (; ks < ks_b; ++ks) c = Op<OT>::mma(ld8_tr(a0 + ks * sa, lay.lde), ld8_tr(b0 + ks * sb, lay.ldf), c);
       return c;
+    }
+  }
+
+  // pred_tile / pred_tiles of a hidden workgroup.  16-bit operands: the W
+  // fragments (row m, eight consecutive k) read transposed from W^T (wt, and
+  // wl for the lo half), the same values and MFMA sequence as from [m][k]
+  // copies.  wtr: the lane's piece of row tile rt in k-step 0.
+  __device__ __forceinline__ int wtr(int rt) const {
+    return m24(8 * lg + (lr >> 2), lay.ldwt) + rt * 16 + 4 * (lr & 3);
+  }
+  __device__ __forceinline__ f32x4 pred_tile_h(int t) const {
+    if constexpr (!TRH) {
+      return pred_tile(t);
+    } else {
+      const int rt = qdiv(t, inv_nbt), ct = t - m24(rt, nbt);
+      const int a0 = wtr(rt), sa = KSTEP * lay.ldwt;
+      const int b0 = m24(ct * 16 + lr, lay.ldf) + lg * KL;
+      f32x4 c = zero4();
+      for (int ks = 0; ks < ks_k; ++ks) {
+        const V8 ah = ld8_tr(lay.wt + a0 + ks * sa, lay.ldwt);
+        const V8 bh = ld8(lay.fh + b0 + ks * KSTEP);
+        c = Op<OT>::mma(ah, bh, c);
+        if (S3) {
+          const V8 al = ld8_tr(lay.wl + a0 + ks * sa, lay.ldwt);
+          const V8 bl = ld8(lay.fl + b0 + ks * KSTEP);
+          c = Op<OT>::mma(al, bh, c);
+          c = Op<OT>::mma(ah, bl, c);
+        }
+      }
+      return c;
+    }
+  }
+  __device__ __forceinline__ void pred_tiles_h(int n, f32x4 (&c)[MAXT]) const {
+    if constexpr (!TRH) {
+      pred_tiles(n, c);
+    } else {
+      const int t0 = wave, t1 = wave + NWV;
+      if (t1 < n && NWV % nbt == 0) {
+        const int rt0 = qdiv(t0, inv_nbt), ct = t0 - m24(rt0, nbt), rt1 = rt0 + NWV / nbt;
+        const int a0 = wtr(rt0), a1 = wtr(rt1), sa = KSTEP * lay.ldwt;
+        const int b0 = m24(ct * 16 + lr, lay.ldf) + lg * KL;
+        f32x4 c0 = zero4(), c1 = zero4();
+        int ks = 0;
+        if constexpr (!S3) {
+          for (; ks + 2 <= ks_k; ks += 2) {
+            V8 bh[2], ah0[2], ah1[2];
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+              bh[u] = ld8(lay.fh + b0 + (ks + u) * KSTEP);
+              ah0[u] = ld8_tr(lay.wt + a0 + (ks + u) * sa, lay.ldwt);
+              ah1[u] = ld8_tr(lay.wt + a1 + (ks + u) * sa, lay.ldwt);
+            }
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+              c0 = Op<OT>::mma(ah0[u], bh[u], c0);
+              c1 = Op<OT>::mma(ah1[u], bh[u], c1);
+            }
+          }
+        }
+        for (; ks < ks_k; ++ks) {
+          const V8 bh = ld8(lay.fh + b0 + ks * KSTEP);
+          const V8 ah0 = ld8_tr(lay.wt + a0 + ks * sa, lay.ldwt), ah1 = ld8_tr(lay.wt + a1 + ks * sa, lay.ldwt);
+          c0 = Op<OT>::mma(ah0, bh, c0);
+          c1 = Op<OT>::mma(ah1, bh, c1);
+          if (S3) {
+            const V8 bl = ld8(lay.fl + b0 + ks * KSTEP);
+            const V8 al0 = ld8_tr(lay.wl + a0 + ks * sa, lay.ldwt), al1 = ld8_tr(lay.wl + a1 + ks * sa, lay.ldwt);
+            c0 = Op<OT>::mma(al0, bh, c0);
+            c1 = Op<OT>::mma(al1, bh, c1);
+            c0 = Op<OT>::mma(ah0, bl, c0);
+            c1 = Op<OT>::mma(ah1, bl, c1);
+          }
+        }
+        c[0] = c0;
+        c[1] = c1;
+      } else {
+        c[0] = t0 < n ? pred_tile_h(t0) : zero4();
+        c[1] = t1 < n ? pred_tile_h(t1) : zero4();
+      }
     }
   }
 
@@ -985,7 +1074,7 @@ __device__ __forceinline__ void run_hidden(Resident<OT, SPLIT, ACT>& k, Resident
     // ---- 1. eps[l] = x[l] - W f(x[l+1]); g = W^T eps[l]
     float* xe = l >= 1 ? p.xe[l] + (long long)buf * npr * RES_TILE : nullptr;
     f32x4 cp[MAXT];
-    k.pred_tiles(npr, cp);
+    k.pred_tiles_h(npr, cp);
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) {
       const int t = wave + NWV * i;
