@@ -1255,9 +1255,13 @@ __device__ __forceinline__ void run_top(Resident<OT, SPLIT, ACT>& k, ResidentArg
   const gu32x4* isrc = (const gu32x4*)image;
   u32x4 img[CB];
   {
-    const BufRead bi(image, n16 * 16);  // pieces past the image read as zeros (and are not stored)
+    // (a wave whose pieces all lie past the image issues no load for them; in
+    // a wave that straddles its end, those lanes read zeros and store nothing)
+    const BufRead bi(image, n16 * 16);
+    const int wbase = __builtin_amdgcn_readfirstlane((int)threadIdx.x & ~63);
 #pragma unroll
-    for (int u = 0; u < CB; ++u) img[u] = bi.u128((threadIdx.x + u * NT) * 16u);
+    for (int u = 0; u < CB; ++u)
+      if (wbase + u * NT < n16) img[u] = bi.u128((threadIdx.x + u * NT) * 16u);
   }
   // A warm launch's first step sums the partial products the previous launch
   // left in xn.  Those of the wave's first prediction tile are loaded here,
